@@ -1,0 +1,346 @@
+"""Pins the CPU oracle before anything is judged against it.
+
+Every check here is either a known-answer vector from the reference's own tests
+(tests/golden/reference_kats.json, each citing its source), or a property fixed by
+the mathematics (exhaustive enumeration, brute-force nearest search, fp64 error
+bounds, exact invariants). None of them retypes the oracle's own formula.
+"""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+KATS = json.loads((GOLDEN / "reference_kats.json").read_text())
+LEVELS = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+
+
+def f32_bits(a):
+    return np.asarray(a, dtype=np.float32).view(np.uint32)
+
+
+# ---------------------------------------------------------------- decode (a1-a4)
+
+def test_decode_smallest_scale_and_signed_zero(oracle):
+    kat = KATS["decode_smallest_scale"]  # engine/src/mxfp4.rs:56-65
+    packed = np.full(16, 0x82, dtype=np.uint8)
+    scales = np.array(kat["scales"], dtype=np.uint8)
+    values = oracle.mx_values(packed, scales, 0, 32)
+    assert f32_bits(values[0]) == int(kat["expect_bits"]["0"], 16)
+    assert f32_bits(values[1]) == int(kat["expect_bits"]["1"], 16)
+
+
+def test_powi_is_exact_power_of_two(oracle):
+    # powi(2, e) must equal 2^e exactly, including the subnormal end and overflow.
+    for e in range(-127, 128):
+        assert oracle.powi2(e) == math.ldexp(1.0, e), e
+    assert math.isinf(oracle.powi2(128))
+
+
+def test_decode_exhaustive_codes_and_scales(oracle):
+    # All 16 codes x 255 valid scale bytes, bitwise, against numpy's ldexp
+    # (a different route from the oracle's LEVELS * powi product).
+    codes = np.arange(16, dtype=np.uint8)
+    packed_row = (codes[0::2] | (codes[1::2] << 4)).astype(np.uint8)  # 8 bytes = 16 codes
+    packed = np.tile(packed_row, 4 * 255)  # 32 codes per block, one block per scale
+    scales = np.arange(255, dtype=np.uint8)
+    got = oracle.mx_values(packed, scales, 0, 255 * 32)
+    level = np.array(LEVELS, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        want_all = [[np.ldexp(level[c & 7], np.int32(s - 127)).astype(np.float32) for c in range(16)]
+                    for s in range(255)]
+    for s in range(255):
+        for i in range(32):
+            c = i % 16
+            mag = want_all[s][c]
+            want = -mag if c & 8 else mag
+            assert f32_bits(got[s * 32 + i]) == f32_bits(want), (s, c)
+    # Closed-form edges named in the numeric contract
+    assert f32_bits(got[0 * 32 + 2]) == 0x00400000            # s=0, level 1 -> 2^-127
+    assert f32_bits(got[0 * 32 + 1]) == 0x00200000            # s=0, 0.5 -> 2^-128
+    assert np.isinf(got[253 * 32 + 6]) and np.isinf(got[253 * 32 + 7])   # 4, 6 at 2^126
+    assert np.isfinite(got[253 * 32 + 5])                    # 3 * 2^126 fits
+    assert np.isinf(got[254 * 32 + 4]) and np.isfinite(got[254 * 32 + 3])
+
+
+def test_value_and_values_agree_on_ragged_ranges(oracle):
+    rng = np.random.default_rng(7)
+    packed = rng.integers(0, 256, 5 * 96 // 2, dtype=np.uint8)
+    scales = rng.integers(90, 160, 5 * 96 // 32, dtype=np.uint8)
+    for start, end in [(0, 480), (3, 37), (31, 33), (64, 65), (100, 479)]:
+        block = oracle.mx_values(packed, scales, start, end)
+        single = np.array([oracle.mx_value(packed, scales, i) for i in range(start, end)],
+                          dtype=np.float32)
+        assert np.array_equal(f32_bits(block), f32_bits(single))
+
+
+def test_dequantize_matches_values(oracle):
+    rng = np.random.default_rng(3)
+    packed = rng.integers(0, 256, (7, 64), dtype=np.uint8)
+    scales = rng.integers(0, 255, (7, 4), dtype=np.uint8)
+    a = oracle.dequantize(packed, scales).reshape(-1)
+    b = oracle.mx_values(packed.reshape(-1), scales.reshape(-1), 0, 7 * 128)
+    assert np.array_equal(f32_bits(a), f32_bits(b))
+
+
+# ---------------------------------------------------------------- validate (a2)
+
+def test_validate_rejects_reference_cases(oracle):
+    for case in KATS["rejects"]["cases"]:  # engine/tests/mxfp4.rs:35-40
+        packed = np.zeros(case["packed_len"], dtype=np.uint8)
+        scales = np.array(case["scales"], dtype=np.uint8)
+        assert oracle.mx_validate(case["shape"], packed, scales) != 0
+    assert oracle.mx_validate((1, 32), np.zeros(16, np.uint8), np.array([127], np.uint8)) == 0
+    assert oracle.mx_validate((0, 32), np.zeros(0, np.uint8), np.zeros(0, np.uint8)) == 1
+    assert oracle.mx_validate((1, 32), np.zeros(16, np.uint8), np.array([255], np.uint8)) == 4
+
+
+# ---------------------------------------------------------------- matmul (a6)
+
+def test_matmul_identity_decodes_every_code(oracle):
+    kat = KATS["identity_all_codes"]  # engine/tests/mxfp4.rs:9-33
+    packed = np.tile(np.array(kat["packed_row"], dtype=np.uint8), kat["packed_repeat"])
+    scales = np.array(kat["scales"], dtype=np.uint8)
+    y = oracle.matmul(np.eye(32, dtype=np.float32), packed, scales)
+    assert list(y.shape) == kat["expect_shape"]
+    want = np.array(kat["expect"], dtype=np.float32)
+    assert np.array_equal(y.reshape(-1), want)
+
+
+def test_matmul_rows_and_blocks_use_different_scales(oracle):
+    kat = KATS["rows_and_blocks_use_different_scales"]  # engine/tests/mxfp4.rs:88-105
+    packed = np.full(64, kat["packed_fill"], dtype=np.uint8)
+    scales = np.array(kat["scales"], dtype=np.uint8)
+    x = np.zeros(kat["input_shape"], dtype=np.float32).reshape(-1)
+    x[kat["input_ones"]] = 1.0
+    y = oracle.matmul(x.reshape(kat["input_shape"]), packed, scales)
+    assert list(y.shape) == kat["expect_shape"]
+    assert y.reshape(-1).tolist() == kat["expect"]
+
+
+def test_matmul_within_fp32_error_bound_of_fp64(oracle):
+    # |y32 - y64| <= K * 2^-24 * sum|x w| (sequential summation bound, Higham 3.1)
+    rng = np.random.default_rng(11)
+    for m, n, k in [(1, 9, 64), (3, 5, 256), (2, 4, 2048)]:
+        packed = rng.integers(0, 256, n * k // 2, dtype=np.uint8)
+        scales = rng.integers(118, 132, n * k // 32, dtype=np.uint8)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        y = oracle.matmul(x, packed, scales)
+        y64 = oracle.matmul_f64(x, packed, scales)
+        w = oracle.dequantize(packed.reshape(n, k // 2), scales.reshape(n, k // 32))
+        absdot = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+        assert np.all(np.abs(y - y64) <= k * 2.0 ** -24 * absdot + 1e-30)
+
+
+def test_matmul_rows_are_independent_and_sliceable(oracle):
+    rng = np.random.default_rng(5)
+    n, k = 13, 96
+    packed = rng.integers(0, 256, n * k // 2, dtype=np.uint8)
+    scales = rng.integers(120, 130, n * k // 32, dtype=np.uint8)
+    x = rng.standard_normal((4, k)).astype(np.float32)
+    y = oracle.matmul(x, packed, scales)
+    for t in range(4):  # token rows do not interact
+        assert np.array_equal(f32_bits(oracle.matmul(x[t:t + 1], packed, scales)[0]), f32_bits(y[t]))
+    part = oracle.matmul_rows(x, packed, scales, 3, 11)
+    assert np.array_equal(f32_bits(part), f32_bits(y[:, 3:11]))
+    part4 = oracle.matmul_rows(x, packed, scales, 0, n, threads=4)
+    assert np.array_equal(f32_bits(part4), f32_bits(y))
+
+
+def test_matmul_bf16_arm_matches_decoded_weights(oracle):
+    # A bf16 weight equal to the decoded MXFP4 value gives the identical result.
+    rng = np.random.default_rng(9)
+    n, k = 6, 64
+    packed = rng.integers(0, 256, n * k // 2, dtype=np.uint8)
+    scales = rng.integers(122, 129, n * k // 32, dtype=np.uint8)
+    w = oracle.dequantize(packed.reshape(n, k // 2), scales.reshape(n, k // 32))
+    bits = (f32_bits(w) >> 16).astype(np.uint16)  # exact: levels have <= 2 significant bits
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    assert np.array_equal(oracle.matmul_bf16(x, bits), oracle.matmul(x, packed, scales))
+
+
+# ---------------------------------------------------------------- quantize (a17)
+
+def test_quantize_all_codes_round_trip(oracle):
+    kat = KATS["quantize_all_codes_round_trip"]  # python/tests/test_mxfp4.py:18-25
+    lv = np.array(LEVELS, dtype=np.float32)
+    values = np.tile(np.concatenate([lv, -lv]), 2)[None, :]
+    packed, scales = oracle.quantize(values)
+    assert packed[0, :8].tolist() == kat["expect_packed_first8"]
+    assert scales.tolist() == kat["expect_scales"]
+    back = oracle.dequantize(packed, scales)
+    assert np.array_equal(back, values)
+    assert np.array_equal(np.signbit(back), np.signbit(values))
+
+
+def test_quantize_ties_to_even_and_saturation(oracle):
+    kat = KATS["quantize_ties_to_even_and_saturate"]  # python/tests/test_mxfp4.py:28-35
+    values = np.zeros((1, kat["width"]), dtype=np.float32)
+    values[0, :8] = kat["values_first8"]
+    packed, scales = oracle.quantize(values)
+    assert scales.tolist() == kat["expect_scales"]
+    assert oracle.dequantize(packed, scales)[0, :8].tolist() == kat["expect_dequant_first8"]
+
+
+def test_quantize_each_block_gets_its_own_scale(oracle):
+    kat = KATS["quantize_per_block_scales"]  # python/tests/test_mxfp4.py:38-44
+    values = np.zeros(kat["shape"], dtype=np.float32)
+    values[0, :32] = kat["row0_first32"]
+    values[0, 32:] = kat["row0_last32"]
+    packed, scales = oracle.quantize(values)
+    assert scales.tolist() == kat["expect_scales"]
+    assert np.array_equal(oracle.dequantize(packed, scales), values)
+
+
+@pytest.mark.parametrize("invalid", [np.nan, np.inf, -np.inf])
+def test_quantize_rejects_non_finite(oracle, invalid):
+    values = np.zeros((1, 32), dtype=np.float32)
+    values[0, 1] = invalid  # python/tests/test_mxfp4.py:47-52
+    with pytest.raises(ValueError, match="non-finite"):
+        oracle.quantize(values)
+
+
+def test_quantize_rejects_bad_width(oracle):
+    with pytest.raises(ValueError, match="divisible"):  # python/tests/test_mxfp4.py:55-57
+        oracle.quantize(np.zeros((1, 31), dtype=np.float32))
+
+
+def test_quantize_converter_constants(oracle):
+    kat = KATS["converter_constants"]  # python/tests/test_mxfp4.py:60-83
+    packed, scales = oracle.quantize(np.full(kat["matrix_shape"], kat["matrix_fill"], np.float32))
+    assert np.all(packed == kat["expect_packed"]) and np.all(scales == kat["expect_scales"])
+    ones = np.ones(4, dtype=np.float32)
+    assert np.all((f32_bits(ones) >> 16) == kat["norm_ones_bf16_bits"])
+
+
+def _brute_force_block(block):
+    """Scale from log2 (not frexp) and nearest level by distance with ties to the
+    even code: an independent route to python/quantize_mxfp4.py:18-39."""
+    amax = max(abs(float(v)) for v in block)
+    if amax == 0.0:
+        e = -127
+    else:
+        e = math.floor(math.log2(amax))
+        # log2 of an f32 near a power of two can round up in fp64; repair exactly
+        if math.ldexp(1.0, e) > amax:
+            e -= 1
+        if math.ldexp(1.0, e + 1) <= amax:
+            e += 1
+        e = min(max(e - 2, -127), 127)
+    codes = []
+    for v in block:
+        q = abs(float(v)) * 2.0 ** (-e)   # exact in fp64 for f32 inputs
+        best = None
+        for c, lv in enumerate(LEVELS):
+            d = abs(q - lv)
+            if best is None or d < best[0] or (d == best[0] and c % 2 == 0):
+                best = (d, c)
+        code = best[1] | (8 if math.copysign(1.0, float(v)) < 0 else 0)
+        codes.append(code)
+    return e + 127, codes
+
+
+def test_quantize_matches_brute_force_nearest(oracle):
+    rng = np.random.default_rng(12)
+    rows = [
+        rng.standard_normal(64) * 0.02,
+        rng.standard_normal(64) * 1e-39,          # subnormal block maxima -> clipped e
+        np.concatenate([rng.standard_normal(32) * 1e30, rng.standard_normal(32)]),
+        rng.integers(-12, 13, 64) * 0.25,          # many exact midpoints and levels
+        np.where(rng.random(64) < 0.5, -0.0, 0.0),
+        np.full(64, 3.0e38),
+    ]
+    values = np.array(rows, dtype=np.float32)
+    packed, scales = oracle.quantize(values)
+    for r in range(values.shape[0]):
+        for b in range(2):
+            s, codes = _brute_force_block(values[r, b * 32:(b + 1) * 32])
+            assert scales[r, b] == s, (r, b)
+            got = []
+            for i in range(32):
+                byte = packed[r, b * 16 + i // 2]
+                got.append(int(byte >> 4) if i % 2 else int(byte & 15))
+            assert got == codes, (r, b)
+
+
+def test_quantize_is_idempotent(oracle):
+    rng = np.random.default_rng(4)
+    values = (rng.standard_normal((16, 256)) * rng.choice([1e-3, 0.02, 1, 300], (16, 1))).astype(np.float32)
+    p1, s1 = oracle.quantize(values)
+    p2, s2 = oracle.quantize(oracle.dequantize(p1, s1))
+    assert np.array_equal(p1, p2) and np.array_equal(s1, s2)
+
+
+# ---------------------------------------------------------------- fp8 requant
+
+def test_fp8_code_table(oracle):
+    assert oracle.fp8_value(0x7E) == 448.0
+    assert math.isnan(oracle.fp8_value(0x7F))
+    assert oracle.fp8_value(0x01) == 2.0 ** -9
+    assert oracle.fp8_value(0x08) == 2.0 ** -6
+    assert oracle.fp8_value(0x38) == 1.0
+    assert oracle.fp8_value(0x80) == 0.0 and math.copysign(1, oracle.fp8_value(0x80)) < 0
+
+
+def test_fp8_quantize_matches_brute_force_nearest(oracle):
+    table = [(c, oracle.fp8_value(c)) for c in range(0x7F)]  # finite magnitudes
+    rng = np.random.default_rng(21)
+    values = np.concatenate([rng.standard_normal(64 * 8), rng.integers(-40, 40, 64) / 16.0]).astype(np.float32)
+    values = values.reshape(-1, 64)
+    codes, scales = oracle.quantize_fp8(values)
+    for r in range(values.shape[0]):
+        for b in range(2):
+            blk = values[r, b * 32:(b + 1) * 32]
+            amax = float(np.max(np.abs(blk)))
+            e = -127 if amax == 0 else min(max(math.frexp(amax)[1] - 1 - 8, -127), 127)
+            assert scales[r, b] == e + 127
+            for i, v in enumerate(blk):
+                q = abs(float(v)) * 2.0 ** -e
+                best = min(table, key=lambda cv: (abs(q - cv[1]), cv[0] & 1))
+                want = best[0] | (0x80 if math.copysign(1, float(v)) < 0 else 0)
+                assert codes[r, b * 32 + i] == want, (r, b, i, v)
+
+
+# ---------------------------------------------------------------- argmax (a16)
+
+def test_argmax_first_maximum(oracle):
+    v = np.array([1, 5, 3, 5, 5], dtype=np.float32)
+    assert oracle.argmax(v) == 1
+    v = np.array([-np.inf, -np.inf], dtype=np.float32)
+    assert oracle.argmax(v) == 0
+    v = np.array([np.nan, 1.0, 2.0, 2.0], dtype=np.float32)   # NaN compares false
+    assert oracle.argmax(v) == 0
+    v = np.array([0.0, np.nan, 2.0, 2.0], dtype=np.float32)
+    assert oracle.argmax(v) == 2
+    rng = np.random.default_rng(1)
+    v = rng.standard_normal(151936).astype(np.float32)
+    assert oracle.argmax(v) == int(np.argmax(v))
+
+
+# ---------------------------------------------------------------- generator
+
+def test_generator_ln_and_cos_match_libm():
+    from oracle import mx4_oracle as o
+
+    rng = np.random.default_rng(0)
+    for u in np.concatenate([rng.random(2000), [2.0 ** -53, 1.0, 0.5, 0.7071067811865476]]):
+        if u <= 0:
+            continue
+        assert abs(o.ln(float(u)) - math.log(u)) <= 1e-15 * max(1.0, abs(math.log(u)))
+    for t in np.concatenate([rng.random(2000), [0.0, 0.25, 0.5, 0.75]]):
+        assert abs(o.cos2pi(float(t)) - math.cos(2 * math.pi * t)) <= 2e-15
+
+
+def test_generator_moments_and_determinism(oracle):
+    z = oracle.bf16_to_f32(oracle.synth_bf16(0, 1.0, 400_000)).astype(np.float64)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1.0) < 0.01
+    assert abs(np.mean(z ** 4) - 3.0) < 0.1        # Gaussian kurtosis
+    a = oracle.synth_bf16(5, 0.02, 100, start=1000)
+    b = oracle.synth_bf16(5, 0.02, 1100)[1000:]
+    assert np.array_equal(a, b)                     # counter-based: any slice
+    fx = json.loads((GOLDEN / "synth_fixtures.json").read_text())
+    for key, case in fx["prefixes"].items():
+        got = oracle.synth_bf16(case["seed"], case["sigma"], len(case["bf16"]))
+        assert got.tolist() == case["bf16"], key
