@@ -1,0 +1,217 @@
+#!/usr/bin/env python3
+"""Headline benchmark: MXFP4 GEMV HBM GB/s on one MI355X.
+
+Workload (one "step"): the M = 1 decode projections of one Qwen3-8B token --
+36 layers x {q 4096->4096, k 4096->1024, v 4096->1024, o 4096->4096,
+gate 4096->12288, up 4096->12288, down 12288->4096} plus lm_head 4096->151936,
+253 GEMVs over 4,029,425,152 algorithmic bytes. Every projection has its own
+resident weight (4.03 GB in HBM, far beyond the 256 MB Infinity Cache), made on
+the GPU by the weight recipe (bf16 N(0, 0.02), MXFP4 by the reference rule;
+tensor j uses seed 1000 + j). Activations are bf16 N(0, 1) from seed 1, already
+in HBM; outputs are f32. A step is replayed as one recorded pass (HIP graph)
+unless --eager is given.
+
+Algorithmic bytes of one GEMV: N*K/2 (nibbles) + N*K/32 (scales) + M*K*2 (bf16
+x) + M*N*4 (f32 y). value = bytes per step / wall time per step.
+
+cpu_baseline: the CPU oracle (a restatement of engine/src/lib.rs:240-266) on
+the box's host, one thread, over a bounded sample with the step's shape mix:
+all 7 projections of the first 3 layers plus the matching 3/36 of lm_head's rows.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "jalapenos-at-home_amd"))
+
+import mx4hip  # noqa: E402
+
+LAYER = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+         ("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
+LM_HEAD = ("lm_head", 151936, 4096)
+LAYERS = 36
+HBM_PEAK_GBS = 8000.0
+
+
+def gemv_bytes(m: int, n: int, k: int, x_bytes: int = 2) -> int:
+    return n * k // 2 + n * k // 32 + m * k * x_bytes + m * n * 4
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_step(ctx: mx4hip.Context):
+    """Distinct resident weights for every projection of the step."""
+    weights = []
+    seed = 1000
+    for layer in range(LAYERS):
+        for name, n, k in LAYER:
+            weights.append((name, n, k, ctx.synth_weight(seed, n, k, 0.02)))
+            seed += 1
+    name, n, k = LM_HEAD
+    weights.append((name, n, k, ctx.synth_weight(seed, n, k, 0.02)))
+    ctx.synchronize()
+    return weights
+
+
+def time_shapes(ctx, weights, xs, ys, reps: int = 3):
+    """Per-shape GPU time: the 36 distinct copies of a shape back to back (cold
+    weights), timed with events on the context stream."""
+    table = {}
+    for name, n, k in LAYER + [LM_HEAD]:
+        ws = [w for (nm, _, _, w) in weights if nm == name]
+        ops = ctx.make_ops([(xs[k].ptr, mx4hip.BF16, 1, w, ys[n].ptr) for w in ws])
+        ctx.matmul_batch(ops)
+        best = None
+        for _ in range(reps):
+            ctx.synchronize()
+            ctx.timer_begin()
+            ctx.matmul_batch(ops)
+            ms = ctx.timer_end() / len(ws)
+            best = ms if best is None else min(best, ms)
+        b = gemv_bytes(1, n, k)
+        table[name] = {"k": k, "n": n, "bytes": b, "us": round(best * 1e3, 3),
+                       "GBps": round(b / (best * 1e-3) / 1e9, 1),
+                       "frac": round(b / (best * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    return table
+
+
+def cpu_baseline(ctx, weights, x_host: dict, layers: int = 3) -> dict:
+    """The oracle on the host: one thread, `layers` layers + the matching share of lm_head."""
+    from oracle import mx4_oracle as oracle
+
+    if not oracle.LIB_PATH.exists():
+        oracle.build()
+    jobs = []
+    for name, n, k, w in weights[: layers * len(LAYER)]:
+        jobs.append((n, k, w, n))
+    name, n, k, w = weights[-1]
+    jobs.append((n, k, w, -(-n * layers // LAYERS)))
+    total_bytes, total_s = 0, 0.0
+    for n, k, w, rows in jobs:
+        packed, scales = ctx.download_weight(w)
+        x = x_host[k]
+        t0 = time.perf_counter()
+        oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), 0, rows, threads=1)
+        total_s += time.perf_counter() - t0
+        total_bytes += gemv_bytes(1, rows, k)
+    return {"value": round(total_bytes / total_s / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"first {layers} of 36 layers (all 7 projections) + {layers}/36 of lm_head rows, "
+                      f"{total_bytes} B in {total_s:.1f} s, single-threaded C restatement of "
+                      "engine/src/lib.rs:240-266"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--eager", action="store_true", help="enqueue each step with one batch call instead of a recorded pass")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-shapes", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (the GEMV would shard "
+              "column-wise with an all-gather of y; see the design notes). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    if mx4hip.device_count() < 1:
+        print("no gfx950 device visible", file=sys.stderr)
+        return 1
+
+    ctx = mx4hip.Context(0)
+    log("synthesizing 253 resident MXFP4 weights (4.03 GB) on the GPU")
+    weights = build_step(ctx)
+
+    ks = sorted({k for (_, _, k, _) in weights})
+    x_host = {}
+    xs = {}
+    for k in ks:
+        xs[k] = ctx.buffer(k * 2)
+        ctx.synth_bf16(1, 1.0, k, xs[k])
+        bits = xs[k].download(np.uint16)
+        x_host[k] = (bits.astype(np.uint32) << 16).view(np.float32).reshape(1, k)
+    ys = {n: ctx.buffer(n * 4) for n in sorted({n for (_, n, _, _) in weights})}
+
+    ops = ctx.make_ops([(xs[k].ptr, mx4hip.BF16, 1, w, ys[n].ptr) for (_, n, k, w) in weights])
+    step_bytes = sum(gemv_bytes(1, n, k) for (_, n, k, _) in weights)
+
+    if args.eager:
+        step = lambda: ctx.matmul_batch(ops)  # noqa: E731
+        launch = "eager batch (one C call per step)"
+    else:
+        pss = ctx.record(lambda: ctx.matmul_batch(ops))
+        step = pss.launch
+        launch = "recorded pass (HIP graph) per step"
+
+    for _ in range(args.warmup):
+        step()
+    ctx.synchronize()
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    ctx.timer_begin()
+    for _ in range(args.steps):
+        step()
+    gpu_ms = ctx.timer_end()
+    ctx.synchronize()
+    wall_s = time.perf_counter() - t0
+    ms_per_step = wall_s / args.steps * 1e3
+    gpu_ms_per_step = gpu_ms / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    achieved = step_bytes / (gpu_ms_per_step * 1e-3) / 1e9
+
+    extra = {"gpu_ms_per_step": round(gpu_ms_per_step, 4), "launch": launch}
+    if not args.no_shapes:
+        log("per-shape timing")
+        extra["shapes"] = time_shapes(ctx, weights, xs, ys)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle, 1 thread)")
+        cpu = cpu_baseline(ctx, weights, x_host)
+
+    traffic = None
+    tf = ROOT / "profiles" / "traffic_gemv_qwen3_8b_m1_step.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_step")
+
+    out = {
+        "metric": "MXFP4 GEMV HBM GB/s + % peak, Qwen3-8B M=1; M=512 prefill TFLOP/s",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4 x bf16 -> f32",
+        "data": "synthetic: weights bf16 N(0,0.02) quantized by the reference MXFP4 rule, x bf16 N(0,1)",
+        "config": {"workload": "qwen3-8b decode step, M=1: 36 layers x 7 projections + lm_head (253 GEMVs)",
+                   "bytes_per_step": step_bytes, "x_dtype": "bf16", "y_dtype": "f32",
+                   "distinct_weights_bytes": sum(w.nbytes for (_, _, _, w) in weights),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,220 @@
+/*
+ * mx4.h -- C ABI of the MI355X (gfx950) MXFP4 weight-quantized matmul.
+ *
+ * Plain pointers and sizes only. Two layers:
+ *
+ *  1. qwen_hip_*: the per-call drop-in for the reference engine's Metal bridge
+ *     (fawwaz46/jalapenos-at-home engine/src/metal.rs:6-19, implemented there
+ *     by engine/src/metal.m:18-117). Same signature, argument meaning, sync
+ *     contract and failure value (NULL / false).
+ *
+ *  2. mx4_*: the resident API in the style of the reference's GPU-resident
+ *     bridge (engine/src/gpu.rs:19-42, engine/src/gpu.m:27-128): weights stay
+ *     in HBM, kernels are enqueued on one HIP stream, device pointers are
+ *     caller-owned, and a pass can be timed with GPU events.
+ *
+ * Data layout (engine/src/mxfp4.rs:5-8): a weight of `rows` x `cols` (= N x K)
+ * is packed u8 [rows][cols/2], element 2j in the low nibble of byte j, and
+ * scales u8 [rows][cols/32], E8M0 with bias 127. Activations x are row-major
+ * [m][cols] f32 (what engine/src/metal.rs:11 passes) or bf16; outputs y are
+ * row-major f32 [m][rows].
+ *
+ * Threading: a context is not thread-safe (the reference's Metal context is
+ * neither Send nor Sync). Errors: every mx4_* call returns an mx4_status;
+ * mx4_last_error() gives the message of the last failure on the calling thread.
+ */
+#ifndef MX4_H
+#define MX4_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum mx4_status {
+    MX4_OK = 0,
+    MX4_ERR_ARGUMENT = 1,    /* null pointer, bad enum, size out of range */
+    MX4_ERR_SHAPE = 2,       /* engine/src/mxfp4.rs:12-14: nonempty rows, width % 32 == 0 */
+    MX4_ERR_TOO_LARGE = 3,   /* engine/src/mxfp4.rs:15-17 */
+    MX4_ERR_LENGTH = 4,      /* engine/src/mxfp4.rs:18-20 */
+    MX4_ERR_NAN_SCALE = 5,   /* engine/src/mxfp4.rs:21-23: scale byte 255 */
+    MX4_ERR_NON_FINITE = 6,  /* python/quantize_mxfp4.py:23-24 */
+    MX4_ERR_DEVICE = 7,      /* HIP runtime failure or no gfx950 device */
+    MX4_ERR_NO_MEMORY = 8,
+    MX4_ERR_UNSUPPORTED = 9
+} mx4_status;
+
+typedef enum mx4_dtype { MX4_F32 = 0, MX4_BF16 = 1 } mx4_dtype;
+
+/* Which kernel family runs a matmul. AUTO follows the M-based dispatch of
+ * engine/src/gpu.rs:469-515 re-tuned for gfx950. */
+typedef enum mx4_path {
+    MX4_PATH_AUTO = 0,
+    MX4_PATH_GEMV = 1,     /* M == 1 decode GEMV (no MFMA) */
+    MX4_PATH_SKINNY = 2,   /* exact skinny kernel, 2 <= M <= 16 */
+    MX4_PATH_GENERIC = 3,  /* exact fallback for any M and K % 32 == 0 */
+    MX4_PATH_PREFILL = 4   /* block-scaled MFMA on requantized activations */
+} mx4_path;
+
+/* Activation format on the block-scaled MFMA path (north-star prefill). */
+typedef enum mx4_act_format {
+    MX4_ACT_MXFP4 = 1,  /* requantized per 32 along K by the MXFP4 rule */
+    MX4_ACT_MXFP8 = 2   /* requantized per 32 along K to MX E4M3 */
+} mx4_act_format;
+
+typedef struct mx4_context mx4_context;
+typedef struct mx4_weight mx4_weight;
+
+/* ------------------------------------------------------------------------
+ * 1. Per-call drop-in (engine/src/metal.rs:6-19)
+ * ------------------------------------------------------------------------ */
+
+/* Replaces qwen_metal_create (engine/src/metal.rs:7, engine/src/metal.m:18-48).
+ * Kernels are precompiled for gfx950, so no source string is taken. Returns
+ * NULL (message on stderr and in mx4_last_error) when no gfx950 device exists. */
+void *qwen_hip_create(void);
+
+/* Replaces qwen_metal_destroy (engine/src/metal.rs:8, engine/src/metal.m:50-52). */
+void qwen_hip_destroy(void *context);
+
+/* Replaces qwen_metal_matmul (engine/src/metal.rs:9-18, engine/src/metal.m:54-117).
+ * y[rows][cols] = x[rows][inner] . W[cols][inner]^T. scales != NULL: w is packed
+ * MXFP4 [cols][inner/2] with scales [cols][inner/32]; scales == NULL: w is bf16
+ * [cols][inner]. Device copies of w and scales are cached by host pointer (the
+ * caller keeps them immutable, engine/src/metal.rs:33). Synchronous: y is valid
+ * on return. Returns false on any failure. */
+bool qwen_hip_matmul(void *context, const float *x, const void *w, const uint8_t *scales,
+                     float *y, uint32_t rows, uint32_t cols, uint32_t inner);
+
+/* Byte budget of the host-pointer weight cache (the Metal bridge's NSCache
+ * limit, engine/src/metal.m:43-44; default 64 GiB here for 288 GB of HBM).
+ * Least recently used entries are evicted beyond it. */
+void qwen_hip_set_cache_limit(void *context, uint64_t bytes);
+
+/* ------------------------------------------------------------------------
+ * 2. Resident API (engine/src/gpu.rs:19-42, engine/src/gpu.m:27-128)
+ * ------------------------------------------------------------------------ */
+
+/* gpu_create (engine/src/gpu.m:27-49): binds HIP device `device` and creates
+ * the context's stream (default priority). */
+mx4_status mx4_create(int device, mx4_context **out);
+void mx4_destroy(mx4_context *ctx);
+const char *mx4_last_error(void);
+/* Number of gfx950 devices visible (0 without a GPU; never fails). */
+int mx4_device_count(void);
+
+/* Enqueue on a caller stream (a hipStream_t) instead of the context's own;
+ * NULL restores the context stream. */
+mx4_status mx4_set_stream(mx4_context *ctx, void *hip_stream);
+void *mx4_get_stream(mx4_context *ctx);
+mx4_status mx4_synchronize(mx4_context *ctx);
+
+/* Host-only check of MXFP4 storage, engine/src/mxfp4.rs:11-25. Needs no GPU. */
+mx4_status mx4_validate(uint64_t rows, uint64_t cols, uint64_t packed_len,
+                        const uint8_t *scales, uint64_t scales_len);
+
+/* Device memory (gpu_buffer / gpu_buffer_contents / gpu_release,
+ * engine/src/gpu.m:69-84). Copies are synchronous with respect to the host. */
+mx4_status mx4_malloc(mx4_context *ctx, uint64_t bytes, void **dev);
+mx4_status mx4_free(mx4_context *ctx, void *dev);
+mx4_status mx4_upload(mx4_context *ctx, void *dev_dst, const void *host_src, uint64_t bytes);
+mx4_status mx4_download(mx4_context *ctx, void *host_dst, const void *dev_src, uint64_t bytes);
+/* Stream-ordered device-to-device copy. */
+mx4_status mx4_copy(mx4_context *ctx, void *dev_dst, const void *dev_src, uint64_t bytes);
+
+/* GpuTensor::new (engine/src/gpu.rs:225-237): validates (mx4_validate) and
+ * copies packed + scales into HBM once; the weight stays resident. */
+mx4_status mx4_weight_upload(mx4_context *ctx, const uint8_t *packed, const uint8_t *scales,
+                             uint32_t rows, uint32_t cols, mx4_weight **out);
+/* Wrap packed/scales already in HBM (not copied, not freed by release). The
+ * scale bytes are scanned on device; a 255 byte fails with MX4_ERR_NAN_SCALE. */
+mx4_status mx4_weight_wrap(mx4_context *ctx, const uint8_t *packed_dev, const uint8_t *scales_dev,
+                           uint32_t rows, uint32_t cols, mx4_weight **out);
+void mx4_weight_release(mx4_weight *w);
+mx4_status mx4_weight_info(const mx4_weight *w, uint32_t *rows, uint32_t *cols,
+                           const uint8_t **packed_dev, const uint8_t **scales_dev);
+
+/* GpuModel::matmul (engine/src/gpu.rs:469-515): y_dev[m][rows] =
+ * x_dev[m][cols] . W^T, enqueued on the context stream, exact arithmetic
+ * (f32 accumulation of exact products). AUTO picks GEMV for m == 1, the exact
+ * skinny kernel for 2 <= m <= 16 and the exact generic kernel beyond. */
+mx4_status mx4_matmul(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m,
+                      const mx4_weight *w, float *y_dev);
+/* The same with an explicit kernel family (MX4_PATH_PREFILL is not exact:
+ * use mx4_matmul_prefill). */
+mx4_status mx4_matmul_path(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m,
+                           const mx4_weight *w, float *y_dev, mx4_path path);
+/* Prefill on CDNA4 block-scaled MFMA (V_MFMA_SCALE_F32_*_F8F6F4): x is
+ * requantized per 32 along K (MXFP4 by python/quantize_mxfp4.py:18-39, or MX
+ * E4M3), then multiplied with the MXFP4 weight, f32 accumulation. The result
+ * equals the exact product of dequant(requant(x)) and W within f32 rounding. */
+mx4_status mx4_matmul_prefill(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m,
+                              const mx4_weight *w, mx4_act_format act, float *y_dev);
+
+/* One projection of a batch or recorded pass: y[m][w.rows] = x[m][w.cols] . W^T. */
+typedef struct mx4_op {
+    const void *x;
+    float *y;
+    const mx4_weight *w;
+    uint32_t m;
+    int32_t x_type; /* mx4_dtype */
+} mx4_op;
+
+/* Enqueue projections in order on the context stream with one call: the
+ * per-projection gpu_dispatch of engine/src/gpu.rs:469-515 without a host
+ * round trip per launch. Every op is checked before the first launch. */
+mx4_status mx4_matmul_batch(mx4_context *ctx, const mx4_op *ops, uint32_t count);
+
+/* A recorded pass: everything enqueued on the context stream between
+ * mx4_pass_begin and mx4_pass_end is captured into a HIP graph and replayed by
+ * mx4_pass_launch -- the analogue of the reference's one command buffer per
+ * forward pass (engine/src/gpu.rs:157, engine/src/gpu.m:87-128). No device
+ * memory is allocated or freed while recording. */
+typedef struct mx4_pass mx4_pass;
+mx4_status mx4_pass_begin(mx4_context *ctx);
+mx4_status mx4_pass_end(mx4_context *ctx, mx4_pass **out);
+mx4_status mx4_pass_launch(mx4_context *ctx, const mx4_pass *pass);
+void mx4_pass_release(mx4_pass *pass);
+
+/* engine/src/mxfp4.rs:35-49 on device: out_dev[rows*cols] f32, bit-exact. */
+mx4_status mx4_dequantize(mx4_context *ctx, const mx4_weight *w, float *out_dev);
+/* python/quantize_mxfp4.py:18-39 on device, bit-exact: in_dev [rows][cols]
+ * -> packed_dev [rows][cols/2], scales_dev [rows][cols/32]. Synchronous (it
+ * reports non-finite input as MX4_ERR_NON_FINITE). */
+mx4_status mx4_quantize(mx4_context *ctx, const void *in_dev, mx4_dtype in_type, uint64_t rows,
+                        uint32_t cols, uint8_t *packed_dev, uint8_t *scales_dev);
+/* MX E4M3 requantization: codes_dev [rows][cols], scales_dev [rows][cols/32]. Synchronous. */
+mx4_status mx4_quantize_fp8(mx4_context *ctx, const void *in_dev, mx4_dtype in_type, uint64_t rows,
+                            uint32_t cols, uint8_t *codes_dev, uint8_t *scales_dev);
+/* engine/src/model.rs:288-296 per row (argmax_rows, engine/src/gpu.metal:176-212). */
+mx4_status mx4_argmax_rows(mx4_context *ctx, const float *x_dev, uint32_t rows, uint32_t width,
+                           uint32_t *out_dev);
+
+/* Synthetic inputs (the reference defines none): element i of stream `seed`
+ * is bf16(RNE(f32(RNE(sigma * z_i)))) with z_i a Box-Muller normal from
+ * SplitMix64 outputs 2i and 2i+1. */
+mx4_status mx4_synth_bf16(mx4_context *ctx, uint64_t seed, double sigma, uint64_t start,
+                          uint64_t count, uint16_t *out_dev);
+/* The weight recipe: rows x cols bf16 N(0, sigma) from `seed`, quantized. */
+mx4_status mx4_synth_weight(mx4_context *ctx, uint64_t seed, double sigma, uint32_t rows,
+                            uint32_t cols, uint8_t *packed_dev, uint8_t *scales_dev);
+
+/* gpu_begin / gpu_finish (engine/src/gpu.m:87-128): GPU events around the
+ * work enqueued between the two calls; end waits and returns milliseconds. */
+mx4_status mx4_timer_begin(mx4_context *ctx);
+mx4_status mx4_timer_end(mx4_context *ctx, double *ms);
+
+/* Decode table of the hardware E2M1 converter as the kernels use it,
+ * out_dev[s*16 + c] for scale byte s and code c (mode 0: bit construction,
+ * 1: converter at scale 1 times 2^(s-127), 2: converter with the scale
+ * folded into bf16). Used by the exhaustive decode test. */
+mx4_status mx4_decode_table(mx4_context *ctx, int mode, float *out_dev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,119 @@
+// mx4_device.h -- device-side building blocks shared by the gfx950 kernels.
+//
+// MXFP4 storage (engine/src/mxfp4.rs:5-8, :27-33): weight row r of width K is
+// K/2 packed bytes (element 2j in the low nibble of byte j, 2j+1 in the high
+// nibble) plus K/32 E8M0 scale bytes. One 32-element block is 16 contiguous
+// bytes -- exactly one 128-bit load -- and one scale byte.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mx4 {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// E2M1 magnitude levels (engine/src/mxfp4.rs:3).
+__device__ __forceinline__ float level_of(uint32_t code) {
+    // Built from bits like gpu.metal's mxfp4_level, independent of a table:
+    // m = code & 7; m == 0 -> 0; m == 1 -> 0.5; else 2^(m/2 - 1) * (1 + (m & 1) / 2).
+    uint32_t m = code & 7u;
+    uint32_t bits = m == 0 ? 0u : (m == 1 ? 0x3f000000u : (((126u + (m >> 1)) << 23) | ((m & 1u) << 22)));
+    return __uint_as_float(bits | ((code & 8u) << 28));
+}
+
+// 2^(s - 127) for an E8M0 byte s in [0, 254], exact (2^-127 is the subnormal
+// 0x00400000; f32 denormals are preserved on gfx950 by default).
+__device__ __forceinline__ float e8m0_to_f32(uint32_t s) {
+    return __builtin_amdgcn_ldexpf(1.0f, (int)s - 127);
+}
+
+// One decoded element, bit-exact with engine/src/mxfp4.rs:27-33:
+// LEVELS[c & 7] * 2^(s-127), negated when c & 8.
+__device__ __forceinline__ float decode_exact(uint32_t code, uint32_t s) {
+    return level_of(code) * e8m0_to_f32(s);
+}
+
+// Two E2M1 codes from byte `sel` of `word` -> two f32 levels (scale 1), using
+// gfx950's hardware converter. Element order: low nibble -> .x, high -> .y.
+template <int SEL>
+__device__ __forceinline__ f32x2 cvt_fp4x2_f32(uint32_t word) {
+    return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, SEL);
+}
+template <int SEL>
+__device__ __forceinline__ bf16x2 cvt_fp4x2_bf16(uint32_t word) {
+    return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, 1.0f, SEL);
+}
+
+__device__ __forceinline__ uint32_t as_u32(bf16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ bf16x2 as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2, v); }
+
+// Sum of 32 products sum_i x[i] * level(code_i) for one MX block whose 16
+// packed bytes are w (4 dwords), x given as 16 bf16 pairs in element order.
+__device__ __forceinline__ float block_dot_bf16(const u32x4 w, const uint32_t* xp) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        acc = __builtin_amdgcn_fdot2_f32_bf16(cvt_fp4x2_bf16<0>(w[d]), as_bf16x2(xp[4 * d + 0]), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(cvt_fp4x2_bf16<1>(w[d]), as_bf16x2(xp[4 * d + 1]), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(cvt_fp4x2_bf16<2>(w[d]), as_bf16x2(xp[4 * d + 2]), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(cvt_fp4x2_bf16<3>(w[d]), as_bf16x2(xp[4 * d + 3]), acc, false);
+    }
+    return acc;
+}
+
+// The same with f32 activations: products x * level are exact in f32 before
+// each FMA's single rounding.
+__device__ __forceinline__ float block_dot_f32(const u32x4 w, const float* x) {
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        f32x2 v0 = cvt_fp4x2_f32<0>(w[d]);
+        f32x2 v1 = cvt_fp4x2_f32<1>(w[d]);
+        f32x2 v2 = cvt_fp4x2_f32<2>(w[d]);
+        f32x2 v3 = cvt_fp4x2_f32<3>(w[d]);
+        a0 = __builtin_fmaf(x[8 * d + 0], v0.x, a0);
+        a1 = __builtin_fmaf(x[8 * d + 1], v0.y, a1);
+        a0 = __builtin_fmaf(x[8 * d + 2], v1.x, a0);
+        a1 = __builtin_fmaf(x[8 * d + 3], v1.y, a1);
+        a0 = __builtin_fmaf(x[8 * d + 4], v2.x, a0);
+        a1 = __builtin_fmaf(x[8 * d + 5], v2.y, a1);
+        a0 = __builtin_fmaf(x[8 * d + 6], v3.x, a0);
+        a1 = __builtin_fmaf(x[8 * d + 7], v3.y, a1);
+    }
+    return a0 + a1;
+}
+
+// Wave64 sum; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ u32x4 load_u32x4(const uint8_t* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ u32x4 load_u32x4_nt(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// bf16 <-> f32 (engine/src/lib.rs:74-76 for the widening direction)
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float v) {
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+}  // namespace mx4

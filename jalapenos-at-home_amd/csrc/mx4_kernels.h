@@ -1,0 +1,66 @@
+// mx4_kernels.h -- host-side launchers of the gfx950 kernels (internal).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mx4 {
+
+// y[m, n] = x[m, k] . dequant(W[n, k])^T on one stream.
+struct GemvArgs {
+    const uint8_t* packed;  // [n][k/2]
+    const uint8_t* scales;  // [n][k/32]
+    const void* x;          // [m][k] f32 or bf16
+    float* y;               // [m][n]
+    uint32_t m, n, k;
+    bool x_bf16;
+    hipStream_t stream;
+};
+
+bool gemv_m1_supported(uint32_t k);
+hipError_t launch_gemv_m1(const GemvArgs& a, int cus);
+hipError_t launch_gemv_generic(const GemvArgs& a);
+
+// Exact skinny path (2 <= m <= 16) on bf16 MFMA with decoded weights.
+bool skinny_supported(uint32_t m, uint32_t k);
+hipError_t launch_skinny(const GemvArgs& a, int cus);
+
+// Block-scaled MFMA prefill on requantized activations.
+struct PrefillArgs {
+    const uint8_t* packed;    // W [n][k/2]
+    const uint8_t* scales;    // W [n][k/32]
+    const uint8_t* xq;        // activations requantized: fp4 [m][k/2] or fp8 [m][k]
+    const uint8_t* xs;        // activation scales [m][k/32]
+    float* y;                 // [m][n]
+    uint32_t m, n, k;
+    bool fp8;                 // activations are MX-FP8 (E4M3) instead of MXFP4
+    hipStream_t stream;
+};
+bool prefill_supported(uint32_t m, uint32_t n, uint32_t k);
+hipError_t launch_prefill(const PrefillArgs& a, int cus);
+
+// quantize_mxfp4.py:18-39 on device: rows x cols (cols % 32 == 0) f32/bf16 ->
+// packed [rows][cols/2] + scales [rows][cols/32]. Non-finite input sets *bad.
+hipError_t launch_quantize_mxfp4(const void* in, bool in_bf16, uint64_t rows, uint32_t cols,
+                                 uint8_t* packed, uint8_t* scales, uint32_t* bad, hipStream_t s);
+// MX-FP8 (E4M3): codes [rows][cols] + scales [rows][cols/32]
+hipError_t launch_quantize_fp8(const void* in, bool in_bf16, uint64_t rows, uint32_t cols,
+                               uint8_t* codes, uint8_t* scales, uint32_t* bad, hipStream_t s);
+// engine/src/mxfp4.rs:35-49 on device: packed/scales -> f32 [elements]
+hipError_t launch_dequantize(const uint8_t* packed, const uint8_t* scales, uint64_t elements,
+                             float* out, hipStream_t s);
+// engine/src/model.rs:288-296 per row
+hipError_t launch_argmax_rows(const float* x, uint32_t rows, uint32_t width, uint32_t* out,
+                              hipStream_t s);
+// Synthetic inputs (SplitMix64 -> Box-Muller -> sigma -> f32 -> bf16)
+hipError_t launch_synth_bf16(uint64_t seed, double sigma, uint64_t start, uint64_t count,
+                             uint16_t* out, hipStream_t s);
+hipError_t launch_synth_weight(uint64_t seed, double sigma, uint32_t rows, uint32_t cols,
+                               uint8_t* packed, uint8_t* scales, hipStream_t s);
+// Smallest scale byte of a resident weight (flags subnormal-scale blocks)
+hipError_t launch_min_max_scale(const uint8_t* scales, uint64_t count, uint32_t* out2,
+                                hipStream_t s);
+// Hardware-converter table for the exhaustive decode check: out[s*16 + c]
+hipError_t launch_decode_table(int mode, float* out, hipStream_t s);
+
+}  // namespace mx4

@@ -1,0 +1,451 @@
+// quant.hip -- MXFP4 format kernels: quantize (the weight recipe and the
+// activation requantizer of the MFMA path), MX-FP8 requantize, dequantize,
+// first-max argmax, scale range scan and the synthetic-input generator.
+#include "mx4_device.h"
+#include "mx4_kernels.h"
+
+namespace mx4 {
+
+// ------------------------------------------------------------------ quantize
+
+// python/quantize_mxfp4.py:18-39 for one 32-element block. The scale byte is
+// s = max(E - 2, 0) with E the biased exponent of amax (0 for zero or
+// subnormal amax): frexp(amax).exp - 3 = E - 129, clipped at -127.
+__device__ __forceinline__ uint32_t mxfp4_scale_byte(float amax) {
+    int e_biased = (int)((__float_as_uint(amax) >> 23) & 0xffu);
+    int s = e_biased - 2;
+    return s < 0 ? 0u : (uint32_t)s;
+}
+
+__device__ __forceinline__ uint32_t mxfp4_code(float v, uint32_t s) {
+    const float scaled = __builtin_amdgcn_ldexpf(__builtin_fabsf(v), 127 - (int)s);
+    // searchsorted(MIDPOINTS, scaled, side="left") = #midpoints < scaled
+    uint32_t code = (scaled > 0.25f) + (scaled > 0.75f) + (scaled > 1.25f) + (scaled > 1.75f) +
+                    (scaled > 2.5f) + (scaled > 3.5f) + (scaled > 5.0f);
+    // ties to even: scaled equal to the midpoint just above an odd code
+    const float mid_tab[7] = {0.25f, 0.75f, 1.25f, 1.75f, 2.5f, 3.5f, 5.0f};
+    float mid = mid_tab[code < 6 ? code : 6];
+    code += ((code & 1u) != 0u) & (scaled == mid);
+    code |= (__float_as_uint(v) >> 31) << 3;  // signbit, so -0.0 -> code 8
+    return code;
+}
+
+template <bool BF16>
+__device__ __forceinline__ void load_block32(const void* in, uint64_t blk, float (&v)[32]) {
+    if constexpr (BF16) {
+        const uint8_t* p = static_cast<const uint8_t*>(in) + blk * 64;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            u32x4 w = load_u32x4(p + 16 * q);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                v[8 * q + 2 * c] = bf16_bits_to_f32(w[c] & 0xffffu);
+                v[8 * q + 2 * c + 1] = bf16_bits_to_f32(w[c] >> 16);
+            }
+        }
+    } else {
+        const float* p = static_cast<const float*>(in) + blk * 32;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            f32x4 w = *reinterpret_cast<const f32x4*>(p + 4 * q);
+            v[4 * q + 0] = w[0];
+            v[4 * q + 1] = w[1];
+            v[4 * q + 2] = w[2];
+            v[4 * q + 3] = w[3];
+        }
+    }
+}
+
+// One thread per 32-element block (blocks are consecutive in memory, so
+// block b of the flat tensor is row b / (cols/32), column block b % (cols/32)).
+template <bool BF16>
+__global__ __launch_bounds__(256) void quantize_mxfp4_kernel(const void* __restrict__ in, uint64_t blocks,
+                                                             uint8_t* __restrict__ packed,
+                                                             uint8_t* __restrict__ scales,
+                                                             uint32_t* __restrict__ bad) {
+    const uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= blocks) return;
+    float v[32];
+    load_block32<BF16>(in, b, v);
+    float amax = 0.0f;
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        float a = __builtin_fabsf(v[i]);
+        finite &= a <= 3.40282347e38f;  // false for inf and NaN
+        amax = a > amax ? a : amax;
+    }
+    if (!finite) atomicOr(bad, 1u);
+    const uint32_t s = mxfp4_scale_byte(amax);
+    u32x4 out;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) word |= mxfp4_code(v[8 * d + i], s) << (4 * i);
+        out[d] = word;
+    }
+    *reinterpret_cast<u32x4*>(packed + b * 16) = out;
+    scales[b] = (uint8_t)s;
+}
+
+hipError_t launch_quantize_mxfp4(const void* in, bool in_bf16, uint64_t rows, uint32_t cols,
+                                 uint8_t* packed, uint8_t* scales, uint32_t* bad, hipStream_t s) {
+    const uint64_t blocks = rows * (cols / 32);
+    if (blocks == 0) return hipSuccess;
+    dim3 grid((unsigned)((blocks + 255) / 256));
+    if (in_bf16)
+        hipLaunchKernelGGL(quantize_mxfp4_kernel<true>, grid, dim3(256), 0, s, in, blocks, packed, scales, bad);
+    else
+        hipLaunchKernelGGL(quantize_mxfp4_kernel<false>, grid, dim3(256), 0, s, in, blocks, packed, scales, bad);
+    return hipGetLastError();
+}
+
+// MX-FP8 E4M3: e = floor(log2 amax) - 8 clipped to [-127, 127], RNE onto the
+// E4M3 grid, saturating at 448 (code 0x7e).
+__device__ __forceinline__ uint32_t fp8_scale_byte(float amax) {
+    int e_biased = (int)((__float_as_uint(amax) >> 23) & 0xffu);
+    // normal amax: floor(log2) = E - 127, e = E - 135, s = E - 8
+    int s = e_biased - 8;
+    return s < 0 ? 0u : (uint32_t)s;
+}
+
+__device__ __forceinline__ uint32_t e4m3_code(float v, uint32_t s) {
+    const float scaled = __builtin_amdgcn_ldexpf(__builtin_fabsf(v), 127 - (int)s);
+    uint32_t code;
+    if (scaled < 0.015625f) {  // 2^-6: subnormal step 2^-9
+        code = (uint32_t)__builtin_rintf(scaled * 512.0f);
+    } else {
+        int E = (int)((__float_as_uint(scaled) >> 23) & 0xffu) - 127;
+        float q = __builtin_rintf(__builtin_amdgcn_ldexpf(scaled, 3 - E));
+        if (q >= 16.0f) {
+            q = 8.0f;
+            E += 1;
+        }
+        int c = ((E + 7) << 3) | ((int)q - 8);
+        code = (E > 8 || c > 0x7e) ? 0x7eu : (uint32_t)c;
+    }
+    return code | ((__float_as_uint(v) >> 31) << 7);
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void quantize_fp8_kernel(const void* __restrict__ in, uint64_t blocks,
+                                                           uint8_t* __restrict__ codes,
+                                                           uint8_t* __restrict__ scales,
+                                                           uint32_t* __restrict__ bad) {
+    const uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= blocks) return;
+    float v[32];
+    load_block32<BF16>(in, b, v);
+    float amax = 0.0f;
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        float a = __builtin_fabsf(v[i]);
+        finite &= a <= 3.40282347e38f;
+        amax = a > amax ? a : amax;
+    }
+    if (!finite) atomicOr(bad, 1u);
+    const uint32_t s = fp8_scale_byte(amax);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        u32x4 out;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) word |= e4m3_code(v[16 * q + 4 * d + i], s) << (8 * i);
+            out[d] = word;
+        }
+        *reinterpret_cast<u32x4*>(codes + b * 32 + 16 * q) = out;
+    }
+    scales[b] = (uint8_t)s;
+}
+
+hipError_t launch_quantize_fp8(const void* in, bool in_bf16, uint64_t rows, uint32_t cols,
+                               uint8_t* codes, uint8_t* scales, uint32_t* bad, hipStream_t s) {
+    const uint64_t blocks = rows * (cols / 32);
+    if (blocks == 0) return hipSuccess;
+    dim3 grid((unsigned)((blocks + 255) / 256));
+    if (in_bf16)
+        hipLaunchKernelGGL(quantize_fp8_kernel<true>, grid, dim3(256), 0, s, in, blocks, codes, scales, bad);
+    else
+        hipLaunchKernelGGL(quantize_fp8_kernel<false>, grid, dim3(256), 0, s, in, blocks, codes, scales, bad);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ dequantize
+
+// engine/src/mxfp4.rs:35-49: one thread per packed byte -> two f32 values.
+__global__ __launch_bounds__(256) void dequantize_kernel(const uint8_t* __restrict__ packed,
+                                                         const uint8_t* __restrict__ scales,
+                                                         uint64_t bytes, float* __restrict__ out) {
+    const uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= bytes) return;
+    const uint32_t byte = packed[j];
+    const uint32_t s = scales[j / 16];
+    f32x2 v;
+    v.x = decode_exact(byte & 15u, s);
+    v.y = decode_exact(byte >> 4, s);
+    *reinterpret_cast<f32x2*>(out + 2 * j) = v;
+}
+
+hipError_t launch_dequantize(const uint8_t* packed, const uint8_t* scales, uint64_t elements,
+                             float* out, hipStream_t s) {
+    const uint64_t bytes = elements / 2;
+    if (bytes == 0) return hipSuccess;
+    hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)((bytes + 255) / 256)), dim3(256), 0, s, packed,
+                       scales, bytes, out);
+    return hipGetLastError();
+}
+
+// Decode tables for the exhaustive converter check: out[s * 16 + c].
+//  mode 0: decode_exact (bit construction x ldexp)
+//  mode 1: hardware fp4 -> f32 at scale 1, times 2^(s-127) (the GEMV factorisation)
+//  mode 2: hardware fp4 -> bf16 with the scale folded in, widened to f32
+__global__ void decode_table_kernel(int mode, float* out) {
+    const uint32_t s = blockIdx.x;      // 0..255
+    const uint32_t c = threadIdx.x;     // 0..15
+    const uint32_t word = c | (c << 4); // byte 0 holds the code in both nibbles
+    float v;
+    if (mode == 0) {
+        v = decode_exact(c, s);
+    } else if (mode == 1) {
+        v = cvt_fp4x2_f32<0>(word).x * e8m0_to_f32(s);
+    } else {
+        bf16x2 p = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, e8m0_to_f32(s), 0);
+        v = bf16_bits_to_f32(as_u32(p) & 0xffffu);
+    }
+    out[s * 16 + c] = v;
+}
+
+hipError_t launch_decode_table(int mode, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(decode_table_kernel, dim3(256), dim3(16), 0, s, mode, out);
+    return hipGetLastError();
+}
+
+// Smallest and largest scale byte (out2[0] = min, out2[1] = max); out2 must
+// start at {255, 0}.
+__global__ __launch_bounds__(256) void min_max_scale_kernel(const uint8_t* __restrict__ scales,
+                                                            uint64_t count, uint32_t* out2) {
+    uint32_t lo = 255, hi = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        uint32_t v = scales[i];
+        lo = v < lo ? v : lo;
+        hi = v > hi ? v : hi;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        uint32_t a = __shfl_xor(lo, off, 64), b = __shfl_xor(hi, off, 64);
+        lo = a < lo ? a : lo;
+        hi = b > hi ? b : hi;
+    }
+    if (threadIdx.x % 64 == 0) {
+        atomicMin(out2, lo);
+        atomicMax(out2 + 1, hi);
+    }
+}
+
+hipError_t launch_min_max_scale(const uint8_t* scales, uint64_t count, uint32_t* out2, hipStream_t s) {
+    uint64_t groups = (count + 255) / 256;
+    if (groups > 2048) groups = 2048;
+    if (groups == 0) groups = 1;
+    hipLaunchKernelGGL(min_max_scale_kernel, dim3((unsigned)groups), dim3(256), 0, s, scales, count, out2);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ argmax
+
+// engine/src/model.rs:288-296 per row: first index of the maximum with a
+// strict >, so NaN never wins, ties go to the lowest index and a NaN in
+// column 0 pins the answer to 0 (the sequential loop compares against it).
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* __restrict__ x, uint32_t width,
+                                                           uint32_t* __restrict__ out) {
+    const float* row = x + (size_t)blockIdx.x * width;
+    float best = -__builtin_inff();
+    uint32_t idx = 0xffffffffu;
+    for (uint32_t i = threadIdx.x; i < width; i += blockDim.x) {
+        float v = row[i];
+        if (v > best) {
+            best = v;
+            idx = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        float ob = __shfl_xor(best, off, 64);
+        uint32_t oi = __shfl_xor(idx, off, 64);
+        if (ob > best || (ob == best && oi < idx)) {
+            best = ob;
+            idx = oi;
+        }
+    }
+    __shared__ float sb[16];
+    __shared__ uint32_t si[16];
+    const uint32_t wave = threadIdx.x / 64;
+    if (threadIdx.x % 64 == 0) {
+        sb[wave] = best;
+        si[wave] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < blockDim.x / 64; ++w) {
+            if (sb[w] > best || (sb[w] == best && si[w] < idx)) {
+                best = sb[w];
+                idx = si[w];
+            }
+        }
+        float first = row[0];
+        if (first != first || idx == 0xffffffffu) idx = 0;
+        out[blockIdx.x] = idx;
+    }
+}
+
+hipError_t launch_argmax_rows(const float* x, uint32_t rows, uint32_t width, uint32_t* out, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(1024), 0, s, x, width, out);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ generator
+//
+// SplitMix64 output n of seed s; element i uses outputs 2i and 2i+1 as
+// u1 in (0, 1] and u2 in [0, 1); z = sqrt(-2 ln u1) cos(2 pi u2) with the
+// fixed polynomial ln and cos below (only +, -, *, /, sqrt, all correctly
+// rounded and never contracted), then f32 = RNE(z * sigma), bf16 = RNE(f32).
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t seed, uint64_t n) {
+    uint64_t z = seed + (n + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ double synth_ln(double u) {
+#pragma clang fp contract(off)
+    const double inv_odd[13] = {
+        0x1.0000000000000p+0, 0x1.5555555555555p-2, 0x1.999999999999ap-3,
+        0x1.2492492492492p-3, 0x1.c71c71c71c71cp-4, 0x1.745d1745d1746p-4,
+        0x1.3b13b13b13b14p-4, 0x1.1111111111111p-4, 0x1.e1e1e1e1e1e1ep-5,
+        0x1.af286bca1af28p-5, 0x1.8618618618618p-5, 0x1.642c8590b2164p-5,
+        0x1.47ae147ae147bp-5};
+    uint64_t bits = __double_as_longlong(u);
+    int e = (int)((bits >> 52) & 0x7ff) - 1023;
+    bits = (bits & 0x000fffffffffffffull) | 0x3ff0000000000000ull;
+    double m = __longlong_as_double(bits);
+    if (m > 0x1.6a09e667f3bcdp+0) {
+        m = m * 0.5;
+        e += 1;
+    }
+    double t = (m - 1.0) / (m + 1.0);
+    double t2 = t * t;
+    double p = inv_odd[12];
+#pragma unroll
+    for (int k = 11; k >= 0; --k) p = p * t2 + inv_odd[k];
+    return (double)e * 0x1.62e42fefa39efp-1 + 2.0 * t * p;
+}
+
+__device__ double synth_cos2pi(double turns) {
+#pragma clang fp contract(off)
+    const double inv_even_fact[17] = {
+        0x1.0000000000000p+0, 0x1.0000000000000p-1, 0x1.5555555555555p-5,
+        0x1.6c16c16c16c17p-10, 0x1.a01a01a01a01ap-16, 0x1.27e4fb7789f5cp-22,
+        0x1.1eed8eff8d898p-29, 0x1.93974a8c07c9dp-37, 0x1.ae7f3e733b81fp-45,
+        0x1.6827863b97d97p-53, 0x1.e542ba4020225p-62, 0x1.0ce396db7f853p-70,
+        0x1.f2cf01972f578p-80, 0x1.88e85fc6a4e5ap-89, 0x1.0a18a2635085dp-98,
+        0x1.3932c5047d60ep-108, 0x1.434d2e783f5bcp-118};
+    double r = turns >= 0.5 ? turns - 1.0 : turns;
+    double th = r * 0x1.921fb54442d18p+2;
+    double th2 = th * th;
+    double c = inv_even_fact[16];
+#pragma unroll
+    for (int k = 15; k >= 0; --k) {
+        double a = (k & 1) ? -inv_even_fact[k] : inv_even_fact[k];
+        c = a + th2 * c;
+    }
+    return c;
+}
+
+__device__ float synth_value(uint64_t seed, double sigma, uint64_t index) {
+#pragma clang fp contract(off)
+    uint64_t a = splitmix64(seed, 2 * index);
+    uint64_t b = splitmix64(seed, 2 * index + 1);
+    double u1 = (double)((a >> 11) + 1) * 0x1p-53;
+    double u2 = (double)(b >> 11) * 0x1p-53;
+    double z = __builtin_sqrt(-2.0 * synth_ln(u1)) * synth_cos2pi(u2);
+    double zs = z * sigma;
+    return (float)zs;
+}
+
+__global__ __launch_bounds__(256) void synth_bf16_kernel(uint64_t seed, double sigma, uint64_t start,
+                                                         uint64_t count, uint16_t* __restrict__ out) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    out[i] = (uint16_t)f32_to_bf16_bits(synth_value(seed, sigma, start + i));
+}
+
+hipError_t launch_synth_bf16(uint64_t seed, double sigma, uint64_t start, uint64_t count, uint16_t* out,
+                             hipStream_t s) {
+    if (count == 0) return hipSuccess;
+    hipLaunchKernelGGL(synth_bf16_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, seed,
+                       sigma, start, count, out);
+    return hipGetLastError();
+}
+
+// Generate one 32-element block of bf16 values and quantize it in place:
+// the weight recipe (bf16 N(0, sigma) from seed, MXFP4 by the reference rule)
+// without materialising the bf16 tensor.
+__global__ __launch_bounds__(256) void synth_weight_kernel(uint64_t seed, double sigma, uint64_t blocks,
+                                                           uint8_t* __restrict__ packed,
+                                                           uint8_t* __restrict__ scales) {
+    const uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= blocks) return;
+    float v[32];
+    float amax = 0.0f;
+    for (int i = 0; i < 32; ++i) {
+        float f = synth_value(seed, sigma, b * 32 + i);
+        v[i] = bf16_bits_to_f32(f32_to_bf16_bits(f));
+        float a = __builtin_fabsf(v[i]);
+        amax = a > amax ? a : amax;
+    }
+    const uint32_t s = mxfp4_scale_byte(amax);
+    u32x4 out;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) word |= mxfp4_code(v[8 * d + i], s) << (4 * i);
+        out[d] = word;
+    }
+    *reinterpret_cast<u32x4*>(packed + b * 16) = out;
+    scales[b] = (uint8_t)s;
+}
+
+hipError_t launch_synth_weight(uint64_t seed, double sigma, uint32_t rows, uint32_t cols, uint8_t* packed,
+                               uint8_t* scales, hipStream_t s) {
+    const uint64_t blocks = (uint64_t)rows * (cols / 32);
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(synth_weight_kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, s, seed,
+                       sigma, blocks, packed, scales);
+    return hipGetLastError();
+}
+
+}  // namespace mx4
+
+namespace mx4 {
+
+// A fill kernel instead of hipMemsetAsync, so callers may capture the
+// enqueued work in a HIP graph.
+__global__ void fill_u32_kernel(uint32_t* p, uint32_t count, uint32_t value) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) p[i] = value;
+}
+
+hipError_t launch_fill_u32(uint32_t* p, uint32_t count, uint32_t value, hipStream_t s) {
+    if (count == 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((count + 255) / 256), dim3(256), 0, s, p, count, value);
+    return hipGetLastError();
+}
+
+}  // namespace mx4

@@ -1,0 +1,701 @@
+// runtime.hip -- context, resident weights, dispatch and the C ABI (include/mx4.h).
+//
+// Native counterpart of the reference's Objective-C bridges:
+//  * qwen_hip_* <- engine/src/metal.m:18-117 (per-call matmul with a weight
+//    cache keyed by host pointer, synchronous round trip);
+//  * mx4_*      <- engine/src/gpu.m:27-128 + engine/src/gpu.rs:225-237, :469-515
+//    (resident weights, one stream, GPU-timed passes, M-based dispatch).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <list>
+#include <string>
+#include <unordered_map>
+
+#include "mx4.h"
+#include "mx4_kernels.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+mx4_status fail(mx4_status st, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return st;
+}
+
+#define HIP_TRY(call)                                                                        \
+    do {                                                                                     \
+        hipError_t e_ = (call);                                                              \
+        if (e_ != hipSuccess) return fail(MX4_ERR_DEVICE, "%s: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+struct CacheKey {
+    const void* w;
+    const void* scales;
+    uint32_t rows, cols;
+    bool operator==(const CacheKey& o) const {
+        return w == o.w && scales == o.scales && rows == o.rows && cols == o.cols;
+    }
+};
+struct CacheKeyHash {
+    size_t operator()(const CacheKey& k) const {
+        size_t h = std::hash<const void*>()(k.w);
+        h ^= std::hash<const void*>()(k.scales) + 0x9e3779b97f4a7c15ull + (h << 6) + (h >> 2);
+        h ^= ((size_t)k.rows << 32 | k.cols) + 0x9e3779b97f4a7c15ull + (h << 6) + (h >> 2);
+        return h;
+    }
+};
+
+constexpr uint64_t kDefaultCacheLimit = 64ull << 30;
+
+}  // namespace
+
+struct mx4_weight {
+    mx4_context* ctx;
+    uint32_t rows, cols;
+    uint8_t* packed;
+    uint8_t* scales;
+    void* allocation;  // owned device memory, or nullptr when wrapped
+    uint32_t min_scale, max_scale;
+};
+
+struct mx4_pass {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    int device;
+};
+
+struct CacheEntry {
+    mx4_weight* w;
+    uint64_t bytes;
+    std::list<CacheKey>::iterator lru;
+};
+
+struct mx4_context {
+    int device = 0;
+    int cus = 256;
+    hipStream_t own = nullptr;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    uint32_t* flags = nullptr;  // device scratch: [0] bad flag, [1..2] min/max scale
+    // per-call drop-in state
+    std::unordered_map<CacheKey, CacheEntry, CacheKeyHash> cache;
+    std::list<CacheKey> lru;
+    uint64_t cache_bytes = 0, cache_limit = kDefaultCacheLimit;
+    void* x_stage = nullptr;
+    uint64_t x_cap = 0;
+    void* y_stage = nullptr;
+    uint64_t y_cap = 0;
+    // prefill workspace: requantized activations + their scales
+    void* work = nullptr;
+    uint64_t work_cap = 0;
+};
+
+namespace mx4 {
+hipError_t launch_fill_u32(uint32_t* p, uint32_t count, uint32_t value, hipStream_t s);
+}
+
+namespace {
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+bool is_gfx950(int dev) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return false;
+    return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+}
+
+mx4_status ensure_buffer(mx4_context* ctx, void** buf, uint64_t* cap, uint64_t need) {
+    if (need <= *cap) return MX4_OK;
+    if (*buf) {
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+        HIP_TRY(hipFree(*buf));
+        *buf = nullptr;
+        *cap = 0;
+    }
+    uint64_t size = need < (1u << 20) ? (1u << 20) : need;
+    if (hipMalloc(buf, size) != hipSuccess) {
+        *buf = nullptr;
+        return fail(MX4_ERR_NO_MEMORY, "could not allocate %llu bytes of device memory",
+                    (unsigned long long)size);
+    }
+    *cap = size;
+    return MX4_OK;
+}
+
+mx4_status check_matmul_args(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
+                             const mx4_weight* w, const float* y) {
+    if (!ctx) return fail(MX4_ERR_ARGUMENT, "null context");
+    if (!x || !w || !y) return fail(MX4_ERR_ARGUMENT, "null x, weight or y");
+    if (xt != MX4_F32 && xt != MX4_BF16) return fail(MX4_ERR_ARGUMENT, "bad activation dtype %d", (int)xt);
+    if (m == 0) return fail(MX4_ERR_ARGUMENT, "m must be at least 1");
+    if (((uintptr_t)x & 15) != 0) return fail(MX4_ERR_ARGUMENT, "x must be 16-byte aligned");
+    if (((uintptr_t)y & 3) != 0) return fail(MX4_ERR_ARGUMENT, "y must be 4-byte aligned");
+    if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
+    return MX4_OK;
+}
+
+mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, const mx4_weight* w,
+                      float* y, mx4_path path) {
+    mx4::GemvArgs a{w->packed, w->scales, x, y, m, w->rows, w->cols, xt == MX4_BF16, ctx->stream};
+    if (path == MX4_PATH_AUTO) {
+        if (m == 1 && mx4::gemv_m1_supported(w->cols))
+            path = MX4_PATH_GEMV;
+        else if (m >= 2 && m <= 16 && mx4::skinny_supported(m, w->cols) && w->min_scale >= 2)
+            path = MX4_PATH_SKINNY;
+        else
+            path = MX4_PATH_GENERIC;
+    }
+    hipError_t e;
+    switch (path) {
+        case MX4_PATH_GEMV:
+            if (m != 1 || !mx4::gemv_m1_supported(w->cols))
+                return fail(MX4_ERR_UNSUPPORTED, "GEMV path needs m == 1 and K/32 in {64,128,192,256,384}");
+            e = mx4::launch_gemv_m1(a, ctx->cus);
+            break;
+        case MX4_PATH_SKINNY:
+            if (!mx4::skinny_supported(m, w->cols))
+                return fail(MX4_ERR_UNSUPPORTED, "skinny path needs 1 <= m <= 16 and K %% 128 == 0");
+            if (w->min_scale < 2)
+                return fail(MX4_ERR_UNSUPPORTED, "skinny path folds scales into bf16; scale bytes < 2 need GENERIC");
+            e = mx4::launch_skinny(a, ctx->cus);
+            break;
+        case MX4_PATH_GENERIC:
+            e = mx4::launch_gemv_generic(a);
+            break;
+        default:
+            return fail(MX4_ERR_ARGUMENT, "bad path %d", (int)path);
+    }
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status new_weight(mx4_context* ctx, uint32_t rows, uint32_t cols, mx4_weight** out) {
+    mx4_weight* w = new (std::nothrow) mx4_weight{};
+    if (!w) return fail(MX4_ERR_NO_MEMORY, "out of host memory");
+    w->ctx = ctx;
+    w->rows = rows;
+    w->cols = cols;
+    *out = w;
+    return MX4_OK;
+}
+
+void cache_evict(mx4_context* ctx) {
+    while (ctx->cache_bytes > ctx->cache_limit && !ctx->lru.empty()) {
+        CacheKey k = ctx->lru.back();
+        ctx->lru.pop_back();
+        auto it = ctx->cache.find(k);
+        if (it != ctx->cache.end()) {
+            ctx->cache_bytes -= it->second.bytes;
+            (void)hipStreamSynchronize(ctx->stream);
+            mx4_weight_release(it->second.w);
+            ctx->cache.erase(it);
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mx4_last_error(void) { return g_error.c_str(); }
+
+int mx4_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    int c = 0;
+    for (int i = 0; i < n; ++i) c += is_gfx950(i) ? 1 : 0;
+    return c;
+}
+
+mx4_status mx4_validate(uint64_t rows, uint64_t cols, uint64_t packed_len, const uint8_t* scales,
+                        uint64_t scales_len) {
+    // engine/src/mxfp4.rs:11-25
+    if (rows == 0 || cols == 0 || cols % 32 != 0)
+        return fail(MX4_ERR_SHAPE, "MXFP4 requires nonempty rows with a width divisible by 32");
+    if (rows > UINT64_MAX / cols) return fail(MX4_ERR_TOO_LARGE, "tensor is too large");
+    const uint64_t elements = rows * cols;
+    if (packed_len != elements / 2 || scales_len != elements / 32)
+        return fail(MX4_ERR_LENGTH, "MXFP4 data length does not match shape");
+    if (scales_len && !scales) return fail(MX4_ERR_ARGUMENT, "null scales");
+    if (std::memchr(scales, 255, scales_len)) return fail(MX4_ERR_NAN_SCALE, "MXFP4 checkpoint contains a NaN scale");
+    return MX4_OK;
+}
+
+mx4_status mx4_create(int device, mx4_context** out) {
+    if (!out) return fail(MX4_ERR_ARGUMENT, "null output pointer");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(MX4_ERR_DEVICE, "no HIP device available");
+    if (device < 0 || device >= n) return fail(MX4_ERR_ARGUMENT, "device %d out of range (%d devices)", device, n);
+    if (!is_gfx950(device)) return fail(MX4_ERR_DEVICE, "device %d is not gfx950 (MI355X)", device);
+    DeviceGuard g(device);
+    mx4_context* ctx = new (std::nothrow) mx4_context();
+    if (!ctx) return fail(MX4_ERR_NO_MEMORY, "out of host memory");
+    ctx->device = device;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) ctx->cus = prop.multiProcessorCount;
+    if (hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&ctx->ev0) != hipSuccess || hipEventCreate(&ctx->ev1) != hipSuccess ||
+        hipMalloc((void**)&ctx->flags, 256) != hipSuccess) {
+        mx4_destroy(ctx);
+        return fail(MX4_ERR_DEVICE, "could not create stream, events or scratch on device %d", device);
+    }
+    ctx->stream = ctx->own;
+    *out = ctx;
+    return MX4_OK;
+}
+
+void mx4_destroy(mx4_context* ctx) {
+    if (!ctx) return;
+    DeviceGuard g(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto& kv : ctx->cache) mx4_weight_release(kv.second.w);
+    ctx->cache.clear();
+    if (ctx->x_stage) (void)hipFree(ctx->x_stage);
+    if (ctx->y_stage) (void)hipFree(ctx->y_stage);
+    if (ctx->work) (void)hipFree(ctx->work);
+    if (ctx->flags) (void)hipFree(ctx->flags);
+    if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
+    if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
+    if (ctx->own) (void)hipStreamDestroy(ctx->own);
+    delete ctx;
+}
+
+mx4_status mx4_set_stream(mx4_context* ctx, void* hip_stream) {
+    if (!ctx) return fail(MX4_ERR_ARGUMENT, "null context");
+    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own;
+    return MX4_OK;
+}
+
+void* mx4_get_stream(mx4_context* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+mx4_status mx4_synchronize(mx4_context* ctx) {
+    if (!ctx) return fail(MX4_ERR_ARGUMENT, "null context");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return MX4_OK;
+}
+
+mx4_status mx4_malloc(mx4_context* ctx, uint64_t bytes, void** dev) {
+    if (!ctx || !dev) return fail(MX4_ERR_ARGUMENT, "null argument");
+    *dev = nullptr;
+    if (bytes == 0) return fail(MX4_ERR_ARGUMENT, "zero-byte allocation");
+    DeviceGuard g(ctx->device);
+    if (hipMalloc(dev, bytes) != hipSuccess) {
+        *dev = nullptr;
+        return fail(MX4_ERR_NO_MEMORY, "could not allocate %llu bytes", (unsigned long long)bytes);
+    }
+    return MX4_OK;
+}
+
+mx4_status mx4_free(mx4_context* ctx, void* dev) {
+    if (!ctx) return fail(MX4_ERR_ARGUMENT, "null context");
+    if (!dev) return MX4_OK;
+    DeviceGuard g(ctx->device);
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    HIP_TRY(hipFree(dev));
+    return MX4_OK;
+}
+
+mx4_status mx4_upload(mx4_context* ctx, void* dst, const void* src, uint64_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (!bytes) return MX4_OK;
+    DeviceGuard g(ctx->device);
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return MX4_OK;
+}
+
+mx4_status mx4_download(mx4_context* ctx, void* dst, const void* src, uint64_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (!bytes) return MX4_OK;
+    DeviceGuard g(ctx->device);
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return MX4_OK;
+}
+
+mx4_status mx4_copy(mx4_context* ctx, void* dst, const void* src, uint64_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (!bytes) return MX4_OK;
+    DeviceGuard g(ctx->device);
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return MX4_OK;
+}
+
+mx4_status mx4_weight_upload(mx4_context* ctx, const uint8_t* packed, const uint8_t* scales, uint32_t rows,
+                             uint32_t cols, mx4_weight** out) {
+    if (!ctx || !out || !packed || !scales) return fail(MX4_ERR_ARGUMENT, "null argument");
+    *out = nullptr;
+    const uint64_t elements = (uint64_t)rows * cols;
+    mx4_status st = mx4_validate(rows, cols, elements / 2, scales, elements / 32);
+    if (st != MX4_OK) return st;
+    uint32_t lo = 255, hi = 0;
+    for (uint64_t i = 0; i < elements / 32; ++i) {
+        lo = scales[i] < lo ? scales[i] : lo;
+        hi = scales[i] > hi ? scales[i] : hi;
+    }
+    DeviceGuard g(ctx->device);
+    const uint64_t pbytes = elements / 2, sbytes = elements / 32;
+    const uint64_t soff = (pbytes + 255) & ~255ull;
+    void* mem = nullptr;
+    if (hipMalloc(&mem, soff + sbytes) != hipSuccess)
+        return fail(MX4_ERR_NO_MEMORY, "could not allocate %llu bytes for a weight",
+                    (unsigned long long)(soff + sbytes));
+    uint8_t* base = static_cast<uint8_t*>(mem);
+    if (hipMemcpyAsync(base, packed, pbytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        hipMemcpyAsync(base + soff, scales, sbytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        (void)hipFree(mem);
+        return fail(MX4_ERR_DEVICE, "weight upload failed");
+    }
+    mx4_weight* w = nullptr;
+    st = new_weight(ctx, rows, cols, &w);
+    if (st != MX4_OK) {
+        (void)hipFree(mem);
+        return st;
+    }
+    w->allocation = mem;
+    w->packed = base;
+    w->scales = base + soff;
+    w->min_scale = lo;
+    w->max_scale = hi;
+    *out = w;
+    return MX4_OK;
+}
+
+mx4_status mx4_weight_wrap(mx4_context* ctx, const uint8_t* packed_dev, const uint8_t* scales_dev, uint32_t rows,
+                           uint32_t cols, mx4_weight** out) {
+    if (!ctx || !out || !packed_dev || !scales_dev) return fail(MX4_ERR_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (rows == 0 || cols == 0 || cols % 32 != 0)
+        return fail(MX4_ERR_SHAPE, "MXFP4 requires nonempty rows with a width divisible by 32");
+    if (((uintptr_t)packed_dev & 15) != 0) return fail(MX4_ERR_ARGUMENT, "packed data must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    const uint64_t sbytes = (uint64_t)rows * cols / 32;
+    HIP_TRY(mx4::launch_fill_u32(ctx->flags + 1, 2, 0, ctx->stream));
+    HIP_TRY(mx4::launch_fill_u32(ctx->flags + 1, 1, 255, ctx->stream));
+    HIP_TRY(mx4::launch_min_max_scale(scales_dev, sbytes, ctx->flags + 1, ctx->stream));
+    uint32_t mm[2];
+    HIP_TRY(hipMemcpyAsync(mm, ctx->flags + 1, 8, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (mm[1] == 255) return fail(MX4_ERR_NAN_SCALE, "MXFP4 checkpoint contains a NaN scale");
+    mx4_weight* w = nullptr;
+    mx4_status st = new_weight(ctx, rows, cols, &w);
+    if (st != MX4_OK) return st;
+    w->packed = const_cast<uint8_t*>(packed_dev);
+    w->scales = const_cast<uint8_t*>(scales_dev);
+    w->min_scale = mm[0];
+    w->max_scale = mm[1];
+    *out = w;
+    return MX4_OK;
+}
+
+void mx4_weight_release(mx4_weight* w) {
+    if (!w) return;
+    if (w->allocation) {
+        DeviceGuard g(w->ctx->device);
+        (void)hipStreamSynchronize(w->ctx->stream);
+        (void)hipFree(w->allocation);
+    }
+    delete w;
+}
+
+mx4_status mx4_weight_info(const mx4_weight* w, uint32_t* rows, uint32_t* cols, const uint8_t** packed_dev,
+                           const uint8_t** scales_dev) {
+    if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
+    if (rows) *rows = w->rows;
+    if (cols) *cols = w->cols;
+    if (packed_dev) *packed_dev = w->packed;
+    if (scales_dev) *scales_dev = w->scales;
+    return MX4_OK;
+}
+
+mx4_status mx4_matmul_path(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, const mx4_weight* w,
+                           float* y, mx4_path path) {
+    mx4_status st = check_matmul_args(ctx, x, xt, m, w, y);
+    if (st != MX4_OK) return st;
+    if (path == MX4_PATH_PREFILL) return fail(MX4_ERR_ARGUMENT, "use mx4_matmul_prefill for the MFMA path");
+    DeviceGuard g(ctx->device);
+    return run_matmul(ctx, x, xt, m, w, y, path);
+}
+
+mx4_status mx4_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, const mx4_weight* w, float* y) {
+    return mx4_matmul_path(ctx, x, xt, m, w, y, MX4_PATH_AUTO);
+}
+
+mx4_status mx4_matmul_prefill(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, const mx4_weight* w,
+                              mx4_act_format act, float* y) {
+    mx4_status st = check_matmul_args(ctx, x, xt, m, w, y);
+    if (st != MX4_OK) return st;
+    if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
+    if (!mx4::prefill_supported(m, w->rows, w->cols))
+        return fail(MX4_ERR_UNSUPPORTED, "prefill path needs K %% 128 == 0 and N %% 64 == 0");
+    DeviceGuard g(ctx->device);
+    const bool fp8 = act == MX4_ACT_MXFP8;
+    const uint64_t qbytes = (uint64_t)m * w->cols / (fp8 ? 1 : 2);
+    const uint64_t qoff = (qbytes + 255) & ~255ull;
+    const uint64_t sbytes = (uint64_t)m * w->cols / 32;
+    st = ensure_buffer(ctx, &ctx->work, &ctx->work_cap, qoff + sbytes);
+    if (st != MX4_OK) return st;
+    uint8_t* xq = static_cast<uint8_t*>(ctx->work);
+    uint8_t* xs = xq + qoff;
+    hipError_t e = fp8 ? mx4::launch_quantize_fp8(x, xt == MX4_BF16, m, w->cols, xq, xs, ctx->flags, ctx->stream)
+                       : mx4::launch_quantize_mxfp4(x, xt == MX4_BF16, m, w->cols, xq, xs, ctx->flags, ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "requantize launch failed: %s", hipGetErrorString(e));
+    mx4::PrefillArgs a{w->packed, w->scales, xq, xs, y, m, w->rows, w->cols, fp8, ctx->stream};
+    e = mx4::launch_prefill(a, ctx->cus);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status mx4_matmul_batch(mx4_context* ctx, const mx4_op* ops, uint32_t count) {
+    if (!ctx || (!ops && count)) return fail(MX4_ERR_ARGUMENT, "null argument");
+    for (uint32_t i = 0; i < count; ++i) {
+        mx4_status st = check_matmul_args(ctx, ops[i].x, (mx4_dtype)ops[i].x_type, ops[i].m, ops[i].w, ops[i].y);
+        if (st != MX4_OK) return fail(st, "op %u: %s", i, g_error.c_str());
+    }
+    DeviceGuard g(ctx->device);
+    for (uint32_t i = 0; i < count; ++i) {
+        mx4_status st = run_matmul(ctx, ops[i].x, (mx4_dtype)ops[i].x_type, ops[i].m, ops[i].w, ops[i].y,
+                                   MX4_PATH_AUTO);
+        if (st != MX4_OK) return fail(st, "op %u: %s", i, g_error.c_str());
+    }
+    return MX4_OK;
+}
+
+mx4_status mx4_pass_begin(mx4_context* ctx) {
+    if (!ctx) return fail(MX4_ERR_ARGUMENT, "null context");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    return MX4_OK;
+}
+
+mx4_status mx4_pass_end(mx4_context* ctx, mx4_pass** out) {
+    if (!ctx || !out) return fail(MX4_ERR_ARGUMENT, "null argument");
+    *out = nullptr;
+    DeviceGuard g(ctx->device);
+    hipGraph_t graph = nullptr;
+    HIP_TRY(hipStreamEndCapture(ctx->stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return fail(MX4_ERR_DEVICE, "graph instantiate failed: %s", hipGetErrorString(e));
+    }
+    mx4_pass* p = new (std::nothrow) mx4_pass{graph, exec, ctx->device};
+    if (!p) {
+        (void)hipGraphExecDestroy(exec);
+        (void)hipGraphDestroy(graph);
+        return fail(MX4_ERR_NO_MEMORY, "out of host memory");
+    }
+    *out = p;
+    return MX4_OK;
+}
+
+mx4_status mx4_pass_launch(mx4_context* ctx, const mx4_pass* pass) {
+    if (!ctx || !pass) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (pass->device != ctx->device) return fail(MX4_ERR_ARGUMENT, "pass recorded on another device");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(hipGraphLaunch(pass->exec, ctx->stream));
+    return MX4_OK;
+}
+
+void mx4_pass_release(mx4_pass* pass) {
+    if (!pass) return;
+    DeviceGuard g(pass->device);
+    (void)hipGraphExecDestroy(pass->exec);
+    (void)hipGraphDestroy(pass->graph);
+    delete pass;
+}
+
+mx4_status mx4_dequantize(mx4_context* ctx, const mx4_weight* w, float* out) {
+    if (!ctx || !w || !out) return fail(MX4_ERR_ARGUMENT, "null argument");
+    DeviceGuard g(ctx->device);
+    hipError_t e = mx4::launch_dequantize(w->packed, w->scales, (uint64_t)w->rows * w->cols, out, ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "dequantize launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+static mx4_status quantize_common(mx4_context* ctx, const void* in, mx4_dtype t, uint64_t rows, uint32_t cols,
+                                  uint8_t* q, uint8_t* s, bool fp8) {
+    if (!ctx || !in || !q || !s) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (t != MX4_F32 && t != MX4_BF16) return fail(MX4_ERR_ARGUMENT, "bad input dtype");
+    if (cols % 32 != 0) return fail(MX4_ERR_SHAPE, "expected a matrix whose row width is divisible by 32");
+    if (((uintptr_t)in & 15) || ((uintptr_t)q & 15)) return fail(MX4_ERR_ARGUMENT, "buffers must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(mx4::launch_fill_u32(ctx->flags, 1, 0, ctx->stream));
+    hipError_t e = fp8 ? mx4::launch_quantize_fp8(in, t == MX4_BF16, rows, cols, q, s, ctx->flags, ctx->stream)
+                       : mx4::launch_quantize_mxfp4(in, t == MX4_BF16, rows, cols, q, s, ctx->flags, ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "quantize launch failed: %s", hipGetErrorString(e));
+    uint32_t bad = 0;
+    HIP_TRY(hipMemcpyAsync(&bad, ctx->flags, 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (bad) return fail(MX4_ERR_NON_FINITE, "cannot quantize non-finite weights");
+    return MX4_OK;
+}
+
+mx4_status mx4_quantize(mx4_context* ctx, const void* in, mx4_dtype t, uint64_t rows, uint32_t cols,
+                        uint8_t* packed, uint8_t* scales) {
+    return quantize_common(ctx, in, t, rows, cols, packed, scales, false);
+}
+
+mx4_status mx4_quantize_fp8(mx4_context* ctx, const void* in, mx4_dtype t, uint64_t rows, uint32_t cols,
+                            uint8_t* codes, uint8_t* scales) {
+    return quantize_common(ctx, in, t, rows, cols, codes, scales, true);
+}
+
+mx4_status mx4_argmax_rows(mx4_context* ctx, const float* x, uint32_t rows, uint32_t width, uint32_t* out) {
+    if (!ctx || !x || !out) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (width == 0) return fail(MX4_ERR_ARGUMENT, "argmax of an empty row");
+    DeviceGuard g(ctx->device);
+    hipError_t e = mx4::launch_argmax_rows(x, rows, width, out, ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "argmax launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status mx4_synth_bf16(mx4_context* ctx, uint64_t seed, double sigma, uint64_t start, uint64_t count,
+                          uint16_t* out) {
+    if (!ctx || (!out && count)) return fail(MX4_ERR_ARGUMENT, "null argument");
+    DeviceGuard g(ctx->device);
+    hipError_t e = mx4::launch_synth_bf16(seed, sigma, start, count, out, ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "synth launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status mx4_synth_weight(mx4_context* ctx, uint64_t seed, double sigma, uint32_t rows, uint32_t cols,
+                            uint8_t* packed, uint8_t* scales) {
+    if (!ctx || !packed || !scales) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (cols % 32 != 0 || rows == 0) return fail(MX4_ERR_SHAPE, "width must be a nonzero multiple of 32");
+    if (((uintptr_t)packed & 15) != 0) return fail(MX4_ERR_ARGUMENT, "packed must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    hipError_t e = mx4::launch_synth_weight(seed, sigma, rows, cols, packed, scales, ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "synth launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status mx4_timer_begin(mx4_context* ctx) {
+    if (!ctx) return fail(MX4_ERR_ARGUMENT, "null context");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(hipEventRecord(ctx->ev0, ctx->stream));
+    return MX4_OK;
+}
+
+mx4_status mx4_timer_end(mx4_context* ctx, double* ms) {
+    if (!ctx || !ms) return fail(MX4_ERR_ARGUMENT, "null argument");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(hipEventRecord(ctx->ev1, ctx->stream));
+    HIP_TRY(hipEventSynchronize(ctx->ev1));
+    float f = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&f, ctx->ev0, ctx->ev1));
+    *ms = f;
+    return MX4_OK;
+}
+
+mx4_status mx4_decode_table(mx4_context* ctx, int mode, float* out) {
+    if (!ctx || !out) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (mode < 0 || mode > 2) return fail(MX4_ERR_ARGUMENT, "bad mode");
+    DeviceGuard g(ctx->device);
+    hipError_t e = mx4::launch_decode_table(mode, out, ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "decode table launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+// ------------------------------------------------------------ per-call drop-in
+
+void* qwen_hip_create(void) {
+    // engine/src/metal.m:18-48: a device, a queue and the pipelines, or NULL.
+    mx4_context* ctx = nullptr;
+    if (mx4_create(0, &ctx) != MX4_OK) {
+        std::fprintf(stderr, "qwen_hip_create: %s\n", g_error.c_str());
+        return nullptr;
+    }
+    return ctx;
+}
+
+void qwen_hip_destroy(void* context) { mx4_destroy(static_cast<mx4_context*>(context)); }
+
+void qwen_hip_set_cache_limit(void* context, uint64_t bytes) {
+    mx4_context* ctx = static_cast<mx4_context*>(context);
+    if (!ctx) return;
+    ctx->cache_limit = bytes;
+    cache_evict(ctx);
+}
+
+bool qwen_hip_matmul(void* context, const float* x, const void* w, const uint8_t* scales, float* y,
+                     uint32_t rows, uint32_t cols, uint32_t inner) {
+    // engine/src/metal.m:54-117
+    mx4_context* ctx = static_cast<mx4_context*>(context);
+    if (!ctx || !x || !w || !y) {
+        fail(MX4_ERR_ARGUMENT, "null argument");
+        return false;
+    }
+    if (rows == 0 || cols == 0 || inner == 0) {
+        fail(MX4_ERR_ARGUMENT, "empty matmul");
+        return false;
+    }
+    if (!scales) {
+        fail(MX4_ERR_UNSUPPORTED, "bf16 weights (scales == NULL) are not supported by this backend yet");
+        return false;
+    }
+    DeviceGuard g(ctx->device);
+    CacheKey key{w, scales, cols, inner};
+    auto it = ctx->cache.find(key);
+    mx4_weight* weight = nullptr;
+    if (it == ctx->cache.end()) {
+        if (mx4_weight_upload(ctx, static_cast<const uint8_t*>(w), scales, cols, inner, &weight) != MX4_OK)
+            return false;
+        uint64_t bytes = (uint64_t)cols * inner / 2 + (uint64_t)cols * inner / 32;
+        ctx->lru.push_front(key);
+        ctx->cache.emplace(key, CacheEntry{weight, bytes, ctx->lru.begin()});
+        ctx->cache_bytes += bytes;
+    } else {
+        weight = it->second.w;
+        ctx->lru.splice(ctx->lru.begin(), ctx->lru, it->second.lru);
+    }
+    const uint64_t xbytes = (uint64_t)rows * inner * 4, ybytes = (uint64_t)rows * cols * 4;
+    if (ensure_buffer(ctx, &ctx->x_stage, &ctx->x_cap, xbytes) != MX4_OK) return false;
+    if (ensure_buffer(ctx, &ctx->y_stage, &ctx->y_cap, ybytes) != MX4_OK) return false;
+    if (hipMemcpyAsync(ctx->x_stage, x, xbytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess) {
+        fail(MX4_ERR_DEVICE, "input upload failed");
+        return false;
+    }
+    if (run_matmul(ctx, ctx->x_stage, MX4_F32, rows, weight, static_cast<float*>(ctx->y_stage), MX4_PATH_AUTO) !=
+        MX4_OK)
+        return false;
+    if (hipMemcpyAsync(y, ctx->y_stage, ybytes, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        fail(MX4_ERR_DEVICE, "matmul or copy-back failed");
+        return false;
+    }
+    // evict only after the call completed, never the weight just used
+    if (ctx->cache_bytes > ctx->cache_limit) {
+        CacheKey keep = key;
+        ctx->lru.remove(keep);
+        cache_evict(ctx);
+        ctx->lru.push_front(keep);
+        auto kit = ctx->cache.find(keep);
+        if (kit != ctx->cache.end()) kit->second.lru = ctx->lru.begin();
+    }
+    return true;
+}
+
+}  // extern "C"

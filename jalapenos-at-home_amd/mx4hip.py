@@ -1,0 +1,388 @@
+"""ctypes binding of libmx4hip.so (include/mx4.h) for tests and the benchmark.
+
+The library is the product: every call here goes straight to the HIP kernels
+through the C ABI. There is no CPU fallback -- if the library is missing or no
+gfx950 device is present the calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+import weakref
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libmx4hip.so"
+HEADER = HERE.parent / "include" / "mx4.h"
+
+MX4_OK = 0
+STATUS = {
+    0: "MX4_OK", 1: "MX4_ERR_ARGUMENT", 2: "MX4_ERR_SHAPE", 3: "MX4_ERR_TOO_LARGE",
+    4: "MX4_ERR_LENGTH", 5: "MX4_ERR_NAN_SCALE", 6: "MX4_ERR_NON_FINITE",
+    7: "MX4_ERR_DEVICE", 8: "MX4_ERR_NO_MEMORY", 9: "MX4_ERR_UNSUPPORTED",
+}
+F32, BF16 = 0, 1
+PATH_AUTO, PATH_GEMV, PATH_SKINNY, PATH_GENERIC, PATH_PREFILL = 0, 1, 2, 3, 4
+ACT_MXFP4, ACT_MXFP8 = 1, 2
+
+_vp = ctypes.c_void_p
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
+_int = ctypes.c_int
+
+SIGNATURES = {
+    "qwen_hip_create": (_vp, []),
+    "qwen_hip_destroy": (None, [_vp]),
+    "qwen_hip_matmul": (ctypes.c_bool, [_vp, _f32p, _vp, _u8p, _f32p, _u32, _u32, _u32]),
+    "qwen_hip_set_cache_limit": (None, [_vp, _u64]),
+    "mx4_create": (_int, [_int, ctypes.POINTER(_vp)]),
+    "mx4_destroy": (None, [_vp]),
+    "mx4_last_error": (ctypes.c_char_p, []),
+    "mx4_device_count": (_int, []),
+    "mx4_set_stream": (_int, [_vp, _vp]),
+    "mx4_get_stream": (_vp, [_vp]),
+    "mx4_synchronize": (_int, [_vp]),
+    "mx4_validate": (_int, [_u64, _u64, _u64, _u8p, _u64]),
+    "mx4_malloc": (_int, [_vp, _u64, ctypes.POINTER(_vp)]),
+    "mx4_free": (_int, [_vp, _vp]),
+    "mx4_upload": (_int, [_vp, _vp, _vp, _u64]),
+    "mx4_download": (_int, [_vp, _vp, _vp, _u64]),
+    "mx4_copy": (_int, [_vp, _vp, _vp, _u64]),
+    "mx4_weight_upload": (_int, [_vp, _u8p, _u8p, _u32, _u32, ctypes.POINTER(_vp)]),
+    "mx4_weight_wrap": (_int, [_vp, _vp, _vp, _u32, _u32, ctypes.POINTER(_vp)]),
+    "mx4_weight_release": (None, [_vp]),
+    "mx4_weight_info": (_int, [_vp, ctypes.POINTER(_u32), ctypes.POINTER(_u32),
+                               ctypes.POINTER(_vp), ctypes.POINTER(_vp)]),
+    "mx4_matmul": (_int, [_vp, _vp, _int, _u32, _vp, _vp]),
+    "mx4_matmul_path": (_int, [_vp, _vp, _int, _u32, _vp, _vp, _int]),
+    "mx4_matmul_prefill": (_int, [_vp, _vp, _int, _u32, _vp, _int, _vp]),
+    "mx4_matmul_batch": (_int, [_vp, _vp, _u32]),
+    "mx4_pass_begin": (_int, [_vp]),
+    "mx4_pass_end": (_int, [_vp, ctypes.POINTER(_vp)]),
+    "mx4_pass_launch": (_int, [_vp, _vp]),
+    "mx4_pass_release": (None, [_vp]),
+    "mx4_dequantize": (_int, [_vp, _vp, _vp]),
+    "mx4_quantize": (_int, [_vp, _vp, _int, _u64, _u32, _vp, _vp]),
+    "mx4_quantize_fp8": (_int, [_vp, _vp, _int, _u64, _u32, _vp, _vp]),
+    "mx4_argmax_rows": (_int, [_vp, _vp, _u32, _u32, _vp]),
+    "mx4_synth_bf16": (_int, [_vp, _u64, ctypes.c_double, _u64, _u64, _vp]),
+    "mx4_synth_weight": (_int, [_vp, _u64, ctypes.c_double, _u32, _u32, _vp, _vp]),
+    "mx4_timer_begin": (_int, [_vp]),
+    "mx4_timer_end": (_int, [_vp, ctypes.POINTER(ctypes.c_double)]),
+    "mx4_decode_table": (_int, [_vp, _int, _vp]),
+}
+
+
+def header_symbols() -> list[str]:
+    """Every function the public header declares."""
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b((?:qwen_hip|mx4)_[a-z0-9_]+)\s*\(", text)))
+
+
+class Op(ctypes.Structure):
+    """mx4_op: one projection of a batch or recorded pass."""
+    _fields_ = [("x", _vp), ("y", _vp), ("w", _vp), ("m", _u32), ("x_type", ctypes.c_int32)]
+
+
+class Mx4Error(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS.get(status, status)}: {message}")
+        self.status = status
+
+
+_LIB: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"HIP library not built: {LIB_PATH} (run __graft_entry__.build())")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def last_error() -> str:
+    return lib().mx4_last_error().decode()
+
+
+def check(status: int) -> None:
+    if status != MX4_OK:
+        raise Mx4Error(status, last_error())
+
+
+def device_count() -> int:
+    return lib().mx4_device_count()
+
+
+def validate(shape, packed: np.ndarray, scales: np.ndarray) -> int:
+    """Host-only check (engine/src/mxfp4.rs:11-25); returns the status code."""
+    rows, cols = shape
+    scales = np.ascontiguousarray(scales, dtype=np.uint8).reshape(-1)
+    return lib().mx4_validate(rows, cols, packed.size, scales.ctypes.data_as(_u8p), scales.size)
+
+
+def _ptr(a: np.ndarray, ty=_vp):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ty)
+
+
+class DeviceBuffer:
+    """Device allocation owned by a Context (hipMalloc through the C ABI)."""
+
+    def __init__(self, ctx: "Context", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = _vp()
+        check(lib().mx4_malloc(ctx.handle, max(self.nbytes, 1), ctypes.byref(p)))
+        self.ptr = p.value
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        check(lib().mx4_upload(self.ctx.handle, self.ptr + offset, _ptr(a), a.nbytes))
+        return self
+
+    def download(self, dtype, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        count = (self.nbytes - offset) // dtype.itemsize if count is None else count
+        out = np.empty(count, dtype=dtype)
+        check(lib().mx4_download(self.ctx.handle, _ptr(out), self.ptr + offset, out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            check(lib().mx4_free(self.ctx.handle, self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and self.ctx.handle:
+                lib().mx4_free(self.ctx.handle, self.ptr)
+        except Exception:
+            pass
+
+
+class Weight:
+    """A resident MXFP4 weight (engine/src/gpu.rs:225-237)."""
+
+    def __init__(self, ctx: "Context", handle: int, rows: int, cols: int, keep=None):
+        self.ctx, self.handle, self.rows, self.cols = ctx, handle, rows, cols
+        self._keep = keep
+
+    @property
+    def nbytes(self) -> int:
+        return self.rows * self.cols // 2 + self.rows * self.cols // 32
+
+    def release(self) -> None:
+        # a weight never outlives its context (release after destroy is a use-after-free)
+        if self.handle and self.ctx.handle:
+            lib().mx4_weight_release(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+
+class Context:
+    def __init__(self, device: int = 0):
+        h = _vp()
+        check(lib().mx4_create(device, ctypes.byref(h)))
+        self.handle = h.value
+        self._weights: "weakref.WeakSet[Weight]" = weakref.WeakSet()
+
+    def close(self) -> None:
+        if self.handle:
+            for w in list(self._weights):
+                w.release()
+            lib().mx4_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # memory
+    def buffer(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, a: np.ndarray) -> DeviceBuffer:
+        a = np.ascontiguousarray(a)
+        return DeviceBuffer(self, a.nbytes).upload(a)
+
+    def synchronize(self) -> None:
+        check(lib().mx4_synchronize(self.handle))
+
+    # weights
+    def upload_weight(self, packed: np.ndarray, scales: np.ndarray, rows: int, cols: int) -> Weight:
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint8)
+        h = _vp()
+        check(lib().mx4_weight_upload(self.handle, _ptr(packed, _u8p), _ptr(scales, _u8p), rows, cols,
+                                      ctypes.byref(h)))
+        return self._track(Weight(self, h.value, rows, cols))
+
+    def _track(self, w: Weight) -> Weight:
+        self._weights.add(w)
+        return w
+
+    def wrap_weight(self, packed: DeviceBuffer, scales: DeviceBuffer, rows: int, cols: int,
+                    packed_offset: int = 0, scales_offset: int = 0) -> Weight:
+        h = _vp()
+        check(lib().mx4_weight_wrap(self.handle, packed.ptr + packed_offset, scales.ptr + scales_offset,
+                                    rows, cols, ctypes.byref(h)))
+        return self._track(Weight(self, h.value, rows, cols, keep=(packed, scales)))
+
+    def synth_weight(self, seed: int, rows: int, cols: int, sigma: float = 0.02) -> Weight:
+        """The weight recipe generated in HBM (no host copy)."""
+        pb = rows * cols // 2
+        soff = (pb + 255) // 256 * 256
+        buf = self.buffer(soff + rows * cols // 32)
+        check(lib().mx4_synth_weight(self.handle, seed, sigma, rows, cols, buf.ptr, buf.ptr + soff))
+        return self.wrap_weight(buf, buf, rows, cols, 0, soff)
+
+    def weight_device_arrays(self, w: Weight):
+        packed = _vp()
+        scales = _vp()
+        check(lib().mx4_weight_info(w.handle, None, None, ctypes.byref(packed), ctypes.byref(scales)))
+        return packed.value, scales.value
+
+    def download_weight(self, w: Weight):
+        p, s = self.weight_device_arrays(w)
+        packed = np.empty((w.rows, w.cols // 2), dtype=np.uint8)
+        scales = np.empty((w.rows, w.cols // 32), dtype=np.uint8)
+        check(lib().mx4_download(self.handle, _ptr(packed), p, packed.nbytes))
+        check(lib().mx4_download(self.handle, _ptr(scales), s, scales.nbytes))
+        return packed, scales
+
+    # compute (asynchronous on the context stream)
+    def matmul(self, x: DeviceBuffer, xtype: int, m: int, w: Weight, y: DeviceBuffer,
+               path: int = PATH_AUTO) -> None:
+        check(lib().mx4_matmul_path(self.handle, x.ptr, xtype, m, w.handle, y.ptr, path))
+
+    def matmul_ptr(self, xptr: int, xtype: int, m: int, w: Weight, yptr: int, path: int = PATH_AUTO) -> None:
+        check(lib().mx4_matmul_path(self.handle, xptr, xtype, m, w.handle, yptr, path))
+
+    def matmul_prefill(self, x: DeviceBuffer, xtype: int, m: int, w: Weight, act: int, y: DeviceBuffer) -> None:
+        check(lib().mx4_matmul_prefill(self.handle, x.ptr, xtype, m, w.handle, act, y.ptr))
+
+    def make_ops(self, ops) -> "ctypes.Array[Op]":
+        """ops: iterable of (x_ptr, x_type, m, Weight, y_ptr)."""
+        ops = list(ops)
+        arr = (Op * len(ops))()
+        for i, (xp, xt, m, w, yp) in enumerate(ops):
+            arr[i] = Op(xp, yp, w.handle, m, xt)
+        return arr
+
+    def matmul_batch(self, ops_array) -> None:
+        check(lib().mx4_matmul_batch(self.handle, ops_array, len(ops_array)))
+
+    def record(self, fn) -> "Pass":
+        """Record everything fn() enqueues into a replayable pass (HIP graph)."""
+        check(lib().mx4_pass_begin(self.handle))
+        try:
+            fn()
+        finally:
+            h = _vp()
+            st = lib().mx4_pass_end(self.handle, ctypes.byref(h))
+        check(st)
+        return Pass(self, h.value)
+
+    def dequantize(self, w: Weight, out: DeviceBuffer) -> None:
+        check(lib().mx4_dequantize(self.handle, w.handle, out.ptr))
+
+    def quantize(self, x: DeviceBuffer, xtype: int, rows: int, cols: int, packed: DeviceBuffer,
+                 scales: DeviceBuffer) -> None:
+        check(lib().mx4_quantize(self.handle, x.ptr, xtype, rows, cols, packed.ptr, scales.ptr))
+
+    def quantize_fp8(self, x: DeviceBuffer, xtype: int, rows: int, cols: int, codes: DeviceBuffer,
+                     scales: DeviceBuffer) -> None:
+        check(lib().mx4_quantize_fp8(self.handle, x.ptr, xtype, rows, cols, codes.ptr, scales.ptr))
+
+    def argmax_rows(self, x: DeviceBuffer, rows: int, width: int, out: DeviceBuffer) -> None:
+        check(lib().mx4_argmax_rows(self.handle, x.ptr, rows, width, out.ptr))
+
+    def synth_bf16(self, seed: int, sigma: float, count: int, out: DeviceBuffer, start: int = 0) -> None:
+        check(lib().mx4_synth_bf16(self.handle, seed, sigma, start, count, out.ptr))
+
+    def decode_table(self, mode: int) -> np.ndarray:
+        out = self.buffer(256 * 16 * 4)
+        check(lib().mx4_decode_table(self.handle, mode, out.ptr))
+        return out.download(np.float32).reshape(256, 16)
+
+    def timer_begin(self) -> None:
+        check(lib().mx4_timer_begin(self.handle))
+
+    def timer_end(self) -> float:
+        ms = ctypes.c_double()
+        check(lib().mx4_timer_end(self.handle, ctypes.byref(ms)))
+        return ms.value
+
+
+class Pass:
+    def __init__(self, ctx: Context, handle: int):
+        self.ctx, self.handle = ctx, handle
+
+    def launch(self) -> None:
+        check(lib().mx4_pass_launch(self.ctx.handle, self.handle))
+
+    def release(self) -> None:
+        if self.handle:
+            lib().mx4_pass_release(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+
+class Hip:
+    """Per-call backend over qwen_hip_* with the shape of the reference's Metal
+    wrapper (engine/src/metal.rs:21-72): construct once, matmul(x, packed,
+    scales) -> y, synchronous, raises on failure (the reference asserts)."""
+
+    def __init__(self):
+        self.handle = lib().qwen_hip_create()
+        if not self.handle:
+            raise RuntimeError(f"could not initialize HIP: {last_error()}")
+
+    def matmul(self, x: np.ndarray, packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        rows, inner = x.shape
+        cols = packed.size * 2 // inner
+        y = np.empty((rows, cols), dtype=np.float32)
+        ok = lib().qwen_hip_matmul(self.handle, _ptr(x, _f32p), _ptr(packed), _ptr(scales, _u8p),
+                                   _ptr(y, _f32p), rows, cols, inner)
+        if not ok:
+            raise RuntimeError(f"HIP projection failed: {last_error()}")
+        return y
+
+    def set_cache_limit(self, nbytes: int) -> None:
+        lib().qwen_hip_set_cache_limit(self.handle, nbytes)
+
+    def close(self) -> None:
+        if self.handle:
+            lib().qwen_hip_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,352 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the CPU oracle.
+
+Bars: bit-exact for decode, quantize, requantize, the generator and argmax;
+max_i |y_i - r_i| / max_i |r_i| <= 1e-3 for matmuls against the oracle r
+(engine/src/lib.rs:240-266), plus the reference's own per-element bound
+|a - b| < 1e-3 + 1e-5 |b| (engine/src/metal.rs:110). Observed errors are ~1e-6.
+"""
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+KATS = json.loads((GOLDEN / "reference_kats.json").read_text())
+REL_TOL = 1e-3
+
+QWEN17 = {"q": (2048, 2048), "k": (1024, 2048), "v": (1024, 2048), "o": (2048, 2048),
+          "gate": (6144, 2048), "up": (6144, 2048), "down": (2048, 6144), "lm_head": (151936, 2048)}
+QWEN8 = {"q": (4096, 4096), "k": (1024, 4096), "v": (1024, 4096), "o": (4096, 4096),
+         "gate": (12288, 4096), "up": (12288, 4096), "down": (4096, 12288), "lm_head": (151936, 4096)}
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def mx4():
+    import mx4hip
+
+    if mx4hip.device_count() < 1:
+        pytest.fail("no gfx950 device visible to the HIP library")
+    return mx4hip
+
+
+@pytest.fixture(scope="module")
+def ctx(mx4):
+    c = mx4.Context(0)
+    yield c
+    c.close()
+
+
+def f32_bits(a):
+    return np.asarray(a, dtype=np.float32).view(np.uint32)
+
+
+def max_rel(y, r):
+    denom = float(np.max(np.abs(r)))
+    return float(np.max(np.abs(y.astype(np.float64) - r.astype(np.float64)))) / (denom if denom else 1.0)
+
+
+def assert_close(y, r, what):
+    rel = max_rel(y, r)
+    assert rel <= REL_TOL, f"{what}: max rel err {rel:.3e}"
+    ok = np.abs(y - r) < 1e-3 + 1e-5 * np.abs(r)
+    if not np.all(ok):
+        # the absolute form assumes O(1) outputs; apply it to the normalised values
+        scale = max(float(np.max(np.abs(r))), 1.0)
+        assert np.all(np.abs(y - r) / scale < 1e-3 + 1e-5 * np.abs(r) / scale), what
+    return rel
+
+
+def run_matmul(mx4, ctx, x_f32, w, path, xtype=None):
+    """Upload x (f32 or its bf16 bits), run one matmul through the C ABI, download y."""
+    m, k = x_f32.shape
+    xtype = mx4.F32 if xtype is None else xtype
+    if xtype == mx4.BF16:
+        bits = (f32_bits(x_f32) >> 16).astype(np.uint16)
+        assert np.array_equal(f32_bits(x_f32) & 0xFFFF, np.zeros_like(f32_bits(x_f32))), "x not bf16"
+        xb = ctx.to_device(bits)
+    else:
+        xb = ctx.to_device(np.ascontiguousarray(x_f32, np.float32))
+    yb = ctx.buffer(m * w.rows * 4)
+    ctx.matmul(xb, xtype, m, w, yb, path)
+    return yb.download(np.float32).reshape(m, w.rows)
+
+
+# ------------------------------------------------------------------ decode
+
+def test_decode_table_bit_exact(mx4, ctx, oracle):
+    say("decode tables: 16 codes x 255 scale bytes")
+    codes = np.arange(16, dtype=np.uint8)
+    packed = np.tile((codes[0::2] | (codes[1::2] << 4)).astype(np.uint8), 2 * 255)
+    scales = np.arange(255, dtype=np.uint8)
+    want = oracle.mx_values(packed, scales, 0, 255 * 32).reshape(255, 32)[:, :16]
+    for mode in (0, 1):  # bit construction; hardware converter x 2^(s-127)
+        got = ctx.decode_table(mode)[:255]
+        bad = np.argwhere(f32_bits(got) != f32_bits(want))
+        assert bad.size == 0, f"mode {mode}: first mismatches (s, c) {bad[:8].tolist()}"
+    # scale folded into bf16: exact wherever the result is a normal bf16
+    got = ctx.decode_table(2)[2:255]
+    assert np.array_equal(f32_bits(got), f32_bits(want[2:])), "bf16 fold mode"
+
+
+def test_dequantize_bit_exact(mx4, ctx, oracle):
+    rng = np.random.default_rng(1)
+    packed = rng.integers(0, 256, (37, 96 // 2), dtype=np.uint8)
+    scales = rng.integers(0, 255, (37, 96 // 32), dtype=np.uint8)
+    w = ctx.upload_weight(packed, scales, 37, 96)
+    out = ctx.buffer(37 * 96 * 4)
+    ctx.dequantize(w, out)
+    got = out.download(np.float32)
+    want = oracle.mx_values(packed.reshape(-1), scales.reshape(-1), 0, 37 * 96)
+    assert np.array_equal(f32_bits(got), f32_bits(want))
+    # engine/src/mxfp4.rs:56-65
+    w2 = ctx.upload_weight(np.full(16, 0x82, np.uint8), np.zeros(1, np.uint8), 1, 32)
+    out2 = ctx.buffer(32 * 4)
+    ctx.dequantize(w2, out2)
+    v = out2.download(np.float32)
+    assert f32_bits(v[0]) == 0x00400000 and f32_bits(v[1]) == 0x80000000
+
+
+# ------------------------------------------------------------------ quantize
+
+def _quantize_cases(rng):
+    return [
+        (rng.standard_normal((64, 256)) * 0.02).astype(np.float32),
+        (rng.standard_normal((8, 128)) * rng.choice([1e-40, 1e-3, 1, 1e30], (8, 1))).astype(np.float32),
+        (rng.integers(-24, 25, (8, 64)) * 0.25).astype(np.float32),   # exact midpoints
+        np.where(rng.random((4, 64)) < 0.5, -0.0, 0.0).astype(np.float32),
+        np.full((2, 32), 3.0e38, np.float32),
+    ]
+
+
+@pytest.mark.parametrize("xtype", ["f32", "bf16"])
+def test_quantize_bit_exact(mx4, ctx, oracle, xtype):
+    rng = np.random.default_rng(2)
+    for vals in _quantize_cases(rng):
+        if xtype == "bf16":
+            bits = (f32_bits(vals) >> 16).astype(np.uint16)
+            vals = oracle.bf16_to_f32(bits).reshape(vals.shape)
+            src = ctx.to_device(bits)
+            t = mx4.BF16
+        else:
+            src = ctx.to_device(vals)
+            t = mx4.F32
+        r, c = vals.shape
+        pk, sc = ctx.buffer(r * c // 2), ctx.buffer(r * c // 32)
+        ctx.quantize(src, t, r, c, pk, sc)
+        want_p, want_s = oracle.quantize(vals)
+        assert np.array_equal(pk.download(np.uint8).reshape(r, -1), want_p)
+        assert np.array_equal(sc.download(np.uint8).reshape(r, -1), want_s)
+
+
+def test_quantize_rejects_non_finite(mx4, ctx):
+    vals = np.zeros((1, 32), np.float32)
+    vals[0, 3] = np.inf
+    src = ctx.to_device(vals)
+    pk, sc = ctx.buffer(16), ctx.buffer(1)
+    with pytest.raises(mx4.Mx4Error, match="non-finite"):
+        ctx.quantize(src, mx4.F32, 1, 32, pk, sc)
+
+
+def test_quantize_fp8_bit_exact(mx4, ctx, oracle):
+    rng = np.random.default_rng(3)
+    for vals in _quantize_cases(rng):
+        r, c = vals.shape
+        src = ctx.to_device(vals)
+        cd, sc = ctx.buffer(r * c), ctx.buffer(r * c // 32)
+        ctx.quantize_fp8(src, mx4.F32, r, c, cd, sc)
+        want_c, want_s = oracle.quantize_fp8(vals)
+        assert np.array_equal(cd.download(np.uint8).reshape(r, -1), want_c)
+        assert np.array_equal(sc.download(np.uint8).reshape(r, -1), want_s)
+
+
+# ------------------------------------------------------------------ generator
+
+def test_synth_matches_oracle_generator(mx4, ctx, oracle):
+    say("generator: 2M bf16 values")
+    n = 1 << 21
+    out = ctx.buffer(n * 2)
+    for seed, sigma, start in [(0, 0.02, 0), (1, 1.0, 0), (7, 0.02, 12345)]:
+        ctx.synth_bf16(seed, sigma, n, out, start=start)
+        got = out.download(np.uint16)
+        assert np.array_equal(got, oracle.synth_bf16(seed, sigma, n, start=start)), (seed, sigma, start)
+    fx = json.loads((GOLDEN / "synth_fixtures.json").read_text())
+    for case in fx["prefixes"].values():
+        ctx.synth_bf16(case["seed"], case["sigma"], 64, out)
+        assert out.download(np.uint16, 64).tolist() == case["bf16"]
+
+
+def test_synth_weight_matches_recipe(mx4, ctx, oracle):
+    import hashlib
+
+    fx = json.loads((GOLDEN / "synth_fixtures.json").read_text())["gemv_2048x6144"]
+    w = ctx.synth_weight(fx["w_seed"], fx["n"], fx["k"], fx["w_sigma"])
+    packed, scales = ctx.download_weight(w)
+    assert hashlib.sha256(packed.tobytes()).hexdigest() == fx["sha256_packed"]
+    assert hashlib.sha256(scales.tobytes()).hexdigest() == fx["sha256_scales"]
+
+
+# ------------------------------------------------------------------ matmul KATs
+
+def test_identity_decodes_every_code(mx4, ctx, oracle):
+    kat = KATS["identity_all_codes"]  # engine/tests/mxfp4.rs:9-33
+    packed = np.tile(np.array(kat["packed_row"], np.uint8), kat["packed_repeat"])
+    w = ctx.upload_weight(packed, np.array(kat["scales"], np.uint8), 1, 32)
+    y = run_matmul(mx4, ctx, np.eye(32, dtype=np.float32), w, mx4.PATH_GENERIC)
+    # by value, as the reference's assert_eq! on f32 (-0.0 == 0.0) ...
+    assert np.array_equal(y.reshape(-1), np.array(kat["expect"], np.float32))
+    # ... and bitwise against the oracle, whose 0.0 + (-0.0) sums are +0.0
+    want = oracle.matmul(np.eye(32, dtype=np.float32), packed, np.array(kat["scales"], np.uint8))
+    assert np.array_equal(f32_bits(y), f32_bits(want))
+    # M = 1 one-hot rows through the auto dispatch
+    for i in (0, 9, 31):
+        x = np.zeros((1, 32), np.float32)
+        x[0, i] = 1.0
+        y1 = run_matmul(mx4, ctx, x, w, mx4.PATH_AUTO)
+        assert y1[0, 0] == np.float32(kat["expect"][i])
+
+
+def test_rows_and_blocks_use_different_scales(mx4, ctx):
+    kat = KATS["rows_and_blocks_use_different_scales"]  # engine/tests/mxfp4.rs:88-105
+    w = ctx.upload_weight(np.full(64, kat["packed_fill"], np.uint8), np.array(kat["scales"], np.uint8), 2, 64)
+    x = np.zeros(3 * 64, np.float32)
+    x[kat["input_ones"]] = 1.0
+    y = run_matmul(mx4, ctx, x.reshape(3, 64), w, mx4.PATH_AUTO)
+    assert y.reshape(-1).tolist() == kat["expect"]
+
+
+def test_dropin_matches_cpu_for_decode_and_prefill(mx4, oracle):
+    # engine/src/metal.rs:86-114 for the HIP backend through qwen_hip_matmul
+    hip = mx4.Hip()
+    try:
+        packed = (np.arange(21 * 32) % 256).astype(np.uint8)
+        scales = (122 + np.arange(21 * 2) % 7).astype(np.uint8)
+        for rows in [1, 2, 4, 8, 16, 19, 33]:
+            x = (((np.arange(rows * 64) % 37) - 18.0) / 19.0).astype(np.float32).reshape(rows, 64)
+            expected = oracle.matmul(x, packed, scales)
+            actual = hip.matmul(x, packed, scales)
+            assert actual.shape == expected.shape
+            assert np.all(np.abs(actual - expected) < 1e-3 + np.abs(expected) * 1e-5), rows
+        # the cache is keyed by host pointer: the same arrays are not re-uploaded,
+        # a second weight at another address is
+        packed2 = packed.copy()
+        packed2[:16] = 0x77  # row 0, block 0: all codes 6.0
+        x = np.ones((1, 64), np.float32)
+        assert not np.array_equal(hip.matmul(x, packed2, scales), hip.matmul(x, packed, scales))
+        # failures return false (here: raise), nothing is launched
+        with pytest.raises(RuntimeError, match="NaN scale"):
+            hip.matmul(x, packed, np.full(42, 255, np.uint8))
+    finally:
+        hip.close()
+
+
+# ------------------------------------------------------------------ GEMV at model shapes
+
+def _sample_rows(n, count, rng):
+    if n <= count:
+        return np.arange(n)
+    return np.unique(np.concatenate([[0, n - 1], rng.choice(n, count, replace=False)]))
+
+
+@pytest.mark.parametrize("model", ["1.7B", "8B"])
+def test_gemv_model_shapes(mx4, ctx, oracle, model):
+    shapes = QWEN17 if model == "1.7B" else QWEN8
+    rng = np.random.default_rng(4)
+    for j, (name, (n, k)) in enumerate(shapes.items()):
+        say(f"gemv {model} {name} {k}->{n}")
+        w = ctx.synth_weight(100 + j, n, k, 0.02)
+        packed, scales = ctx.download_weight(w)
+        xbits = oracle.synth_bf16(1, 1.0, k)
+        x = oracle.bf16_to_f32(xbits).reshape(1, k)
+        rows = _sample_rows(n, 384, rng)
+        ref = np.concatenate([oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), int(r), int(r) + 1)
+                              for r in rows], axis=1)
+        for xtype in (mx4.BF16, mx4.F32):
+            y = run_matmul(mx4, ctx, x, w, mx4.PATH_AUTO, xtype)
+            assert np.all(np.isfinite(y))
+            assert_close(y[:, rows], ref, f"{model} {name} xtype={xtype}")
+        w.release()
+
+
+def test_gemv_config1_against_fixture(mx4, ctx, oracle):
+    import hashlib
+
+    fx = json.loads((GOLDEN / "synth_fixtures.json").read_text())["gemv_2048x6144"]
+    w = ctx.synth_weight(fx["w_seed"], fx["n"], fx["k"], fx["w_sigma"])
+    packed, scales = ctx.download_weight(w)
+    x = oracle.bf16_to_f32(oracle.synth_bf16(fx["x_seed"], fx["x_sigma"], fx["k"])).reshape(1, -1)
+    ref = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
+    assert hashlib.sha256(ref.tobytes()).hexdigest() == fx["sha256_y_f32"]
+    for xtype in (mx4.BF16, mx4.F32):
+        y = run_matmul(mx4, ctx, x, w, mx4.PATH_GEMV, xtype)
+        assert_close(y, ref, "config 1")
+        assert oracle.argmax(y[0]) == fx["argmax"]
+
+
+def test_lm_head_greedy_argmax_identical(mx4, ctx, oracle):
+    n, k = QWEN17["lm_head"]
+    say("lm_head argmax 2048->151936, full oracle")
+    w = ctx.synth_weight(7, n, k, 0.02)
+    packed, scales = ctx.download_weight(w)
+    idx = ctx.buffer(4 * 4)
+    for seed in (1, 2, 3):
+        x = oracle.bf16_to_f32(oracle.synth_bf16(seed, 1.0, k)).reshape(1, k)
+        ref = oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), 0, n, threads=16)
+        xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+        yb = ctx.buffer(n * 4)
+        ctx.matmul(xb, mx4.BF16, 1, w, yb)
+        ctx.argmax_rows(yb, 1, n, idx)
+        y = yb.download(np.float32).reshape(1, n)
+        assert_close(y, ref, "lm_head")
+        assert int(idx.download(np.uint32, 1)[0]) == oracle.argmax(ref[0])
+        assert oracle.argmax(y[0]) == oracle.argmax(ref[0])
+
+
+def test_argmax_rows_first_max_rule(mx4, ctx, oracle):
+    rng = np.random.default_rng(6)
+    rows = [rng.standard_normal(151936).astype(np.float32) for _ in range(3)]
+    rows[1][[5, 777, 151935]] = 100.0                       # planted ties -> 5
+    rows[2][:] = -np.inf                                    # nothing beats column 0
+    extra = np.array([np.nan, 9.0, 9.0] + [0.0] * (151936 - 3), np.float32)  # NaN in column 0 -> 0
+    x = np.stack(rows + [extra])
+    xb, out = ctx.to_device(x), ctx.buffer(4 * 4)
+    ctx.argmax_rows(xb, 4, x.shape[1], out)
+    got = out.download(np.uint32).tolist()
+    assert got == [oracle.argmax(r) for r in x]
+
+
+# ------------------------------------------------------------------ generic / odd shapes
+
+@pytest.mark.parametrize("m,n,k", [(1, 5, 32), (1, 7, 96), (3, 9, 160), (5, 33, 64), (17, 12, 2048),
+                                   (33, 40, 256), (1, 300, 8192)])
+def test_generic_shapes(mx4, ctx, oracle, m, n, k):
+    rng = np.random.default_rng(m * 1000 + n)
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(110, 135, (n, k // 32), dtype=np.uint8)
+    w = ctx.upload_weight(packed, scales, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
+    for path in (mx4.PATH_AUTO, mx4.PATH_GENERIC):
+        y = run_matmul(mx4, ctx, x, w, path)
+        assert_close(y, ref, f"m={m} n={n} k={k} path={path}")
+
+
+def test_errors_are_reported_not_launched(mx4, ctx):
+    w = ctx.upload_weight(np.zeros(16, np.uint8), np.array([127], np.uint8), 1, 32)
+    x, y = ctx.buffer(64 * 4), ctx.buffer(64 * 4)
+    with pytest.raises(mx4.Mx4Error, match="m must be"):
+        ctx.matmul(x, mx4.F32, 0, w, y)
+    with pytest.raises(mx4.Mx4Error, match="GEMV path"):
+        ctx.matmul(x, mx4.F32, 2, w, y, mx4.PATH_GEMV)
+    with pytest.raises(mx4.Mx4Error):
+        ctx.upload_weight(np.zeros(16, np.uint8), np.array([255], np.uint8), 1, 32)
+    with pytest.raises(mx4.Mx4Error, match="divisible"):
+        ctx.upload_weight(np.zeros(16, np.uint8), np.array([127], np.uint8), 1, 31)
