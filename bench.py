@@ -8,8 +8,11 @@ gate 4096->12288, up 4096->12288, down 12288->4096} plus lm_head 4096->151936,
 resident weight (4.03 GB in HBM, far beyond the 256 MB Infinity Cache), made on
 the GPU by the weight recipe (bf16 N(0, 0.02), MXFP4 by the reference rule;
 tensor j uses seed 1000 + j). Activations are bf16 N(0, 1) from seed 1, already
-in HBM; outputs are f32. A step is replayed as one recorded pass (HIP graph)
-unless --eager is given.
+in HBM; outputs are f32. Projections that read the same activations in the
+model share a launch, as a decode step allows: q|k|v and gate|up, so a layer
+is 4 launches (qkv, o, gate|up, down) and the step 145. A step is replayed as
+one recorded pass (HIP graph) unless --eager is given; --separate launches all
+253 GEMVs one by one.
 
 Algorithmic bytes of one GEMV: N*K/2 (nibbles) + N*K/32 (scales) + M*K*2 (bf16
 x) + M*N*4 (f32 y). value = bytes per step / wall time per step.
@@ -64,24 +67,46 @@ def build_step(ctx: mx4hip.Context):
 
 
 def time_shapes(ctx, weights, xs, ys, reps: int = 3):
-    """Per-shape GPU time: the 36 distinct copies of a shape back to back (cold
-    weights), timed with events on the context stream."""
+    """Per-launch GPU time of each projection shape and of the grouped launches:
+    the 36 distinct copies back to back (cold weights) in a recorded pass, timed
+    with events on the context stream."""
+    by = {}
+    for (nm, n, k, w) in weights:
+        by.setdefault(nm, []).append((n, k, w))
+    plans = [(name, [name]) for name, _, _ in LAYER] + [("qkv", ["q", "k", "v"]), ("gate_up", ["gate", "up"]),
+                                                         ("lm_head", ["lm_head"])]
     table = {}
-    for name, n, k in LAYER + [LM_HEAD]:
-        ws = [w for (nm, _, _, w) in weights if nm == name]
-        ops = ctx.make_ops([(xs[k].ptr, mx4hip.BF16, 1, w, ys[n].ptr) for w in ws])
-        ctx.matmul_batch(ops)
+    for label, members in plans:
+        copies = len(by[members[0]])
+        k = by[members[0]][0][1]
+        ybufs = [ys[by[m][0][0]] for m in members]
+        if len(members) > 1:
+            yext = [ctx.buffer(by[m][0][0] * 4) for m in members]
+            ybufs = yext
+
+        def enqueue():
+            for c in range(copies):
+                ws = [by[m][c][2] for m in members]
+                if len(ws) == 1:
+                    ctx.matmul_ptr(xs[k].ptr, mx4hip.BF16, 1, ws[0], ybufs[0].ptr)
+                else:
+                    ctx.matmul_group(xs[k].ptr, mx4hip.BF16, 1, ws, [y.ptr for y in ybufs])
+
+        p = ctx.record(enqueue)
+        p.launch()
         best = None
         for _ in range(reps):
             ctx.synchronize()
             ctx.timer_begin()
-            ctx.matmul_batch(ops)
-            ms = ctx.timer_end() / len(ws)
+            p.launch()
+            ms = ctx.timer_end() / copies
             best = ms if best is None else min(best, ms)
-        b = gemv_bytes(1, n, k)
-        table[name] = {"k": k, "n": n, "bytes": b, "us": round(best * 1e3, 3),
-                       "GBps": round(b / (best * 1e-3) / 1e9, 1),
-                       "frac": round(b / (best * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        p.release()
+        b = sum(gemv_bytes(1, by[m][0][0], k) for m in members)
+        n = sum(by[m][0][0] for m in members)
+        table[label] = {"k": k, "n": n, "bytes": b, "us": round(best * 1e3, 3),
+                        "GBps": round(b / (best * 1e-3) / 1e9, 1),
+                        "frac": round(b / (best * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     return table
 
 
@@ -115,7 +140,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--eager", action="store_true", help="enqueue each step with one batch call instead of a recorded pass")
+    ap.add_argument("--eager", action="store_true", help="enqueue each step from the host instead of replaying a recorded pass")
+    ap.add_argument("--separate", action="store_true", help="one launch per projection (253) instead of q|k|v and gate|up groups")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-shapes", action="store_true")
     args = ap.parse_args()
@@ -146,14 +172,33 @@ def main() -> int:
 
     ops = ctx.make_ops([(xs[k].ptr, mx4hip.BF16, 1, w, ys[n].ptr) for (_, n, k, w) in weights])
     step_bytes = sum(gemv_bytes(1, n, k) for (_, n, k, _) in weights)
+    # per layer: q|k|v share x, gate|up share x (distinct y buffers for each)
+    yq = {name: ctx.buffer(n * 4) for name, n, _ in LAYER}
 
-    if args.eager:
-        step = lambda: ctx.matmul_batch(ops)  # noqa: E731
-        launch = "eager batch (one C call per step)"
+    def enqueue_grouped():
+        for layer in range(LAYERS):
+            lw = {name: w for (name, _, _, w) in weights[layer * len(LAYER):(layer + 1) * len(LAYER)]}
+            ctx.matmul_group(xs[4096].ptr, mx4hip.BF16, 1, [lw["q"], lw["k"], lw["v"]],
+                             [yq["q"].ptr, yq["k"].ptr, yq["v"].ptr])
+            ctx.matmul_ptr(xs[4096].ptr, mx4hip.BF16, 1, lw["o"], yq["o"].ptr)
+            ctx.matmul_group(xs[4096].ptr, mx4hip.BF16, 1, [lw["gate"], lw["up"]], [yq["gate"].ptr, yq["up"].ptr])
+            ctx.matmul_ptr(xs[12288].ptr, mx4hip.BF16, 1, lw["down"], yq["down"].ptr)
+        _, n, k, w = weights[-1]
+        ctx.matmul_ptr(xs[k].ptr, mx4hip.BF16, 1, w, ys[n].ptr)
+
+    if args.separate:
+        enqueue = lambda: ctx.matmul_batch(ops)  # noqa: E731
+        launches = len(weights)
     else:
-        pss = ctx.record(lambda: ctx.matmul_batch(ops))
+        enqueue = enqueue_grouped
+        launches = LAYERS * 4 + 1
+    if args.eager:
+        step = enqueue
+        launch = f"eager, {launches} launches per step"
+    else:
+        pss = ctx.record(enqueue)
         step = pss.launch
-        launch = "recorded pass (HIP graph) per step"
+        launch = f"recorded pass (HIP graph), {launches} launches per step"
 
     for _ in range(args.warmup):
         step()

@@ -147,6 +147,22 @@ mx4_status mx4_matmul(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uin
  * use mx4_matmul_prefill). */
 mx4_status mx4_matmul_path(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m,
                            const mx4_weight *w, float *y_dev, mx4_path path);
+/* Up to 4 weights of the same width that read the same activations (q|k|v,
+ * gate|up) in one launch: y_dev[i][m][w[i].rows] = x . W_i^T. For m == 1 this
+ * is one GEMV over the concatenated rows; otherwise the projections run one
+ * after another. Same arithmetic as mx4_matmul. */
+mx4_status mx4_matmul_group(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m,
+                            const mx4_weight *const *w, float *const *y_dev, uint32_t count);
+
+/* Tuning hook for the M == 1 GEMV over a group of 1 to 4 weights (as
+ * mx4_matmul_group): waves per team (the team splits each row's K; K/32 must
+ * be a multiple of 64*team), rows per team per iteration (1, 2, 4 or 8, with
+ * rows * K/(2048*team) <= 8), and workgroups (0: the default grid). Zero team
+ * or rows keep the defaults. */
+mx4_status mx4_gemv_config(mx4_context *ctx, const void *x_dev, mx4_dtype x_type,
+                           const mx4_weight *const *w, float *const *y_dev, uint32_t count,
+                           int team_waves, int rows_per_team, uint32_t workgroups);
+
 /* Prefill on CDNA4 block-scaled MFMA (V_MFMA_SCALE_F32_*_F8F6F4): x is
  * requantized per 32 along K (MXFP4 by python/quantize_mxfp4.py:18-39, or MX
  * E4M3), then multiplied with the MXFP4 weight, f32 accumulation. The result
@@ -210,7 +226,8 @@ mx4_status mx4_timer_end(mx4_context *ctx, double *ms);
 /* Decode table of the hardware E2M1 converter as the kernels use it,
  * out_dev[s*16 + c] for scale byte s and code c (mode 0: bit construction,
  * 1: converter at scale 1 times 2^(s-127), 2: converter with the scale
- * folded into bf16). Used by the exhaustive decode test. */
+ * folded into bf16, 3: converter with the scale folded into f32). Used by the
+ * exhaustive decode test. */
 mx4_status mx4_decode_table(mx4_context *ctx, int mode, float *out_dev);
 
 #ifdef __cplusplus

@@ -68,95 +68,236 @@ struct LaneX<false, BPL> {
     __device__ __forceinline__ float dot(int j, const u32x4 w) const { return block_dot_f32(w, f[j]); }
 };
 
+// Up to kMaxSegs weights of the same width K that share one activation row
+// (q|k|v, gate|up) run as one launch: segment s owns rowsets
+// [first[s], first[s+1]) of the flattened row space.
+constexpr int kMaxSegs = 4;
+struct Segs {
+    const uint8_t* packed[kMaxSegs];
+    const uint8_t* scales[kMaxSegs];
+    float* y[kMaxSegs];
+    uint32_t n[kMaxSegs];
+    uint32_t first[kMaxSegs + 1];
+    uint32_t count;
+};
+
+// Sum R per-lane values over the 64 lanes of a wave with log2(64) exchange
+// steps: in the first log2(R) steps each lane keeps half of its values and
+// sends the other half to its partner, so the R totals need 63 + R - 1
+// additions in total instead of R * 63. Afterwards lane l holds the total of
+// row rowsel(l) = sum over the first log2(R) steps of (l & off ? half : 0).
+template <int R>
+__device__ __forceinline__ float wave_reduce_rows(float (&v)[R], uint32_t lane) {
+    int n = R;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        if (n > 1) {
+            const bool upper = (lane & off) != 0;
+            const int half = n / 2;
+#pragma unroll
+            for (int i = 0; i < R / 2; ++i) {
+                if (i < half) {
+                    float send = upper ? v[i] : v[i + half];
+                    float keep = upper ? v[i + half] : v[i];
+                    v[i] = keep + __shfl_xor(send, off, kWave);
+                }
+            }
+            n = half;
+        } else {
+            v[0] += __shfl_xor(v[0], off, kWave);
+        }
+    }
+    return v[0];
+}
+
+template <int R>
+__device__ __forceinline__ uint32_t reduced_row_of_lane(uint32_t lane) {
+    uint32_t row = 0;
+    int half = R / 2;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        if (half >= 1) {
+            row += (lane & off) ? half : 0;
+            half /= 2;
+        }
+    }
+    return row;
+}
+
+// Buffer resource over [base, base + bytes): loads past the end return zero
+// without touching memory, which bounds the tail row-set in hardware.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+constexpr int kNonTemporal = 2;  // streamed once per pass: do not keep in the caches
+
+template <bool XBF16, int BPL, int R>
+struct RowSet {
+    u32x4 w[R][BPL];
+    uint32_t s[R][BPL];
+};
+
+// One segment's fields, selected from the table with uniform conditional
+// moves (a dynamic index into the by-value table would become scalar loads
+// from the argument segment, with waits in the middle of the stream).
+struct Seg {
+    const uint8_t* packed;
+    const uint8_t* scales;
+    float* y;
+    uint32_t n, first;
+};
+
+__device__ __forceinline__ Seg pick_seg(const Segs& sg, uint32_t rs) {
+    Seg s{sg.packed[0], sg.scales[0], sg.y[0], sg.n[0], sg.first[0]};
+#pragma unroll
+    for (int q = 1; q < kMaxSegs; ++q) {
+        const bool in = q < (int)sg.count && rs >= sg.first[q];
+        s.packed = in ? sg.packed[q] : s.packed;
+        s.scales = in ? sg.scales[q] : s.scales;
+        s.y = in ? sg.y[q] : s.y;
+        s.n = in ? sg.n[q] : s.n;
+        s.first = in ? sg.first[q] : s.first;
+    }
+    return s;
+}
+
+// Issue the loads of one row-set. A row-set index past the end gets
+// zero-sized buffer resources: its loads return zeros without touching memory,
+// so the prefetch can be issued unconditionally. (A prefetch under a branch
+// makes the compiler's wait-count merge fall back to waiting for every load,
+// the prefetch included, which serialises streaming and compute.)
 template <bool XBF16, int WG, int BPL, int R>
-__global__ __launch_bounds__(64 * WG) void gemv_m1_kernel(const uint8_t* __restrict__ packed,
-                                                          const uint8_t* __restrict__ scales,
-                                                          const void* __restrict__ x,
-                                                          float* __restrict__ y, uint32_t n,
-                                                          uint32_t k, uint32_t rowsets) {
+__device__ __forceinline__ void load_rowset(const Segs& sg, uint32_t rs, uint32_t rowsets, uint32_t t,
+                                            uint32_t row_bytes, uint32_t nblk, RowSet<XBF16, BPL, R>& out) {
+    const bool valid = rs < rowsets;
+    const Seg sgm = pick_seg(sg, rs);
+    const uint32_t row0 = valid ? (rs - sgm.first) * R : 0;
+    uint32_t rows = sgm.n - row0 < (uint32_t)R ? sgm.n - row0 : (uint32_t)R;
+    rows = valid ? rows : 0;
+    const __amdgpu_buffer_rsrc_t wr = rsrc(sgm.packed + (size_t)row0 * row_bytes, rows * row_bytes);
+    const __amdgpu_buffer_rsrc_t sr = rsrc(sgm.scales + (size_t)row0 * nblk, rows * nblk);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+#pragma unroll
+        for (int j = 0; j < BPL; ++j) {
+            const uint32_t b = t + j * 64 * WG;
+            out.w[i][j] = __builtin_amdgcn_raw_buffer_load_b128(wr, 16 * b, i * row_bytes, kNonTemporal);
+            out.s[i][j] = __builtin_amdgcn_raw_buffer_load_b8(sr, b, i * nblk, 0);
+        }
+    }
+    // keep the stream ahead of the arithmetic that follows
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Sum over one row's blocks owned by this lane. The E8M0 scale is folded into
+// the hardware converter (level * 2^(s-127) is exact in bf16/f32 for scale
+// bytes 2..254, which the dispatcher guarantees), so each 32-element block costs
+// 16 conversions and 16 bf16 dot2 (or 32 f32 FMA) and one shift.
+template <bool XBF16, int BPL>
+__device__ __forceinline__ float row_dot(const LaneX<XBF16, BPL>& xr, const u32x4 (&w)[BPL], const uint32_t (&s)[BPL]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+        const float sc = __uint_as_float(s[j] << 23);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            if constexpr (XBF16) {
+                acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j][d], sc, 0),
+                                                      as_bf16x2(xr.p[j][4 * d + 0]), acc, false);
+                acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j][d], sc, 1),
+                                                      as_bf16x2(xr.p[j][4 * d + 1]), acc, false);
+                acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j][d], sc, 2),
+                                                      as_bf16x2(xr.p[j][4 * d + 2]), acc, false);
+                acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j][d], sc, 3),
+                                                      as_bf16x2(xr.p[j][4 * d + 3]), acc, false);
+            } else {
+                f32x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[j][d], sc, 0);
+                f32x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[j][d], sc, 1);
+                f32x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[j][d], sc, 2);
+                f32x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[j][d], sc, 3);
+                acc = __builtin_fmaf(xr.f[j][8 * d + 0], v0.x, acc);
+                acc = __builtin_fmaf(xr.f[j][8 * d + 1], v0.y, acc);
+                acc = __builtin_fmaf(xr.f[j][8 * d + 2], v1.x, acc);
+                acc = __builtin_fmaf(xr.f[j][8 * d + 3], v1.y, acc);
+                acc = __builtin_fmaf(xr.f[j][8 * d + 4], v2.x, acc);
+                acc = __builtin_fmaf(xr.f[j][8 * d + 5], v2.y, acc);
+                acc = __builtin_fmaf(xr.f[j][8 * d + 6], v3.x, acc);
+                acc = __builtin_fmaf(xr.f[j][8 * d + 7], v3.y, acc);
+            }
+        }
+    }
+    return acc;
+}
+
+template <bool XBF16, int WG, int BPL, int R>
+__device__ __forceinline__ void finish_rowset(const Segs& sg, uint32_t rs, const LaneX<XBF16, BPL>& xr,
+                                              const RowSet<XBF16, BPL, R>& cur, uint32_t t,
+                                              float (&red)[2][WG][R], uint32_t& parity) {
+    const uint32_t wave = t / 64, lane = t % 64;
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = row_dot<XBF16, BPL>(xr, cur.w[i], cur.s[i]);
+    const Seg sgm = pick_seg(sg, rs);
+    const uint32_t row0 = (rs - sgm.first) * R;
+    const uint32_t n = sgm.n;
+    float* y = sgm.y;
+    const float total = wave_reduce_rows<R>(acc, lane);
+    const uint32_t myrow = reduced_row_of_lane<R>(lane);
+    const bool writer = (lane & (64 / R - 1)) == 0;
+    if constexpr (WG == 1) {
+        if (writer && row0 + myrow < n) y[row0 + myrow] = total;
+    } else {
+        if (writer) red[parity][wave][myrow] = total;
+        __syncthreads();
+        if (t < (uint32_t)R) {
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WG; ++w) v += red[parity][w][t];
+            if (row0 + t < n) y[row0 + t] = v;
+        }
+        parity ^= 1;
+    }
+}
+
+template <bool XBF16, int WG, int BPL, int R>
+__global__ __launch_bounds__(64 * WG) void gemv_m1_kernel(Segs sg, const void* __restrict__ x, uint32_t k) {
     constexpr uint32_t T = 64 * WG;
     const uint32_t t = threadIdx.x;
-    const uint32_t wave = t / 64, lane = t % 64;
-    const size_t row_bytes = k / 2;
+    const uint32_t row_bytes = k / 2;
     const uint32_t nblk = k / 32;
+    const uint32_t rowsets = sg.first[sg.count];
+    uint32_t rs = blockIdx.x;
+    if (rs >= rowsets) return;
 
+    RowSet<XBF16, BPL, R> a, b;
+    load_rowset<XBF16, WG, BPL, R>(sg, rs, rowsets, t, row_bytes, nblk, a);
     LaneX<XBF16, BPL> xr;
     xr.load(x, t, T);
 
     __shared__ float red[2][WG][R];
-
-    u32x4 wa[R][BPL];
-    uint32_t sa[R][BPL];
-    auto load_set = [&](uint32_t rs, u32x4 (&w)[R][BPL], uint32_t (&s)[R][BPL]) {
-#pragma unroll
-        for (int i = 0; i < R; ++i) {
-            uint32_t row = rs * R + i;
-            row = row < n ? row : n - 1;  // clamp: tail rows read a valid row, never written
-            const uint8_t* prow = packed + row * row_bytes;
-            const uint8_t* srow = scales + (size_t)row * nblk;
-#pragma unroll
-            for (int j = 0; j < BPL; ++j) {
-                uint32_t b = t + j * T;
-                w[i][j] = load_u32x4_nt(prow + 16 * (size_t)b);
-                s[i][j] = srow[b];
-            }
-        }
-    };
-
-    uint32_t rs = blockIdx.x;
-    if (rs >= rowsets) return;
-    load_set(rs, wa, sa);
     uint32_t parity = 0;
-    for (; rs < rowsets; rs += gridDim.x) {
-        u32x4 wb[R][BPL];
-        uint32_t sb[R][BPL];
-        const uint32_t nxt = rs + gridDim.x;
-        if (nxt < rowsets) load_set(nxt, wb, sb);
-
-        float acc[R];
-#pragma unroll
-        for (int i = 0; i < R; ++i) {
-            float a = 0.0f;
-#pragma unroll
-            for (int j = 0; j < BPL; ++j) a = __builtin_fmaf(xr.dot(j, wa[i][j]), e8m0_to_f32(sa[i][j]), a);
-            acc[i] = wave_sum(a);
-        }
-        if constexpr (WG == 1) {
-            if (lane == 0) {
-#pragma unroll
-                for (int i = 0; i < R; ++i) {
-                    uint32_t row = rs * R + i;
-                    if (row < n) y[row] = acc[i];
-                }
-            }
-        } else {
-            if (lane == 0) {
-#pragma unroll
-                for (int i = 0; i < R; ++i) red[parity][wave][i] = acc[i];
-            }
-            __syncthreads();
-            if (t < R) {
-                float v = 0.0f;
-#pragma unroll
-                for (int w = 0; w < WG; ++w) v += red[parity][w][t];
-                uint32_t row = rs * R + t;
-                if (row < n) y[row] = v;
-            }
-            parity ^= 1;
-        }
-#pragma unroll
-        for (int i = 0; i < R; ++i)
-#pragma unroll
-            for (int j = 0; j < BPL; ++j) {
-                wa[i][j] = wb[i][j];
-                sa[i][j] = sb[i][j];
-            }
+    // ping-pong: the next row-set streams in while the current one is reduced
+    for (;;) {
+        uint32_t nxt = rs + gridDim.x;
+        load_rowset<XBF16, WG, BPL, R>(sg, nxt, rowsets, t, row_bytes, nblk, b);
+        finish_rowset<XBF16, WG, BPL, R>(sg, rs, xr, a, t, red, parity);
+        if (nxt >= rowsets) break;
+        rs = nxt;
+        nxt = rs + gridDim.x;
+        load_rowset<XBF16, WG, BPL, R>(sg, nxt, rowsets, t, row_bytes, nblk, a);
+        finish_rowset<XBF16, WG, BPL, R>(sg, rs, xr, b, t, red, parity);
+        if (nxt >= rowsets) break;
+        rs = nxt;
     }
 }
 
-// Generic exact kernel: any M (tokens processed MT at a time), any K % 32 == 0.
-// One wave per row; lanes stride over the row's blocks; activations are read
-// from global memory (L1/L2-resident) for every block.
+// Generic exact kernel: any M (tokens processed MT at a time), any K % 32 == 0,
+// any scale byte. Every element is decoded exactly as engine/src/mxfp4.rs:27-33
+// does (level * 2^(s-127): subnormal for small bytes, inf for large levels at
+// bytes 253/254) and multiplied with its activation, so inf/NaN and subnormal
+// weights behave like the reference's sequential loop; only the summation
+// order differs. One wave per weight row; lanes stride over the row's blocks.
 template <bool XBF16, int MT>
 __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* __restrict__ packed,
                                                            const uint8_t* __restrict__ scales,
@@ -174,79 +315,77 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* __rest
 #pragma unroll
     for (int q = 0; q < MT; ++q) acc[q] = 0.0f;
     for (uint32_t b = lane; b < nblk; b += 64) {
-        u32x4 w = load_u32x4(prow + 16 * (size_t)b);
-        float sc = e8m0_to_f32(srow[b]);
+        const u32x4 w = load_u32x4(prow + 16 * (size_t)b);
+        const float sc = e8m0_to_f32(srow[b]);
+        float wv[32];
+#pragma unroll
+        for (int e = 0; e < 32; ++e) wv[e] = level_of((w[e / 8] >> (4 * (e % 8))) & 15u) * sc;
 #pragma unroll
         for (int q = 0; q < MT; ++q) {
-            uint32_t tok = m0 + q < m ? m0 + q : m - 1;
-            float part;
+            const uint32_t tok = m0 + q < m ? m0 + q : m - 1;
             if constexpr (XBF16) {
                 const uint8_t* src = static_cast<const uint8_t*>(xv) + ((size_t)tok * k + (size_t)b * 32) * 2;
-                uint32_t xp[16];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    u32x4 v = load_u32x4(src + 16 * c);
-                    xp[4 * c + 0] = v[0];
-                    xp[4 * c + 1] = v[1];
-                    xp[4 * c + 2] = v[2];
-                    xp[4 * c + 3] = v[3];
+                    const u32x4 v = load_u32x4(src + 16 * c);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        acc[q] = __builtin_fmaf(bf16_bits_to_f32(v[e] & 0xffffu), wv[8 * c + 2 * e], acc[q]);
+                        acc[q] = __builtin_fmaf(bf16_bits_to_f32(v[e] >> 16), wv[8 * c + 2 * e + 1], acc[q]);
+                    }
                 }
-                part = block_dot_bf16(w, xp);
             } else {
                 const float* src = static_cast<const float*>(xv) + (size_t)tok * k + (size_t)b * 32;
-                float xf[32];
 #pragma unroll
                 for (int c = 0; c < 8; ++c) {
-                    f32x4 v = *reinterpret_cast<const f32x4*>(src + 4 * c);
-                    xf[4 * c + 0] = v[0];
-                    xf[4 * c + 1] = v[1];
-                    xf[4 * c + 2] = v[2];
-                    xf[4 * c + 3] = v[3];
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(src + 4 * c);
+                    acc[q] = __builtin_fmaf(v[0], wv[4 * c + 0], acc[q]);
+                    acc[q] = __builtin_fmaf(v[1], wv[4 * c + 1], acc[q]);
+                    acc[q] = __builtin_fmaf(v[2], wv[4 * c + 2], acc[q]);
+                    acc[q] = __builtin_fmaf(v[3], wv[4 * c + 3], acc[q]);
                 }
-                part = block_dot_f32(w, xf);
             }
-            acc[q] = __builtin_fmaf(part, sc, acc[q]);
         }
     }
 #pragma unroll
     for (int q = 0; q < MT; ++q) {
-        float v = wave_sum(acc[q]);
+        const float v = wave_sum(acc[q]);
         if (lane == 0 && m0 + q < m) y[(size_t)(m0 + q) * n + row] = v;
     }
 }
 
 // ------------------------------------------------------------------ launchers
 
-struct M1Config {
-    int wg, bpl, r;
-};
-
 template <bool XBF16, int WG, int BPL, int R>
-static hipError_t launch_m1(const GemvArgs& a, int max_groups) {
-    uint32_t rowsets = (a.n + R - 1) / R;
-    uint32_t grid = rowsets < (uint32_t)max_groups ? rowsets : (uint32_t)max_groups;
-    // even split: every team visits the same number of row-sets (+-1)
-    uint32_t per = (rowsets + grid - 1) / grid;
-    grid = (rowsets + per - 1) / per;
-    hipLaunchKernelGGL((gemv_m1_kernel<XBF16, WG, BPL, R>), dim3(grid), dim3(64 * WG), 0, a.stream,
-                       a.packed, a.scales, a.x, a.y, a.n, a.k, rowsets);
+static hipError_t go_m1(const Segs& sg, const void* x, uint32_t k, uint32_t grid, hipStream_t st) {
+    hipLaunchKernelGGL((gemv_m1_kernel<XBF16, WG, BPL, R>), dim3(grid), dim3(64 * WG), 0, st, sg, x, k);
     return hipGetLastError();
 }
 
-template <bool XBF16>
-static hipError_t dispatch_m1(const GemvArgs& a, int cus) {
-    const uint32_t nblk = a.k / 32;
-    // Waves per CU the persistent grid aims for; each wave keeps R*BPL KiB of
-    // packed weights (plus the prefetched set) in flight.
-    const int waves_per_cu = 8;
-    switch (nblk) {
-        case 64:  return launch_m1<XBF16, 1, 1, 4>(a, cus * waves_per_cu);
-        case 128: return launch_m1<XBF16, 1, 2, 4>(a, cus * waves_per_cu);
-        case 192: return launch_m1<XBF16, 1, 3, 2>(a, cus * waves_per_cu);
-        case 256: return launch_m1<XBF16, 2, 2, 4>(a, cus * waves_per_cu / 2);
-        case 384: return launch_m1<XBF16, 3, 2, 4>(a, cus * waves_per_cu / 3);
-        default:  return hipErrorNotSupported;
+// Rows per team allowed for a blocks-per-lane count: R * BPL <= 8 keeps the
+// double-buffered weights within 64 VGPRs.
+template <bool XBF16, int WG, int BPL>
+static hipError_t go_r(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int r, hipStream_t st) {
+    switch (r) {
+        case 1: return go_m1<XBF16, WG, BPL, 1>(sg, x, k, grid, st);
+        case 2: if constexpr (BPL <= 4) return go_m1<XBF16, WG, BPL, 2>(sg, x, k, grid, st); break;
+        case 4: if constexpr (BPL <= 2) return go_m1<XBF16, WG, BPL, 4>(sg, x, k, grid, st); break;
+        case 8: if constexpr (BPL <= 1) return go_m1<XBF16, WG, BPL, 8>(sg, x, k, grid, st); break;
+        default: break;
     }
+    return hipErrorNotSupported;
+}
+
+template <bool XBF16>
+static hipError_t go_cfg(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int wg, int bpl, int r,
+                         hipStream_t st) {
+#define MX4_M1_CASE(W, B) \
+    if (wg == W && bpl == B) return go_r<XBF16, W, B>(sg, x, k, grid, r, st);
+    MX4_M1_CASE(1, 1) MX4_M1_CASE(1, 2) MX4_M1_CASE(2, 1) MX4_M1_CASE(1, 3) MX4_M1_CASE(3, 1)
+    MX4_M1_CASE(1, 4) MX4_M1_CASE(2, 2) MX4_M1_CASE(4, 1) MX4_M1_CASE(1, 6) MX4_M1_CASE(2, 3)
+    MX4_M1_CASE(3, 2) MX4_M1_CASE(6, 1)
+#undef MX4_M1_CASE
+    return hipErrorNotSupported;
 }
 
 bool gemv_m1_supported(uint32_t k) {
@@ -254,8 +393,83 @@ bool gemv_m1_supported(uint32_t k) {
     return k % 32 == 0 && (nblk == 64 || nblk == 128 || nblk == 192 || nblk == 256 || nblk == 384);
 }
 
+// Default configuration: team size and rows per team by K, persistent grid
+// of about `waves_per_cu` waves per CU, every team visiting the same number
+// of rowsets (+-1).
+// Default configuration, from sweeps on MI355X over the launches of the Qwen3
+// 1.7B and 8B decode steps (q|k|v and gate|up grouped, cold weights, recorded
+// passes): the team splits K into 1-2 blocks per lane, 2-4 rows per team, and
+// a grid of up to `grid` teams (one row-set each when the matrix is small).
+static void default_m1_config(uint32_t k, uint32_t rows, int cus, M1Config& c) {
+    const uint32_t nblk = k / 32;
+    const uint32_t scale = (uint32_t)(cus > 0 ? cus : 256);  // the table is for 256 CUs
+    switch (nblk) {
+        case 64:  // K = 2048
+            c.wg = 1; c.r = rows > 8192 ? 4 : 2; c.grid = 8 * scale;
+            break;
+        case 128:  // K = 4096
+            c.wg = rows > 8192 ? 1 : 2; c.r = rows > 65536 ? 4 : 2; c.grid = (rows > 65536 ? 4 : 8) * scale;
+            break;
+        case 192:  // K = 6144
+            c.wg = 3; c.r = 2; c.grid = 4 * scale;
+            break;
+        case 256:  // K = 8192
+            c.wg = 2; c.r = 4; c.grid = 8 * scale;
+            break;
+        default:  // K = 12288
+            c.wg = 3; c.r = 2; c.grid = 16 * scale;
+            break;
+    }
+    c.waves_per_cu = 0;
+}
+
+hipError_t launch_gemv_m1_group(const GemvGroup& g, int cus, const M1Config* forced) {
+    if (g.count < 1 || g.count > kMaxSegs || !gemv_m1_supported(g.k)) return hipErrorNotSupported;
+    uint32_t rows = 0;
+    for (uint32_t s = 0; s < g.count; ++s) rows += g.n[s];
+    M1Config c;
+    default_m1_config(g.k, rows, cus, c);
+    if (forced) {
+        if (forced->wg) c.wg = forced->wg;
+        if (forced->r) c.r = forced->r;
+        if (forced->wg || forced->r || forced->grid) c.grid = forced->grid;
+    }
+    const uint32_t nblk = g.k / 32;
+    if (c.wg < 1 || nblk % (64u * c.wg) != 0) return hipErrorNotSupported;
+    const int bpl = (int)(nblk / (64u * c.wg));
+    Segs sg{};
+    sg.count = g.count;
+    sg.first[0] = 0;
+    for (uint32_t s = 0; s < g.count; ++s) {
+        sg.packed[s] = g.packed[s];
+        sg.scales[s] = g.scales[s];
+        sg.y[s] = g.y[s];
+        sg.n[s] = g.n[s];
+        sg.first[s + 1] = sg.first[s] + (g.n[s] + c.r - 1) / c.r;
+    }
+    for (uint32_t s = g.count; s < (uint32_t)kMaxSegs; ++s) sg.first[s + 1] = sg.first[g.count];
+    const uint32_t rowsets = sg.first[g.count];
+    // grid 0 (a forced configuration without a grid): one row-set per team
+    uint32_t grid = c.grid == 0 || c.grid > rowsets ? rowsets : c.grid;
+    // even split: every team visits the same number of row-sets (+-1)
+    const uint32_t per = (rowsets + grid - 1) / grid;
+    grid = (rowsets + per - 1) / per;
+    return g.x_bf16 ? go_cfg<true>(sg, g.x, g.k, grid, c.wg, bpl, c.r, g.stream)
+                    : go_cfg<false>(sg, g.x, g.k, grid, c.wg, bpl, c.r, g.stream);
+}
+
 hipError_t launch_gemv_m1(const GemvArgs& a, int cus) {
-    return a.x_bf16 ? dispatch_m1<true>(a, cus) : dispatch_m1<false>(a, cus);
+    GemvGroup g{};
+    g.count = 1;
+    g.packed[0] = a.packed;
+    g.scales[0] = a.scales;
+    g.y[0] = a.y;
+    g.n[0] = a.n;
+    g.k = a.k;
+    g.x = a.x;
+    g.x_bf16 = a.x_bf16;
+    g.stream = a.stream;
+    return launch_gemv_m1_group(g, cus, nullptr);
 }
 
 template <bool XBF16, int MT>

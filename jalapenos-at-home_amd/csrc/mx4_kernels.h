@@ -19,6 +19,25 @@ struct GemvArgs {
 
 bool gemv_m1_supported(uint32_t k);
 hipError_t launch_gemv_m1(const GemvArgs& a, int cus);
+
+// M == 1 over up to 4 weights of width k sharing one x (q|k|v, gate|up).
+struct GemvGroup {
+    const uint8_t* packed[4];
+    const uint8_t* scales[4];
+    float* y[4];
+    uint32_t n[4];
+    uint32_t count, k;
+    const void* x;
+    bool x_bf16;
+    hipStream_t stream;
+};
+// Kernel configuration of the M == 1 GEMV: waves per team (the team splits a
+// row's K), rows per team per iteration, teams in the grid (0: one row-set each).
+struct M1Config {
+    int wg = 0, r = 0, waves_per_cu = 0;
+    uint32_t grid = 0;
+};
+hipError_t launch_gemv_m1_group(const GemvGroup& g, int cus, const M1Config* forced);
 hipError_t launch_gemv_generic(const GemvArgs& a);
 
 // Exact skinny path (2 <= m <= 16) on bf16 MFMA with decoded weights.

@@ -203,6 +203,7 @@ hipError_t launch_dequantize(const uint8_t* packed, const uint8_t* scales, uint6
 //  mode 0: decode_exact (bit construction x ldexp)
 //  mode 1: hardware fp4 -> f32 at scale 1, times 2^(s-127) (the GEMV factorisation)
 //  mode 2: hardware fp4 -> bf16 with the scale folded in, widened to f32
+//  mode 3: hardware fp4 -> f32 with the scale folded in
 __global__ void decode_table_kernel(int mode, float* out) {
     const uint32_t s = blockIdx.x;      // 0..255
     const uint32_t c = threadIdx.x;     // 0..15
@@ -212,9 +213,11 @@ __global__ void decode_table_kernel(int mode, float* out) {
         v = decode_exact(c, s);
     } else if (mode == 1) {
         v = cvt_fp4x2_f32<0>(word).x * e8m0_to_f32(s);
-    } else {
+    } else if (mode == 2) {
         bf16x2 p = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, e8m0_to_f32(s), 0);
         v = bf16_bits_to_f32(as_u32(p) & 0xffffu);
+    } else {
+        v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, e8m0_to_f32(s), 0)[0];
     }
     out[s * 16 + c] = v;
 }

@@ -152,13 +152,19 @@ mx4_status check_matmul_args(mx4_context* ctx, const void* x, mx4_dtype xt, uint
     return MX4_OK;
 }
 
+// The fast kernels fold the E8M0 scale into the E2M1 converter and the
+// per-block sums; that is exact for scale bytes 2..252 (every byte the
+// reference quantizer emits for a nonzero block; python/quantize_mxfp4.py
+// never produces more than 252). Other bytes go to the exact generic kernel.
+bool scales_foldable(const mx4_weight* w) { return w->min_scale >= 2 && w->max_scale <= 252; }
+
 mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, const mx4_weight* w,
                       float* y, mx4_path path) {
     mx4::GemvArgs a{w->packed, w->scales, x, y, m, w->rows, w->cols, xt == MX4_BF16, ctx->stream};
     if (path == MX4_PATH_AUTO) {
-        if (m == 1 && mx4::gemv_m1_supported(w->cols))
+        if (m == 1 && mx4::gemv_m1_supported(w->cols) && scales_foldable(w))
             path = MX4_PATH_GEMV;
-        else if (m >= 2 && m <= 16 && mx4::skinny_supported(m, w->cols) && w->min_scale >= 2)
+        else if (m >= 2 && m <= 16 && mx4::skinny_supported(m, w->cols) && scales_foldable(w))
             path = MX4_PATH_SKINNY;
         else
             path = MX4_PATH_GENERIC;
@@ -168,13 +174,15 @@ mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
         case MX4_PATH_GEMV:
             if (m != 1 || !mx4::gemv_m1_supported(w->cols))
                 return fail(MX4_ERR_UNSUPPORTED, "GEMV path needs m == 1 and K/32 in {64,128,192,256,384}");
+            if (!scales_foldable(w))
+                return fail(MX4_ERR_UNSUPPORTED, "GEMV path folds scales into the converter; scale bytes outside 2..252 need GENERIC");
             e = mx4::launch_gemv_m1(a, ctx->cus);
             break;
         case MX4_PATH_SKINNY:
             if (!mx4::skinny_supported(m, w->cols))
                 return fail(MX4_ERR_UNSUPPORTED, "skinny path needs 1 <= m <= 16 and K %% 128 == 0");
-            if (w->min_scale < 2)
-                return fail(MX4_ERR_UNSUPPORTED, "skinny path folds scales into bf16; scale bytes < 2 need GENERIC");
+            if (!scales_foldable(w))
+                return fail(MX4_ERR_UNSUPPORTED, "skinny path folds scales into bf16; scale bytes outside 2..252 need GENERIC");
             e = mx4::launch_skinny(a, ctx->cus);
             break;
         case MX4_PATH_GENERIC:
@@ -442,6 +450,76 @@ mx4_status mx4_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
     return mx4_matmul_path(ctx, x, xt, m, w, y, MX4_PATH_AUTO);
 }
 
+mx4_status mx4_matmul_group(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, const mx4_weight* const* w,
+                            float* const* y, uint32_t count) {
+    if (!ctx || !w || !y) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (count < 1 || count > 4) return fail(MX4_ERR_ARGUMENT, "a group holds 1 to 4 weights");
+    for (uint32_t i = 0; i < count; ++i) {
+        mx4_status st = check_matmul_args(ctx, x, xt, m, w[i], y[i]);
+        if (st != MX4_OK) return fail(st, "weight %u: %s", i, g_error.c_str());
+        if (w[i]->cols != w[0]->cols) return fail(MX4_ERR_SHAPE, "grouped weights must share their width");
+    }
+    DeviceGuard g(ctx->device);
+    bool foldable = true;
+    for (uint32_t i = 0; i < count; ++i) foldable &= scales_foldable(w[i]);
+    if (m == 1 && mx4::gemv_m1_supported(w[0]->cols) && foldable) {
+        mx4::GemvGroup gg{};
+        gg.count = count;
+        gg.k = w[0]->cols;
+        gg.x = x;
+        gg.x_bf16 = xt == MX4_BF16;
+        gg.stream = ctx->stream;
+        for (uint32_t i = 0; i < count; ++i) {
+            gg.packed[i] = w[i]->packed;
+            gg.scales[i] = w[i]->scales;
+            gg.y[i] = y[i];
+            gg.n[i] = w[i]->rows;
+        }
+        hipError_t e = mx4::launch_gemv_m1_group(gg, ctx->cus, nullptr);
+        if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
+        return MX4_OK;
+    }
+    for (uint32_t i = 0; i < count; ++i) {
+        mx4_status st = run_matmul(ctx, x, xt, m, w[i], y[i], MX4_PATH_AUTO);
+        if (st != MX4_OK) return st;
+    }
+    return MX4_OK;
+}
+
+mx4_status mx4_gemv_config(mx4_context* ctx, const void* x, mx4_dtype xt, const mx4_weight* const* w,
+                           float* const* y, uint32_t count, int team_waves, int rows_per_team, uint32_t workgroups) {
+    if (!ctx || !w || !y) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (count < 1 || count > 4) return fail(MX4_ERR_ARGUMENT, "a group holds 1 to 4 weights");
+    if (team_waves < 0 || rows_per_team < 0) return fail(MX4_ERR_ARGUMENT, "negative configuration");
+    mx4::GemvGroup gg{};
+    for (uint32_t i = 0; i < count; ++i) {
+        mx4_status st = check_matmul_args(ctx, x, xt, 1, w[i], y[i]);
+        if (st != MX4_OK) return st;
+        if (w[i]->cols != w[0]->cols) return fail(MX4_ERR_SHAPE, "grouped weights must share their width");
+        if (!scales_foldable(w[i])) return fail(MX4_ERR_UNSUPPORTED, "scale bytes outside 2..252 need the generic kernel");
+        gg.packed[i] = w[i]->packed;
+        gg.scales[i] = w[i]->scales;
+        gg.y[i] = y[i];
+        gg.n[i] = w[i]->rows;
+    }
+    if (!mx4::gemv_m1_supported(w[0]->cols))
+        return fail(MX4_ERR_UNSUPPORTED, "GEMV path needs K/32 in {64,128,192,256,384}");
+    DeviceGuard g(ctx->device);
+    gg.count = count;
+    gg.k = w[0]->cols;
+    gg.x = x;
+    gg.x_bf16 = xt == MX4_BF16;
+    gg.stream = ctx->stream;
+    mx4::M1Config c;
+    c.wg = team_waves;
+    c.r = rows_per_team;
+    c.grid = workgroups;
+    hipError_t e = mx4::launch_gemv_m1_group(gg, ctx->cus, &c);
+    if (e == hipErrorNotSupported) return fail(MX4_ERR_UNSUPPORTED, "configuration not instantiated");
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
 mx4_status mx4_matmul_prefill(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, const mx4_weight* w,
                               mx4_act_format act, float* y) {
     mx4_status st = check_matmul_args(ctx, x, xt, m, w, y);
@@ -612,7 +690,7 @@ mx4_status mx4_timer_end(mx4_context* ctx, double* ms) {
 
 mx4_status mx4_decode_table(mx4_context* ctx, int mode, float* out) {
     if (!ctx || !out) return fail(MX4_ERR_ARGUMENT, "null argument");
-    if (mode < 0 || mode > 2) return fail(MX4_ERR_ARGUMENT, "bad mode");
+    if (mode < 0 || mode > 3) return fail(MX4_ERR_ARGUMENT, "bad mode");
     DeviceGuard g(ctx->device);
     hipError_t e = mx4::launch_decode_table(mode, out, ctx->stream);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "decode table launch failed: %s", hipGetErrorString(e));

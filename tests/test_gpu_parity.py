@@ -92,9 +92,12 @@ def test_decode_table_bit_exact(mx4, ctx, oracle):
         got = ctx.decode_table(mode)[:255]
         bad = np.argwhere(f32_bits(got) != f32_bits(want))
         assert bad.size == 0, f"mode {mode}: first mismatches (s, c) {bad[:8].tolist()}"
-    # scale folded into bf16: exact wherever the result is a normal bf16
-    got = ctx.decode_table(2)[2:255]
-    assert np.array_equal(f32_bits(got), f32_bits(want[2:])), "bf16 fold mode"
+    # scale folded into the converter (bf16 and f32 outputs): exact for every
+    # scale byte the fast kernels accept (2..252) and up to 254
+    for mode in (2, 3):
+        got = ctx.decode_table(mode)[2:255]
+        bad = np.argwhere(f32_bits(got) != f32_bits(want[2:]))
+        assert bad.size == 0, f"mode {mode}: first mismatches (s-2, c) {bad[:8].tolist()}"
 
 
 def test_dequantize_bit_exact(mx4, ctx, oracle):
@@ -350,3 +353,90 @@ def test_errors_are_reported_not_launched(mx4, ctx):
         ctx.upload_weight(np.zeros(16, np.uint8), np.array([255], np.uint8), 1, 32)
     with pytest.raises(mx4.Mx4Error, match="divisible"):
         ctx.upload_weight(np.zeros(16, np.uint8), np.array([127], np.uint8), 1, 31)
+
+
+# ------------------------------------------------------------------ kernel configurations
+
+CONFIG_SHAPES = [(1000, 2048), (1000, 4096), (700, 6144), (999, 8192), (700, 12288)]
+
+
+@pytest.mark.parametrize("n,k", CONFIG_SHAPES)
+def test_gemv_every_configuration(mx4, ctx, oracle, n, k):
+    """Every instantiated (team, rows, grid) of the M = 1 kernel agrees with the oracle,
+    including ragged tails (n not a multiple of the rows per team)."""
+    say(f"gemv configurations {k}->{n}")
+    w = ctx.synth_weight(77, n, k, 0.02)
+    packed, scales = ctx.download_weight(w)
+    xb16 = oracle.synth_bf16(3, 1.0, k)
+    x = oracle.bf16_to_f32(xb16).reshape(1, k)
+    ref = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
+    xdev = {mx4.BF16: ctx.to_device(xb16), mx4.F32: ctx.to_device(x)}
+    y = ctx.buffer(n * 4)
+    nblk = k // 32
+    tried = 0
+    for team in (1, 2, 3, 4, 6):
+        if nblk % (64 * team):
+            continue
+        bpl = nblk // (64 * team)
+        for rows in (1, 2, 4, 8):
+            if rows * bpl > 8:
+                continue
+            for groups in (0, 1, 7, 64):
+                for xt in (mx4.BF16, mx4.F32):
+                    ctx.gemv_config(xdev[xt].ptr, xt, w, y.ptr, team, rows, groups)
+                    got = y.download(np.float32).reshape(1, n)
+                    assert_close(got, ref, f"team={team} rows={rows} groups={groups} xt={xt}")
+                    tried += 1
+    assert tried >= 16
+
+
+def test_group_equals_individual(mx4, ctx, oracle):
+    """q|k|v and gate|up as one launch give bitwise the same rows as separate launches."""
+    k = 4096
+    shapes = [4096, 1024, 1024]
+    ws = [ctx.synth_weight(200 + i, n, k, 0.02) for i, n in enumerate(shapes)]
+    xb = ctx.to_device(oracle.synth_bf16(5, 1.0, k))
+    ys = [ctx.buffer(n * 4) for n in shapes]
+    ctx.matmul_group(xb.ptr, mx4.BF16, 1, ws, [y.ptr for y in ys])
+    grouped = [y.download(np.float32) for y in ys]
+    for w, y, g in zip(ws, ys, grouped):
+        ctx.matmul_ptr(xb.ptr, mx4.BF16, 1, w, y.ptr)
+        assert np.array_equal(f32_bits(y.download(np.float32)), f32_bits(g))
+    with pytest.raises(mx4.Mx4Error, match="share their width"):
+        other = ctx.synth_weight(9, 64, 2048, 0.02)
+        ctx.matmul_group(xb.ptr, mx4.BF16, 1, [ws[0], other], [ys[0].ptr, ys[1].ptr])
+
+
+def test_extreme_scales_take_the_exact_path(mx4, ctx, oracle):
+    """Scale bytes 0, 1 (subnormal weights) and 253, 254 (inf weights) are outside
+    the converter-folding range; AUTO routes them to the exact generic kernel."""
+    rng = np.random.default_rng(8)
+    n, k = 64, 4096
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(118, 130, (n, k // 32), dtype=np.uint8)
+    scales[0:8, 3] = 0
+    scales[8:16, 5] = 1
+    x = oracle.bf16_to_f32(oracle.synth_bf16(4, 1.0, k)).reshape(1, k)
+    w = ctx.upload_weight(packed, scales, n, k)
+    ref = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
+    y = run_matmul(mx4, ctx, x, w, mx4.PATH_AUTO, mx4.BF16)
+    assert_close(y, ref, "subnormal scales")
+    with pytest.raises(mx4.Mx4Error, match="2..252"):
+        run_matmul(mx4, ctx, x, w, mx4.PATH_GEMV, mx4.BF16)
+    # a row made only of scale-0 blocks: every weight is subnormal, exact products
+    scales2 = scales.copy()
+    scales2[20, :] = 0
+    w2 = ctx.upload_weight(packed, scales2, n, k)
+    y2 = run_matmul(mx4, ctx, x, w2, mx4.PATH_AUTO, mx4.F32)
+    ref2 = oracle.matmul(x, packed.reshape(-1), scales2.reshape(-1))
+    assert abs(float(y2[0, 20]) - float(ref2[0, 20])) <= 1e-3 * abs(float(ref2[0, 20])) + 1e-44
+    # overflowing weights: inf and NaN patterns match the oracle's
+    scales3 = scales.copy()
+    scales3[30, 0] = 254
+    scales3[31, 0] = 253
+    w3 = ctx.upload_weight(packed, scales3, n, k)
+    y3 = run_matmul(mx4, ctx, x, w3, mx4.PATH_AUTO, mx4.F32)
+    ref3 = oracle.matmul(x, packed.reshape(-1), scales3.reshape(-1))
+    assert np.array_equal(np.isnan(y3), np.isnan(ref3)) and np.array_equal(np.isinf(y3), np.isinf(ref3))
+    fin = np.isfinite(ref3)
+    assert_close(y3[fin].reshape(1, -1), ref3[fin].reshape(1, -1), "finite rows next to inf rows")
