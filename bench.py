@@ -110,6 +110,42 @@ def time_shapes(ctx, weights, xs, ys, reps: int = 3):
     return table
 
 
+def time_skinny(ctx, weights, ms=(1, 2, 4, 8, 16), reps: int = 3):
+    """Speculative-verify shapes: each 8B projection at M token rows (exact path:
+    GEMV for M = 1, skinny bf16-MFMA kernel above), 36 cold copies in a recorded
+    pass, per-call latency and effective GB/s (bytes with M*K*2 + M*N*4)."""
+    by = {}
+    for (nm, n, k, w) in weights:
+        by.setdefault(nm, []).append((n, k, w))
+    out = {}
+    for name, n, k in LAYER + [LM_HEAD]:
+        ws = [w for (_, _, w) in by[name]]
+        row = {}
+        for m in ms:
+            xb = ctx.buffer(m * k * 2)
+            ctx.synth_bf16(2, 1.0, m * k, xb)
+            yb = ctx.buffer(m * n * 4)
+
+            def enqueue():
+                for w in ws:
+                    ctx.matmul_ptr(xb.ptr, mx4hip.BF16, m, w, yb.ptr)
+
+            p = ctx.record(enqueue)
+            p.launch()
+            best = None
+            for _ in range(reps):
+                ctx.synchronize()
+                ctx.timer_begin()
+                p.launch()
+                t = ctx.timer_end() / len(ws)
+                best = t if best is None else min(best, t)
+            p.release()
+            b = gemv_bytes(m, n, k)
+            row[f"M{m}"] = {"us": round(best * 1e3, 3), "GBps": round(b / (best * 1e-3) / 1e9, 1)}
+        out[name] = row
+    return out
+
+
 def cpu_baseline(ctx, weights, x_host: dict, layers: int = 3) -> dict:
     """The oracle on the host: one thread, `layers` layers + the matching share of lm_head."""
     from oracle import mx4_oracle as oracle
@@ -144,6 +180,7 @@ def main() -> int:
     ap.add_argument("--separate", action="store_true", help="one launch per projection (253) instead of q|k|v and gate|up groups")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-shapes", action="store_true")
+    ap.add_argument("--no-skinny", action="store_true")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -220,6 +257,10 @@ def main() -> int:
     if not args.no_shapes:
         log("per-shape timing")
         extra["shapes"] = time_shapes(ctx, weights, xs, ys)
+
+    if not args.no_skinny:
+        log("skinny (speculative verify) timing")
+        extra["skinny"] = time_skinny(ctx, weights)
 
     cpu = None
     if not args.no_cpu_baseline:

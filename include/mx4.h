@@ -54,7 +54,7 @@ typedef enum mx4_dtype { MX4_F32 = 0, MX4_BF16 = 1 } mx4_dtype;
 typedef enum mx4_path {
     MX4_PATH_AUTO = 0,
     MX4_PATH_GEMV = 1,     /* M == 1 decode GEMV (no MFMA) */
-    MX4_PATH_SKINNY = 2,   /* exact skinny kernel, 2 <= M <= 16 */
+    MX4_PATH_SKINNY = 2,   /* exact skinny kernel on bf16 MFMA, M <= 32, K in {2,4,6,8,12}*1024 */
     MX4_PATH_GENERIC = 3,  /* exact fallback for any M and K % 32 == 0 */
     MX4_PATH_PREFILL = 4   /* block-scaled MFMA on requantized activations */
 } mx4_path;
@@ -140,7 +140,7 @@ mx4_status mx4_weight_info(const mx4_weight *w, uint32_t *rows, uint32_t *cols,
 /* GpuModel::matmul (engine/src/gpu.rs:469-515): y_dev[m][rows] =
  * x_dev[m][cols] . W^T, enqueued on the context stream, exact arithmetic
  * (f32 accumulation of exact products). AUTO picks GEMV for m == 1, the exact
- * skinny kernel for 2 <= m <= 16 and the exact generic kernel beyond. */
+ * skinny kernel for 2 <= m <= 32 and the exact generic kernel beyond. */
 mx4_status mx4_matmul(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m,
                       const mx4_weight *w, float *y_dev);
 /* The same with an explicit kernel family (MX4_PATH_PREFILL is not exact:

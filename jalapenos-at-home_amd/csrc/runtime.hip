@@ -164,7 +164,7 @@ mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
     if (path == MX4_PATH_AUTO) {
         if (m == 1 && mx4::gemv_m1_supported(w->cols) && scales_foldable(w))
             path = MX4_PATH_GEMV;
-        else if (m >= 2 && m <= 16 && mx4::skinny_supported(m, w->cols) && scales_foldable(w))
+        else if (m >= 2 && mx4::skinny_supported(m, w->cols) && scales_foldable(w))
             path = MX4_PATH_SKINNY;
         else
             path = MX4_PATH_GENERIC;
@@ -180,7 +180,7 @@ mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
             break;
         case MX4_PATH_SKINNY:
             if (!mx4::skinny_supported(m, w->cols))
-                return fail(MX4_ERR_UNSUPPORTED, "skinny path needs 1 <= m <= 16 and K %% 128 == 0");
+                return fail(MX4_ERR_UNSUPPORTED, "skinny path needs 1 <= m <= 32 and K in {2048, 4096, 6144, 8192, 12288}");
             if (!scales_foldable(w))
                 return fail(MX4_ERR_UNSUPPORTED, "skinny path folds scales into bf16; scale bytes outside 2..252 need GENERIC");
             e = mx4::launch_skinny(a, ctx->cus);

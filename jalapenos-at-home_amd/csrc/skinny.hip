@@ -1,10 +1,251 @@
-// skinny.hip -- exact skinny kernel (2 <= M <= 16) on bf16 MFMA.
+// skinny.hip -- exact skinny kernel for a few tokens (speculative verify,
+// 2 <= M <= 32): y[m, r] = sum_k x[m, k] * w(r, k) on bf16 matrix cores.
+//
+// The reference runs these shapes on project_rows{4,8,12}_mxfp4
+// (engine/src/gpu.metal:277-322, dispatch engine/src/gpu.rs:484-509): FP32
+// FMA, one weight read per chunk of 4/8/12 tokens. On gfx950 a VALU dot2 per
+// token would be VALU-bound from M = 4 on, so the multiply-accumulate moves to
+// V_MFMA_F32_16X16X32_BF16 while the weights stay 4-bit in HBM:
+//  * each lane converts its 16 packed bytes (one MX block of one weight row)
+//    with the hardware E2M1 converter, the E8M0 scale folded in -- exact in
+//    bf16 for scale bytes 2..252, which the dispatcher guarantees;
+//  * MFMA operand B is 16 weight rows x 32 K, operand A 16 tokens x 32 K.
+//    Within a 128-element K chunk, lane group g (= lane / 16) holds block
+//    4c + g and MFMA t takes elements [8t, 8t + 8) of it, for A and B alike;
+//    the contraction is over K, so any K order shared by A and B is exact;
+//  * bf16 activations are exact operands. f32 activations are split into
+//    three bf16 terms hi + mid + lo (24 significant bits), three MFMAs each;
+//  * a persistent workgroup of TW waves splits K (wave w takes chunks w,
+//    w + TW, ...; its activation fragments stay in registers for the whole
+//    kernel), walks 16-row weight tiles with the next tile prefetched, and
+//    reduces its TW partial tiles through LDS;
+//  * loads go through buffer resources: token rows >= M and weight rows >= N
+//    read as zeros without touching memory.
 #include "mx4_device.h"
 #include "mx4_kernels.h"
 
 namespace mx4 {
 
-bool skinny_supported(uint32_t, uint32_t) { return false; }
-hipError_t launch_skinny(const GemvArgs&, int) { return hipErrorNotSupported; }
+namespace {
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+constexpr int kNT = 2;  // streamed once: do not keep in the caches
+
+// Eight bf16 weights: elements [8t, 8t + 8) of a lane's block (dword t of
+// its 16 packed bytes), scale folded into the converter.
+__device__ __forceinline__ bf16x8 weights8(uint32_t word, float sc) {
+    bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 0);
+    bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 1);
+    bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 2);
+    bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 3);
+    bf16x8 r;
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+    return r;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Wait states after an MFMA chain whose accumulators are read next. The
+// compiler can place a v_accvgpr_read of an XDL result right after a branch
+// without the wait states the result needs (seen with ROCm 7.2 on gfx950: the
+// last two MFMAs of a chain were lost), so the chain is drained explicitly;
+// 24 wait states cover the longest 16x16 XDL op.
+__device__ __forceinline__ void mfma_drain() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// f32 -> three bf16 terms with x = hi + mid + lo to within f32 rounding.
+__device__ __forceinline__ void split3(const f32x4 a, const f32x4 b, bf16x8& hi, bf16x8& mid, bf16x8& lo) {
+    float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        __bf16 h = (__bf16)v[e];
+        float r1 = v[e] - (float)h;
+        __bf16 m = (__bf16)r1;
+        float r2 = r1 - (float)m;
+        hi[e] = h;
+        mid[e] = m;
+        lo[e] = (__bf16)r2;
+    }
+}
+
+// Persistent kernel, K = 128 * U * NU * TW exactly. Wave w of a workgroup
+// owns the K chunks w, w + TW, w + 2 TW, ... of every weight row. The
+// workgroup walks 16-row weight tiles (tile, tile + grid, ...); each tile is
+// NU work units of U chunks per wave. A unit's weights (16 rows x U blocks per
+// lane group), scales and activation fragments are loaded one unit ahead of the
+// MFMAs. After a tile's last unit the TW partial 16x16 tiles are summed
+// through LDS (double-buffered: one barrier per tile).
+template <bool XBF16, int MT, int U, int NU, int TW>
+__global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restrict__ packed,
+                                                         const uint8_t* __restrict__ scales,
+                                                         const void* __restrict__ x, float* __restrict__ y,
+                                                         uint32_t m, uint32_t n) {
+    constexpr uint32_t k = 128 * U * NU * TW;
+    constexpr uint32_t row_bytes = k / 2, nblk = k / 32;
+    constexpr int XQ = XBF16 ? 4 : 8;  // 16-byte activation loads per chunk and token tile
+    // the wave index is uniform; saying so keeps chunk indices and buffer
+    // resources in scalar registers (otherwise every load becomes a waterfall loop)
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t col = lane % 16, g = lane / 16;
+    const uint32_t tiles = (n + 15) / 16;
+    const __amdgpu_buffer_rsrc_t empty = rsrc(packed, 0);
+    const __amdgpu_buffer_rsrc_t xr = rsrc(x, m * k * (XBF16 ? 2u : 4u));
+
+    struct Unit {
+        u32x4 w[U];
+        uint32_t s[U];
+        u32x4 xa[MT][U][XQ];
+    };
+    auto load = [&](uint32_t tile, uint32_t part, Unit& out) {
+        const bool valid = tile < tiles;
+        const uint32_t row0 = valid ? tile * 16 : 0;
+        const uint32_t rows = valid ? (n - row0 < 16u ? n - row0 : 16u) : 0;
+        const __amdgpu_buffer_rsrc_t wr = valid ? rsrc(packed + (size_t)row0 * row_bytes, rows * row_bytes) : empty;
+        const __amdgpu_buffer_rsrc_t sr = valid ? rsrc(scales + (size_t)row0 * nblk, rows * nblk) : empty;
+        const __amdgpu_buffer_rsrc_t xq = valid ? xr : empty;
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const uint32_t blk = 4 * (wave + (part * U + q) * TW) + g;
+            out.w[q] = __builtin_amdgcn_raw_buffer_load_b128(wr, col * row_bytes + 16 * blk, 0, kNT);
+            out.s[q] = __builtin_amdgcn_raw_buffer_load_b8(sr, col * nblk + blk, 0, 0);
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+                const uint32_t off = ((16 * j + col) * k + 32 * blk) * (XBF16 ? 2u : 4u);
+#pragma unroll
+                for (int c = 0; c < XQ; ++c) out.xa[j][q][c] = __builtin_amdgcn_raw_buffer_load_b128(xq, off + 16 * c, 0, 0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    f32x4 acc[MT];
+    auto zero = [&]() {
+#pragma unroll
+        for (int j = 0; j < MT; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    };
+    auto compute = [&](const Unit& cur) {
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const float sc = __uint_as_float(cur.s[q] << 23);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bf16x8 b = weights8(cur.w[q][t], sc);
+#pragma unroll
+                for (int j = 0; j < MT; ++j) {
+                    if constexpr (XBF16) {
+                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.xa[j][q][t]), b, acc[j], 0, 0, 0);
+                    } else {
+                        bf16x8 hi, mid, lo;
+                        split3(__builtin_bit_cast(f32x4, cur.xa[j][q][2 * t]),
+                               __builtin_bit_cast(f32x4, cur.xa[j][q][2 * t + 1]), hi, mid, lo);
+                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, acc[j], 0, 0, 0);
+                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b, acc[j], 0, 0, 0);
+                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, acc[j], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        mfma_drain();
+    };
+
+    __shared__ f32x4 red[2][TW][MT][64];
+    uint32_t parity = 0;
+    auto reduce_write = [&](uint32_t tile) {
+#pragma unroll
+        for (int j = 0; j < MT; ++j) red[parity][wave][j][lane] = acc[j];
+        __syncthreads();
+        if (wave < (uint32_t)MT) {
+            const uint32_t j = wave;
+            f32x4 sum = red[parity][0][j][lane];
+#pragma unroll
+            for (int w = 1; w < TW; ++w) sum += red[parity][w][j][lane];
+            const uint32_t row = tile * 16 + col;
+            if (row < n) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t tok = 16 * j + 4 * g + r;
+                    if (tok < m) y[(size_t)tok * n + row] = sum[r];
+                }
+            }
+        }
+        parity ^= 1;
+        zero();
+    };
+
+    uint32_t tile = blockIdx.x, part = 0;
+    if (tile >= tiles) return;
+    zero();
+    Unit ua, ub;
+    load(tile, part, ua);
+    for (;;) {
+        uint32_t nt = tile, np = part + 1;
+        if (np == (uint32_t)NU) { np = 0; nt = tile + gridDim.x; }
+        load(nt, np, ub);
+        compute(ua);
+        if (part == (uint32_t)NU - 1) reduce_write(tile);
+        if (nt >= tiles) break;
+        tile = nt;
+        part = np;
+        nt = tile;
+        np = part + 1;
+        if (np == (uint32_t)NU) { np = 0; nt = tile + gridDim.x; }
+        load(nt, np, ua);
+        compute(ub);
+        if (part == (uint32_t)NU - 1) reduce_write(tile);
+        if (nt >= tiles) break;
+        tile = nt;
+        part = np;
+    }
+}
+
+template <bool XBF16, int MT, int U, int NU, int TW>
+hipError_t go(const GemvArgs& a, int cus) {
+    const uint32_t tiles = (a.n + 15) / 16;
+    uint32_t grid = (uint32_t)cus * 2u;  // two workgroups of TW waves per CU
+    if (grid > tiles) grid = tiles;
+    const uint32_t per = (tiles + grid - 1) / grid;
+    grid = (tiles + per - 1) / per;
+    hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW>), dim3(grid), dim3(64 * TW), 0, a.stream, a.packed,
+                       a.scales, a.x, a.y, a.m, a.n);
+    return hipGetLastError();
+}
+
+// Chunks per unit: two for bf16 activations and one token tile, one otherwise,
+// so that two units (the one computed and the one in flight) fit the registers.
+template <bool XBF16, int MT>
+hipError_t go_k(const GemvArgs& a, int cus) {
+    constexpr int U = (XBF16 && MT == 1) ? 2 : 1;
+    constexpr int TW = 8;
+    switch (a.k) {
+        case 2048: return go<XBF16, MT, U, 16 / (U * 4), 4>(a, cus);
+        case 4096: return go<XBF16, MT, U, 4 / U, TW>(a, cus);
+        case 6144: return go<XBF16, MT, U, 6 / U, TW>(a, cus);
+        case 8192: return go<XBF16, MT, U, 8 / U, TW>(a, cus);
+        case 12288: return go<XBF16, MT, U, 12 / U, TW>(a, cus);
+        default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace
+
+bool skinny_supported(uint32_t m, uint32_t k) {
+    // the Qwen3 widths; M within two 16-token tiles
+    const bool kk = k == 2048 || k == 4096 || k == 6144 || k == 8192 || k == 12288;
+    return m >= 1 && m <= 32 && kk;
+}
+
+hipError_t launch_skinny(const GemvArgs& a, int cus) {
+    if (!skinny_supported(a.m, a.k)) return hipErrorNotSupported;
+    if (a.m <= 16) return a.x_bf16 ? go_k<true, 1>(a, cus) : go_k<false, 1>(a, cus);
+    return a.x_bf16 ? go_k<true, 2>(a, cus) : go_k<false, 2>(a, cus);
+}
 
 }  // namespace mx4

@@ -440,3 +440,50 @@ def test_extreme_scales_take_the_exact_path(mx4, ctx, oracle):
     assert np.array_equal(np.isnan(y3), np.isnan(ref3)) and np.array_equal(np.isinf(y3), np.isinf(ref3))
     fin = np.isfinite(ref3)
     assert_close(y3[fin].reshape(1, -1), ref3[fin].reshape(1, -1), "finite rows next to inf rows")
+
+
+# ------------------------------------------------------------------ skinny (speculative verify)
+
+@pytest.mark.parametrize("name", ["k", "q", "gate", "down"])
+def test_skinny_8b_shapes(mx4, ctx, oracle, name):
+    """M = 1..32 token rows (draft length + 1 and beyond) on the exact skinny kernel,
+    bf16 and f32 activations, sampled weight rows against the oracle."""
+    n, k = QWEN8[name]
+    say(f"skinny 8B {name} {k}->{n}")
+    rng = np.random.default_rng(11)
+    w = ctx.synth_weight(300, n, k, 0.02)
+    packed, scales = ctx.download_weight(w)
+    rows = _sample_rows(n, 160, rng)
+    for m in (1, 2, 3, 4, 5, 8, 9, 12, 16, 17, 24, 32):
+        xbits = oracle.synth_bf16(40 + m, 1.0, m * k)
+        x = oracle.bf16_to_f32(xbits).reshape(m, k)
+        ref = np.concatenate([oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), int(r), int(r) + 1)
+                              for r in rows], axis=1)
+        for xtype in (mx4.BF16, mx4.F32):
+            xin = x if xtype == mx4.BF16 else (x + rng.standard_normal(x.shape).astype(np.float32) * 1e-3)
+            refx = ref if xtype == mx4.BF16 else np.concatenate(
+                [oracle.matmul_rows(xin, packed.reshape(-1), scales.reshape(-1), int(r), int(r) + 1) for r in rows], axis=1)
+            path = mx4.PATH_SKINNY if m == 1 else mx4.PATH_AUTO
+            y = run_matmul(mx4, ctx, xin, w, path, xtype)
+            assert_close(y[:, rows], refx, f"skinny {name} m={m} xtype={xtype}")
+
+
+def test_skinny_ragged_rows_and_identity(mx4, ctx, oracle):
+    """Weight rows not a multiple of the 16-row tile, and an exact identity KAT:
+    one-hot activations return the decoded weights bit for bit."""
+    rng = np.random.default_rng(12)
+    n, k = 37, 2048
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(110, 140, (n, k // 32), dtype=np.uint8)
+    w = ctx.upload_weight(packed, scales, n, k)
+    m = 16
+    x = np.zeros((m, k), np.float32)
+    cols = rng.choice(k, m, replace=False)
+    x[np.arange(m), cols] = 1.0
+    for xtype in (mx4.BF16, mx4.F32):
+        y = run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, xtype)
+        dec = oracle.dequantize(packed, scales)
+        assert np.array_equal(y, dec[:, cols].T), xtype
+    x2 = rng.standard_normal((5, k)).astype(np.float32)
+    ref = oracle.matmul(x2, packed.reshape(-1), scales.reshape(-1))
+    assert_close(run_matmul(mx4, ctx, x2, w, mx4.PATH_AUTO, mx4.F32), ref, "ragged f32")
