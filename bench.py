@@ -146,6 +146,51 @@ def time_skinny(ctx, weights, ms=(1, 2, 4, 8, 16), reps: int = 3):
     return out
 
 
+def time_prefill(ctx, weights, m: int = 512, reps: int = 5):
+    """Prefill on block-scaled MFMA: each 8B q/o/gate/up/down shape at M = 512,
+    activations bf16 N(0, 1) requantized per 32 along K (MXFP4, and MX-FP8).
+    Reports the GEMM kernel alone and requant + GEMM, as TFLOP/s of 2*M*N*K."""
+    by = {}
+    for (nm, n, k, w) in weights:
+        by.setdefault(nm, (n, k, w))
+    peaks = {"mxfp4": 10.1e15, "mxfp8": 5.0e15}
+    ctx.reserve_prefill(m, max(k for (_, k, _) in by.values()))
+    out = {}
+    for name in ("q", "o", "gate", "up", "down"):
+        n, k, w = by[name]
+        xb = ctx.buffer(m * k * 2)
+        ctx.synth_bf16(3, 1.0, m * k, xb)
+        yb = ctx.buffer(m * n * 4)
+        row = {}
+        for act, code in (("mxfp4", mx4hip.ACT_MXFP4), ("mxfp8", mx4hip.ACT_MXFP8)):
+            qbytes = m * k // 2 if act == "mxfp4" else m * k
+            xq, xs = ctx.buffer(qbytes), ctx.buffer(m * k // 32)
+            if act == "mxfp4":
+                ctx.quantize(xb, mx4hip.BF16, m, k, xq, xs)
+            else:
+                ctx.quantize_fp8(xb, mx4hip.BF16, m, k, xq, xs)
+            flops = 2.0 * m * n * k
+            res = {}
+            for label, fn in (("gemm", lambda: ctx.matmul_mx(xq, xs, code, m, w, yb)),
+                              ("requant+gemm", lambda: ctx.matmul_prefill(xb, mx4hip.BF16, m, w, code, yb))):
+                p = ctx.record(lambda: [fn() for _ in range(8)])
+                p.launch()
+                best = None
+                for _ in range(reps):
+                    ctx.synchronize()
+                    ctx.timer_begin()
+                    p.launch()
+                    t = ctx.timer_end() / 8
+                    best = t if best is None else min(best, t)
+                p.release()
+                tf = flops / (best * 1e-3)
+                res[label] = {"us": round(best * 1e3, 2), "TFLOPs": round(tf / 1e12, 1),
+                              "frac": round(tf / peaks[act], 4)}
+            row[act] = res
+        out[name] = {"m": m, "n": n, "k": k, **row}
+    return out
+
+
 def cpu_baseline(ctx, weights, x_host: dict, layers: int = 3) -> dict:
     """The oracle on the host: one thread, `layers` layers + the matching share of lm_head."""
     from oracle import mx4_oracle as oracle
@@ -181,6 +226,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-shapes", action="store_true")
     ap.add_argument("--no-skinny", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -261,6 +307,10 @@ def main() -> int:
     if not args.no_skinny:
         log("skinny (speculative verify) timing")
         extra["skinny"] = time_skinny(ctx, weights)
+
+    if not args.no_prefill:
+        log("prefill (M=512, block-scaled MFMA) timing")
+        extra["prefill"] = time_prefill(ctx, weights)
 
     cpu = None
     if not args.no_cpu_baseline:

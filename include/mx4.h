@@ -195,6 +195,17 @@ mx4_status mx4_pass_end(mx4_context *ctx, mx4_pass **out);
 mx4_status mx4_pass_launch(mx4_context *ctx, const mx4_pass *pass);
 void mx4_pass_release(mx4_pass *pass);
 
+/* Reserve the requantization workspace of mx4_matmul_prefill for up to max_m
+ * rows of max_cols (either activation format), so later calls -- including
+ * calls recorded into a pass, where allocation is impossible -- allocate nothing. */
+mx4_status mx4_reserve_prefill(mx4_context *ctx, uint32_t max_m, uint32_t max_cols);
+
+/* The block-scaled MFMA product for activations that are already requantized
+ * (xq_dev: MXFP4 packed [m][cols/2] or E4M3 [m][cols]; xs_dev: E8M0 [m][cols/32],
+ * as mx4_quantize / mx4_quantize_fp8 produce them). */
+mx4_status mx4_matmul_mx(mx4_context *ctx, const uint8_t *xq_dev, const uint8_t *xs_dev,
+                         mx4_act_format act, uint32_t m, const mx4_weight *w, float *y_dev);
+
 /* engine/src/mxfp4.rs:35-49 on device: out_dev[rows*cols] f32, bit-exact. */
 mx4_status mx4_dequantize(mx4_context *ctx, const mx4_weight *w, float *out_dev);
 /* python/quantize_mxfp4.py:18-39 on device, bit-exact: in_dev [rows][cols]

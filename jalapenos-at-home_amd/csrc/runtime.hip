@@ -124,6 +124,11 @@ bool is_gfx950(int dev) {
 
 mx4_status ensure_buffer(mx4_context* ctx, void** buf, uint64_t* cap, uint64_t need) {
     if (need <= *cap) return MX4_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return fail(MX4_ERR_NO_MEMORY,
+                    "workspace of %llu bytes needed while recording a pass; reserve it first (mx4_reserve_prefill)",
+                    (unsigned long long)need);
     if (*buf) {
         HIP_TRY(hipStreamSynchronize(ctx->stream));
         HIP_TRY(hipFree(*buf));
@@ -138,6 +143,12 @@ mx4_status ensure_buffer(mx4_context* ctx, void** buf, uint64_t* cap, uint64_t n
     }
     *cap = size;
     return MX4_OK;
+}
+
+// requantized activations (FP4 or FP8 codes, 256-byte aligned) followed by their scales
+uint64_t prefill_workspace_bytes(uint64_t m, uint64_t cols, bool fp8) {
+    const uint64_t qbytes = m * cols / (fp8 ? 1 : 2);
+    return ((qbytes + 255) & ~255ull) + m * cols / 32;
 }
 
 mx4_status check_matmul_args(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
@@ -526,13 +537,12 @@ mx4_status mx4_matmul_prefill(mx4_context* ctx, const void* x, mx4_dtype xt, uin
     if (st != MX4_OK) return st;
     if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
     if (!mx4::prefill_supported(m, w->rows, w->cols))
-        return fail(MX4_ERR_UNSUPPORTED, "prefill path needs K %% 128 == 0 and N %% 64 == 0");
+        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
     DeviceGuard g(ctx->device);
     const bool fp8 = act == MX4_ACT_MXFP8;
     const uint64_t qbytes = (uint64_t)m * w->cols / (fp8 ? 1 : 2);
     const uint64_t qoff = (qbytes + 255) & ~255ull;
-    const uint64_t sbytes = (uint64_t)m * w->cols / 32;
-    st = ensure_buffer(ctx, &ctx->work, &ctx->work_cap, qoff + sbytes);
+    st = ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(m, w->cols, fp8));
     if (st != MX4_OK) return st;
     uint8_t* xq = static_cast<uint8_t*>(ctx->work);
     uint8_t* xs = xq + qoff;
@@ -603,6 +613,27 @@ void mx4_pass_release(mx4_pass* pass) {
     (void)hipGraphExecDestroy(pass->exec);
     (void)hipGraphDestroy(pass->graph);
     delete pass;
+}
+
+mx4_status mx4_reserve_prefill(mx4_context* ctx, uint32_t max_m, uint32_t max_cols) {
+    if (!ctx) return fail(MX4_ERR_ARGUMENT, "null context");
+    DeviceGuard g(ctx->device);
+    return ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(max_m, max_cols, true));
+}
+
+mx4_status mx4_matmul_mx(mx4_context* ctx, const uint8_t* xq, const uint8_t* xs, mx4_act_format act, uint32_t m,
+                         const mx4_weight* w, float* y) {
+    if (!ctx || !xq || !xs || !w || !y) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
+    if (m == 0) return fail(MX4_ERR_ARGUMENT, "m must be at least 1");
+    if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
+    if (!mx4::prefill_supported(m, w->rows, w->cols))
+        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
+    DeviceGuard g(ctx->device);
+    mx4::PrefillArgs a{w->packed, w->scales, xq, xs, y, m, w->rows, w->cols, act == MX4_ACT_MXFP8, ctx->stream};
+    hipError_t e = mx4::launch_prefill(a, ctx->cus);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
 }
 
 mx4_status mx4_dequantize(mx4_context* ctx, const mx4_weight* w, float* out) {

@@ -63,6 +63,8 @@ SIGNATURES = {
     "mx4_matmul_group": (_int, [_vp, _vp, _int, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32]),
     "mx4_gemv_config": (_int, [_vp, _vp, _int, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32, _int, _int, _u32]),
     "mx4_matmul_batch": (_int, [_vp, _vp, _u32]),
+    "mx4_matmul_mx": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
+    "mx4_reserve_prefill": (_int, [_vp, _u32, _u32]),
     "mx4_pass_begin": (_int, [_vp]),
     "mx4_pass_end": (_int, [_vp, ctypes.POINTER(_vp)]),
     "mx4_pass_launch": (_int, [_vp, _vp]),
@@ -318,6 +320,12 @@ class Context:
             st = lib().mx4_pass_end(self.handle, ctypes.byref(h))
         check(st)
         return Pass(self, h.value)
+
+    def reserve_prefill(self, max_m: int, max_cols: int) -> None:
+        check(lib().mx4_reserve_prefill(self.handle, max_m, max_cols))
+
+    def matmul_mx(self, xq: DeviceBuffer, xs: DeviceBuffer, act: int, m: int, w: Weight, y: DeviceBuffer) -> None:
+        check(lib().mx4_matmul_mx(self.handle, xq.ptr, xs.ptr, act, m, w.handle, y.ptr))
 
     def dequantize(self, w: Weight, out: DeviceBuffer) -> None:
         check(lib().mx4_dequantize(self.handle, w.handle, out.ptr))

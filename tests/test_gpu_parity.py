@@ -487,3 +487,78 @@ def test_skinny_ragged_rows_and_identity(mx4, ctx, oracle):
     x2 = rng.standard_normal((5, k)).astype(np.float32)
     ref = oracle.matmul(x2, packed.reshape(-1), scales.reshape(-1))
     assert_close(run_matmul(mx4, ctx, x2, w, mx4.PATH_AUTO, mx4.F32), ref, "ragged f32")
+
+
+# ------------------------------------------------------------------ prefill (block-scaled MFMA)
+
+def _prefill_ref(oracle, x, packed, scales, act):
+    """The oracle on requantized activations: dequant(requant(x)) . dequant(W)^T."""
+    if act == "mxfp4":
+        xq, xs = oracle.quantize(x)
+        xd = oracle.dequantize(xq, xs)
+    else:
+        xq, xs = oracle.quantize_fp8(x)
+        xd = oracle.dequantize_fp8(xq, xs)
+    return oracle.matmul(xd, packed.reshape(-1), scales.reshape(-1)), xd
+
+
+def _run_prefill(mx4, ctx, x, w, act, xtype):
+    m, k = x.shape
+    if xtype == mx4.BF16:
+        xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+    else:
+        xb = ctx.to_device(np.ascontiguousarray(x, np.float32))
+    yb = ctx.buffer(m * w.rows * 4)
+    ctx.matmul_prefill(xb, xtype, m, w, mx4.ACT_MXFP4 if act == "mxfp4" else mx4.ACT_MXFP8, yb)
+    return yb.download(np.float32).reshape(m, w.rows)
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+def test_prefill_identity_is_exact(mx4, ctx, oracle, act):
+    """One-hot activations requantize exactly (1.0 -> code 4.0 at scale 2^-2, or
+    E4M3 1.0), so the block-scaled MFMA must return the decoded weights bit for bit:
+    pins the matrix core's E2M1 decode, the per-lane E8M0 scales and the output layout."""
+    rng = np.random.default_rng(31)
+    n, k, m = 64, 512, 64
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(100, 150, (n, k // 32), dtype=np.uint8)
+    w = ctx.upload_weight(packed, scales, n, k)
+    cols = rng.choice(k, m, replace=False)
+    x = np.zeros((m, k), np.float32)
+    x[np.arange(m), cols] = 1.0
+    y = _run_prefill(mx4, ctx, x, w, act, mx4.F32)
+    dec = oracle.dequantize(packed, scales)
+    assert np.array_equal(y, dec[:, cols].T)
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+@pytest.mark.parametrize("m,n,k", [(1, 32, 256), (7, 200, 512), (64, 128, 1024), (130, 96, 256), (256, 256, 4096)])
+def test_prefill_matches_oracle_on_requantized_x(mx4, ctx, oracle, act, m, n, k):
+    rng = np.random.default_rng(m * 7 + n)
+    w = ctx.synth_weight(50 + m, n, k, 0.02)
+    packed, scales = ctx.download_weight(w)
+    x = oracle.bf16_to_f32(oracle.synth_bf16(60 + m, 1.0, m * k)).reshape(m, k)
+    ref, _ = _prefill_ref(oracle, x, packed, scales, act)
+    for xtype in (mx4.BF16, mx4.F32):
+        y = _run_prefill(mx4, ctx, x, w, act, xtype)
+        assert_close(y, ref, f"prefill {act} m={m} n={n} k={k} xtype={xtype}")
+
+
+def test_prefill_8b_shapes_sampled(mx4, ctx, oracle):
+    """M = 512 at the Qwen3-8B q and down shapes, sampled rows/cols against the oracle."""
+    rng = np.random.default_rng(77)
+    for name in ("q", "down"):
+        n, k = QWEN8[name]
+        say(f"prefill 8B {name} 512 x {k} -> {n}")
+        m = 512
+        w = ctx.synth_weight(400, n, k, 0.02)
+        packed, scales = ctx.download_weight(w)
+        x = oracle.bf16_to_f32(oracle.synth_bf16(401, 1.0, m * k)).reshape(m, k)
+        rows = rng.choice(m, 24, replace=False)
+        cols = _sample_rows(n, 96, rng)
+        xq, xs = oracle.quantize(x[rows])
+        xd = oracle.dequantize(xq, xs)
+        ref = np.concatenate([oracle.matmul_rows(xd, packed.reshape(-1), scales.reshape(-1), int(c), int(c) + 1)
+                              for c in cols], axis=1)
+        y = _run_prefill(mx4, ctx, x, w, "mxfp4", mx4.BF16)
+        assert_close(y[np.ix_(rows, cols)], ref, f"prefill 8B {name}")
