@@ -227,6 +227,8 @@ def main() -> int:
     ap.add_argument("--no-shapes", action="store_true")
     ap.add_argument("--no-skinny", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--profile-traffic", action="store_true",
+                    help="for counter runs: 2 eager grouped steps, then a 1 GiB device copy as the byte calibration")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -275,6 +277,18 @@ def main() -> int:
     else:
         enqueue = enqueue_grouped
         launches = LAYERS * 4 + 1
+    if args.profile_traffic:
+        for _ in range(2):
+            enqueue()
+        ctx.synchronize()
+        src, dst = ctx.buffer(1 << 30), ctx.buffer(1 << 30)
+        mx4hip.check(mx4hip.lib().mx4_copy(ctx.handle, dst.ptr, src.ptr, 1 << 30))
+        ctx.synchronize()
+        print(json.dumps({"profile_traffic": True, "steps": 2, "launches_per_step": launches,
+                          "bytes_per_step": step_bytes, "calibration_copy_bytes": 1 << 30}), flush=True)
+        ctx.close()
+        return 0
+
     if args.eager:
         step = enqueue
         launch = f"eager, {launches} launches per step"
@@ -317,10 +331,13 @@ def main() -> int:
         log("cpu baseline (oracle, 1 thread)")
         cpu = cpu_baseline(ctx, weights, x_host)
 
+    # HBM bytes per step from the committed FETCH_SIZE + WRITE_SIZE counter runs
     traffic = None
-    tf = ROOT / "profiles" / "traffic_gemv_qwen3_8b_m1_step.json"
-    if tf.exists():
-        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_step")
+    tf = ROOT / "profiles" / "gemv_qwen3_8b_m1_step_traffic.md"
+    if tf.exists() and not args.separate:
+        for line in tf.read_text().splitlines():
+            if line.startswith("hbm_bytes_per_step:"):
+                traffic = int(line.split(":")[1])
 
     out = {
         "metric": "MXFP4 GEMV HBM GB/s + % peak, Qwen3-8B M=1; M=512 prefill TFLOP/s",
@@ -339,8 +356,10 @@ def main() -> int:
                    "bytes_per_step": step_bytes, "x_dtype": "bf16", "y_dtype": "f32",
                    "distinct_weights_bytes": sum(w.nbytes for (_, _, _, w) in weights),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "roofline": {"bound": "hbm", "kernel": "gemv_m1_kernel (all launches of the step)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "basis": "algorithmic bytes of one decode step / GPU event time of one step"},
         "cpu_baseline": cpu,
         "extra": extra,
     }
