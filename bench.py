@@ -191,7 +191,7 @@ def time_prefill(ctx, weights, m: int = 512, reps: int = 5):
     return out
 
 
-def cpu_baseline(ctx, weights, x_host: dict, layers: int = 3) -> dict:
+def cpu_baseline(ctx, weights, x_host: dict, layers: int = 9) -> dict:
     """The oracle on the host: one thread, `layers` layers + the matching share of lm_head."""
     from oracle import mx4_oracle as oracle
 

@@ -79,49 +79,99 @@ struct Segs {
     uint32_t n[kMaxSegs];
     uint32_t first[kMaxSegs + 1];
     uint32_t count;
+    uint32_t rowsets;  // first[count], passed directly so no argument load depends on another
 };
 
-// Sum R per-lane values over the 64 lanes of a wave with log2(64) exchange
-// steps: in the first log2(R) steps each lane keeps half of its values and
-// sends the other half to its partner, so the R totals need 63 + R - 1
-// additions in total instead of R * 63. Afterwards lane l holds the total of
-// row rowsel(l) = sum over the first log2(R) steps of (l & off ? half : 0).
+// Sum R per-lane values over the 64 lanes of a wave in log2(64) exchange
+// stages. In the first log2(R) stages each lane keeps half of its values and
+// sends the other half to its partner, so the R totals cost 63 + R - 1
+// additions instead of R * 63. The exchanges stay in the VALU: DPP
+// row_half_mirror (partner l ^ 7), quad permutations (l ^ 1, l ^ 2) and
+// row_ror:8 (l ^ 8) within rows of 16 lanes, then v_permlane16_swap (l ^ 16)
+// and v_permlane32_swap (l ^ 32). The half-mirror stage goes first: it flips
+// lane bits 0-2 together, which is a valid butterfly partner only while no
+// earlier stage has made lanes differ in bits 0-1. The halving stages select
+// by lane bits 2, 0, 1 in that order, so lane l ends with the total of row
+// reduced_row_of_lane<R>(l).
+template <int CTRL>
+__device__ __forceinline__ float dpp_partner(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+template <int CTRL, int R>
+__device__ __forceinline__ void dpp_stage(float (&v)[R], int& n, bool upper) {
+    if (n > 1) {
+        const int half = n / 2;
+#pragma unroll
+        for (int i = 0; i < R / 2; ++i) {
+            if (i < half) {
+                const float send = upper ? v[i] : v[i + half];
+                const float keep = upper ? v[i + half] : v[i];
+                v[i] = keep + dpp_partner<CTRL>(send);
+            }
+        }
+        n = half;
+    } else {
+        v[0] += dpp_partner<CTRL>(v[0]);
+    }
+}
+
+// Exchange across rows (SWAP = 16) or half-waves (SWAP = 32). After
+// permlane*_swap(a, b) lane l holds {own a, partner's a} if it is the lower
+// partner and {partner's b, own b} if it is the upper one, so the sum of the
+// pair is keep + partner's send in both cases.
+template <int SWAP>
+__device__ __forceinline__ float swap_sum(float lower_keeps, float upper_keeps) {
+    const auto p = SWAP == 16
+                       ? __builtin_amdgcn_permlane16_swap(__float_as_uint(lower_keeps), __float_as_uint(upper_keeps), false, false)
+                       : __builtin_amdgcn_permlane32_swap(__float_as_uint(lower_keeps), __float_as_uint(upper_keeps), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+template <int SWAP, int R>
+__device__ __forceinline__ void swap_stage(float (&v)[R], int& n) {
+    if (n > 1) {
+        const int half = n / 2;
+#pragma unroll
+        for (int i = 0; i < R / 2; ++i)
+            if (i < half) v[i] = swap_sum<SWAP>(v[i], v[i + half]);
+        n = half;
+    } else {
+        v[0] = swap_sum<SWAP>(v[0], v[0]);
+    }
+}
+
+constexpr int kDppHalfMirror = 0x141, kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppRowRor8 = 0x128;
+
 template <int R>
 __device__ __forceinline__ float wave_reduce_rows(float (&v)[R], uint32_t lane) {
     int n = R;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        if (n > 1) {
-            const bool upper = (lane & off) != 0;
-            const int half = n / 2;
-#pragma unroll
-            for (int i = 0; i < R / 2; ++i) {
-                if (i < half) {
-                    float send = upper ? v[i] : v[i + half];
-                    float keep = upper ? v[i + half] : v[i];
-                    v[i] = keep + __shfl_xor(send, off, kWave);
-                }
-            }
-            n = half;
-        } else {
-            v[0] += __shfl_xor(v[0], off, kWave);
-        }
-    }
+    dpp_stage<kDppHalfMirror, R>(v, n, (lane & 4) != 0);
+    dpp_stage<kDppQuadXor1, R>(v, n, (lane & 1) != 0);
+    dpp_stage<kDppQuadXor2, R>(v, n, (lane & 2) != 0);
+    dpp_stage<kDppRowRor8, R>(v, n, (lane & 8) != 0);
+    swap_stage<16, R>(v, n);
+    swap_stage<32, R>(v, n);
     return v[0];
 }
 
+// Row whose total lane `lane` holds after wave_reduce_rows<R> (R <= 8): the
+// halving stages take the upper half when lane bit 2, then 0, then 1 is set.
 template <int R>
 __device__ __forceinline__ uint32_t reduced_row_of_lane(uint32_t lane) {
+    static_assert(R == 1 || R == 2 || R == 4 || R == 8, "rows per team");
     uint32_t row = 0;
-    int half = R / 2;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        if (half >= 1) {
-            row += (lane & off) ? half : 0;
-            half /= 2;
-        }
-    }
+    if constexpr (R >= 2) row += (lane & 4) ? R / 2 : 0;
+    if constexpr (R >= 4) row += (lane & 1) ? R / 4 : 0;
+    if constexpr (R >= 8) row += (lane & 2) ? 1 : 0;
     return row;
+}
+
+// One lane per row writes its total: lane bits outside the row-select bits are zero.
+template <int R>
+__device__ __forceinline__ bool row_writer(uint32_t lane) {
+    constexpr uint32_t row_bits = R >= 8 ? 7u : R == 4 ? 5u : R == 2 ? 4u : 0u;
+    return (lane & ~row_bits) == 0;
 }
 
 // Buffer resource over [base, base + bytes): loads past the end return zero
@@ -244,7 +294,7 @@ __device__ __forceinline__ void finish_rowset(const Segs& sg, uint32_t rs, const
     float* y = sgm.y;
     const float total = wave_reduce_rows<R>(acc, lane);
     const uint32_t myrow = reduced_row_of_lane<R>(lane);
-    const bool writer = (lane & (64 / R - 1)) == 0;
+    const bool writer = row_writer<R>(lane);
     if constexpr (WG == 1) {
         if (writer && row0 + myrow < n) y[row0 + myrow] = total;
     } else {
@@ -266,10 +316,18 @@ __global__ __launch_bounds__(64 * WG) void gemv_m1_kernel(Segs sg, const void* _
     const uint32_t t = threadIdx.x;
     const uint32_t row_bytes = k / 2;
     const uint32_t nblk = k / 32;
-    const uint32_t rowsets = sg.first[sg.count];
-    uint32_t rs = blockIdx.x;
-    if (rs >= rowsets) return;
+    const uint32_t rowsets = sg.rowsets;
+    uint32_t rs = blockIdx.x;  // the host launches at most `rowsets` teams
 
+    // Every kernel argument is needed before the first load. Pinning them in
+    // SGPRs here makes the compiler fetch them in one scalar round trip
+    // (otherwise it splits the fetch and waits twice before the first weight
+    // load); the weight stream is issued first, the activations right behind.
+#pragma unroll
+    for (int q = 0; q < kMaxSegs; ++q)
+        asm volatile("" ::"s"(sg.packed[q]), "s"(sg.scales[q]), "s"(sg.y[q]), "s"(sg.n[q]), "s"(sg.first[q]));
+    asm volatile("" ::"s"(x), "s"(sg.count), "s"(k));
+    __builtin_amdgcn_sched_barrier(0);
     RowSet<XBF16, BPL, R> a, b;
     load_rowset<XBF16, WG, BPL, R>(sg, rs, rowsets, t, row_bytes, nblk, a);
     LaneX<XBF16, BPL> xr;
@@ -393,31 +451,30 @@ bool gemv_m1_supported(uint32_t k) {
     return k % 32 == 0 && (nblk == 64 || nblk == 128 || nblk == 192 || nblk == 256 || nblk == 384);
 }
 
-// Default configuration: team size and rows per team by K, persistent grid
-// of about `waves_per_cu` waves per CU, every team visiting the same number
-// of rowsets (+-1).
 // Default configuration, from sweeps on MI355X over the launches of the Qwen3
 // 1.7B and 8B decode steps (q|k|v and gate|up grouped, cold weights, recorded
-// passes): the team splits K into 1-2 blocks per lane, 2-4 rows per team, and
-// a grid of up to `grid` teams (one row-set each when the matrix is small).
+// passes). One wave per team for K <= 4096 (1-2 blocks per lane); for long K
+// a 3-wave team and few workgroups, because every workgroup loads the whole
+// activation row (24 KiB at K = 12288) and the number of workgroups, not the
+// number of rows, sets that cost. Grids are in teams per CU.
 static void default_m1_config(uint32_t k, uint32_t rows, int cus, M1Config& c) {
     const uint32_t nblk = k / 32;
     const uint32_t scale = (uint32_t)(cus > 0 ? cus : 256);  // the table is for 256 CUs
     switch (nblk) {
         case 64:  // K = 2048
-            c.wg = 1; c.r = rows > 8192 ? 4 : 2; c.grid = 8 * scale;
+            c.wg = 1; c.r = rows > 2048 ? 4 : 2; c.grid = (rows > 65536 ? 8 : 12) * scale;
             break;
         case 128:  // K = 4096
-            c.wg = rows > 8192 ? 1 : 2; c.r = rows > 65536 ? 4 : 2; c.grid = (rows > 65536 ? 4 : 8) * scale;
+            c.wg = 1; c.r = rows > 65536 ? 4 : 2; c.grid = (rows > 65536 || rows <= 8192 ? 4 : 8) * scale;
             break;
         case 192:  // K = 6144
-            c.wg = 3; c.r = 2; c.grid = 4 * scale;
+            c.wg = 3; c.r = 2; c.grid = 3 * scale;
             break;
         case 256:  // K = 8192
             c.wg = 2; c.r = 4; c.grid = 8 * scale;
             break;
         default:  // K = 12288
-            c.wg = 3; c.r = 2; c.grid = 16 * scale;
+            c.wg = 3; c.r = 4; c.grid = scale;
             break;
     }
     c.waves_per_cu = 0;
@@ -449,6 +506,7 @@ hipError_t launch_gemv_m1_group(const GemvGroup& g, int cus, const M1Config* for
     }
     for (uint32_t s = g.count; s < (uint32_t)kMaxSegs; ++s) sg.first[s + 1] = sg.first[g.count];
     const uint32_t rowsets = sg.first[g.count];
+    sg.rowsets = rowsets;
     // grid 0 (a forced configuration without a grid): one row-set per team
     uint32_t grid = c.grid == 0 || c.grid > rowsets ? rowsets : c.grid;
     // even split: every team visits the same number of row-sets (+-1)
