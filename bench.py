@@ -149,7 +149,8 @@ def time_skinny(ctx, weights, ms=(1, 2, 4, 8, 16), reps: int = 3):
 def time_prefill(ctx, weights, m: int = 512, reps: int = 5):
     """Prefill on block-scaled MFMA: each 8B q/o/gate/up/down shape at M = 512,
     activations bf16 N(0, 1) requantized per 32 along K (MXFP4, and MX-FP8).
-    Reports the GEMM kernel alone and requant + GEMM, as TFLOP/s of 2*M*N*K."""
+    Reports the GEMM kernel alone (activations requantized beforehand, as when
+    q|k|v or gate|up share them) and requant + GEMM, as TFLOP/s of 2*M*N*K."""
     by = {}
     for (nm, n, k, w) in weights:
         by.setdefault(nm, (n, k, w))
@@ -162,16 +163,13 @@ def time_prefill(ctx, weights, m: int = 512, reps: int = 5):
         ctx.synth_bf16(3, 1.0, m * k, xb)
         yb = ctx.buffer(m * n * 4)
         row = {}
+        w.prepare_prefill()  # the matrix-core copy of the weight is built outside the timed passes
         for act, code in (("mxfp4", mx4hip.ACT_MXFP4), ("mxfp8", mx4hip.ACT_MXFP8)):
-            qbytes = m * k // 2 if act == "mxfp4" else m * k
-            xq, xs = ctx.buffer(qbytes), ctx.buffer(m * k // 32)
-            if act == "mxfp4":
-                ctx.quantize(xb, mx4hip.BF16, m, k, xq, xs)
-            else:
-                ctx.quantize_fp8(xb, mx4hip.BF16, m, k, xq, xs)
+            xq, xs = ctx.prefill_act_buffers(m, k, code)
+            ctx.prefill_quantize(xb, mx4hip.BF16, m, k, code, xq, xs)
             flops = 2.0 * m * n * k
             res = {}
-            for label, fn in (("gemm", lambda: ctx.matmul_mx(xq, xs, code, m, w, yb)),
+            for label, fn in (("gemm", lambda: ctx.prefill_matmul(xq, xs, code, m, w, yb)),
                               ("requant+gemm", lambda: ctx.matmul_prefill(xb, mx4hip.BF16, m, w, code, yb))):
                 p = ctx.record(lambda: [fn() for _ in range(8)])
                 p.launch()

@@ -195,16 +195,38 @@ mx4_status mx4_pass_end(mx4_context *ctx, mx4_pass **out);
 mx4_status mx4_pass_launch(mx4_context *ctx, const mx4_pass *pass);
 void mx4_pass_release(mx4_pass *pass);
 
-/* Reserve the requantization workspace of mx4_matmul_prefill for up to max_m
- * rows of max_cols (either activation format), so later calls -- including
- * calls recorded into a pass, where allocation is impossible -- allocate nothing. */
+/* Reserve the requantization workspace of mx4_matmul_prefill / mx4_matmul_mx
+ * for up to max_m rows of max_cols (either activation format), so later calls
+ * -- including calls recorded into a pass, where allocation is impossible --
+ * allocate nothing. */
 mx4_status mx4_reserve_prefill(mx4_context *ctx, uint32_t max_m, uint32_t max_cols);
+
+/* Build the weight's copy in the matrix-core operand order used by the
+ * block-scaled MFMA path (rows in groups of 32, one 1 KiB block per group and
+ * 64 columns; about 1.06x the packed size, freed with the weight). The first
+ * mx4_matmul_prefill / mx4_matmul_mx on a weight builds it on its own; call
+ * this first for weights used inside a recorded pass. No counterpart in the
+ * reference (its Metal kernels read the stored layout). */
+mx4_status mx4_weight_prepare_prefill(mx4_weight *w);
 
 /* The block-scaled MFMA product for activations that are already requantized
  * (xq_dev: MXFP4 packed [m][cols/2] or E4M3 [m][cols]; xs_dev: E8M0 [m][cols/32],
  * as mx4_quantize / mx4_quantize_fp8 produce them). */
 mx4_status mx4_matmul_mx(mx4_context *ctx, const uint8_t *xq_dev, const uint8_t *xs_dev,
                          mx4_act_format act, uint32_t m, const mx4_weight *w, float *y_dev);
+
+/* Activations requantized once for several prefill GEMMs that read the same
+ * x (q|k|v, gate|up): mx4_prefill_quantize writes them in the matrix-core
+ * operand order of the block-scaled MFMA path (rows in groups of 32), and
+ * mx4_prefill_matmul multiplies such activations with a weight. Sizes of the
+ * two device buffers (codes, scales) for m rows of cols (cols % 256 == 0).
+ * Same arithmetic as mx4_matmul_prefill, which is these two calls in one. */
+mx4_status mx4_prefill_act_bytes(uint32_t m, uint32_t cols, mx4_act_format act, uint64_t *codes_bytes,
+                                 uint64_t *scales_bytes);
+mx4_status mx4_prefill_quantize(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m, uint32_t cols,
+                                mx4_act_format act, uint8_t *codes_dev, uint8_t *scales_dev);
+mx4_status mx4_prefill_matmul(mx4_context *ctx, const uint8_t *codes_dev, const uint8_t *scales_dev,
+                              mx4_act_format act, uint32_t m, const mx4_weight *w, float *y_dev);
 
 /* engine/src/mxfp4.rs:35-49 on device: out_dev[rows*cols] f32, bit-exact. */
 mx4_status mx4_dequantize(mx4_context *ctx, const mx4_weight *w, float *out_dev);

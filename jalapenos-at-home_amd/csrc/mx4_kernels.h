@@ -44,12 +44,14 @@ hipError_t launch_gemv_generic(const GemvArgs& a);
 bool skinny_supported(uint32_t m, uint32_t k);
 hipError_t launch_skinny(const GemvArgs& a, int cus);
 
-// Block-scaled MFMA prefill on requantized activations.
+// Block-scaled MFMA prefill on requantized activations. Both operands are in
+// the fragment-native layout of prefill.hip (launch_to_fragments, or the
+// quantizers' fragment output).
 struct PrefillArgs {
-    const uint8_t* packed;    // W [n][k/2]
-    const uint8_t* scales;    // W [n][k/32]
-    const uint8_t* xq;        // activations requantized: fp4 [m][k/2] or fp8 [m][k]
-    const uint8_t* xs;        // activation scales [m][k/32]
+    const uint8_t* wf;        // weight codes, fragment-native, rows padded to 32
+    const uint8_t* wsf;       // weight scales, fragment-native
+    const uint8_t* xf;        // requantized activations: fp4 or fp8 fragments
+    const uint8_t* xsf;       // activation scales, fragment-native
     float* y;                 // [m][n]
     uint32_t m, n, k;
     bool fp8;                 // activations are MX-FP8 (E4M3) instead of MXFP4
@@ -57,6 +59,13 @@ struct PrefillArgs {
 };
 bool prefill_supported(uint32_t m, uint32_t n, uint32_t k);
 hipError_t launch_prefill(const PrefillArgs& a, int cus);
+// Sizes of the fragment-native copies of a rows x k operand (rows padded to 32).
+uint64_t fragment_bytes(uint32_t rows, uint32_t k, bool fp8);
+uint64_t fragment_scale_bytes(uint32_t rows, uint32_t k);
+// Row-major codes [rows][k/2] (fp4) or [rows][k] (fp8) + scales [rows][k/32]
+// -> fragment-native copies.
+hipError_t launch_to_fragments(const uint8_t* codes, const uint8_t* scales, uint32_t rows, uint32_t k, bool fp8,
+                               uint8_t* codes_f, uint8_t* scales_f, hipStream_t s);
 
 // quantize_mxfp4.py:18-39 on device: rows x cols (cols % 32 == 0) f32/bf16 ->
 // packed [rows][cols/2] + scales [rows][cols/32]. Non-finite input sets *bad.
@@ -65,6 +74,10 @@ hipError_t launch_quantize_mxfp4(const void* in, bool in_bf16, uint64_t rows, ui
 // MX-FP8 (E4M3): codes [rows][cols] + scales [rows][cols/32]
 hipError_t launch_quantize_fp8(const void* in, bool in_bf16, uint64_t rows, uint32_t cols,
                                uint8_t* codes, uint8_t* scales, uint32_t* bad, hipStream_t s);
+// The same two rules writing the fragment-native layout of prefill.hip
+// (cols % 256 == 0); rows past `rows` in the last group of 32 are left unset.
+hipError_t launch_quantize_fragments(const void* in, bool in_bf16, uint32_t rows, uint32_t cols, bool fp8,
+                                     uint8_t* codes_f, uint8_t* scales_f, uint32_t* bad, hipStream_t s);
 // engine/src/mxfp4.rs:35-49 on device: packed/scales -> f32 [elements]
 hipError_t launch_dequantize(const uint8_t* packed, const uint8_t* scales, uint64_t elements,
                              float* out, hipStream_t s);

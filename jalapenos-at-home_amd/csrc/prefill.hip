@@ -4,13 +4,13 @@
 // The reference runs prefill on a 16x16 FP32 tiled kernel that decodes each
 // weight element into threadgroup memory (project_mxfp4,
 // engine/src/matmul.metal:65-97). Here the weights stay in their MXFP4 form all
-// the way into the matrix core: operand B is the packed E2M1 nibbles exactly as
-// stored (element 2j in the low nibble of byte j, which is also the operand's
-// element order) with the E8M0 byte of each 32-element block as the lane's B
-// scale. Operand A is the activations after per-32 requantization (MXFP4 by the
-// same rule as the weights, python/quantize_mxfp4.py:18-39, or MX-FP8 E4M3),
-// with their E8M0 bytes as A scales. Products of FP4/FP8 values with power-of-
-// two scales are exact; the matrix core accumulates in f32.
+// the way into the matrix core: operand B is the packed E2M1 nibbles (element
+// 2j in the low nibble of byte j, which is also the operand's element order)
+// with the E8M0 byte of each 32-element block as the lane's B scale. Operand A
+// is the activations after per-32 requantization (MXFP4 by the same rule as
+// the weights, python/quantize_mxfp4.py:18-39, or MX-FP8 E4M3), with their
+// E8M0 bytes as A scales. Products of FP4/FP8 values with power-of-two scales
+// are exact; the matrix core accumulates in f32.
 //
 // Operand layout (32x32x64), established by in-bounds probes and pinned by the
 // identity tests: for FP4, lane l holds row (l % 32) of A (column of B) and the
@@ -19,11 +19,27 @@
 // scale byte of lane group h applies to K block h. C: lane l holds column
 // l % 32, rows 8 (v / 4) + 4 (l / 32) + v % 4 of accumulator register v.
 //
-// Tiling: a 256-thread workgroup computes a 128 x 128 output tile as 2 x 2
-// waves of 64 x 64 (2 x 2 MFMA tiles each). K advances in stages of 256: each
-// stage's A and B tiles (128 rows x 128 bytes of FP4, or 256 bytes of FP8) and
-// their scales are loaded with 128-byte contiguous row segments into registers,
-// written to padded LDS, and consumed while the next stage is in flight.
+// Fragment-native layout. Read in the stored row-major layout, one operand
+// fragment (32 rows x 32 bytes) touches 32 cache lines per load instruction,
+// and the address path, not HBM, limits the kernel. The operands are therefore
+// rewritten once into the order the matrix core consumes them: rows in groups
+// of 32; for group g and k-step kk (64 elements of K) the FP4 fragment is 1 KiB
+// contiguous, lane l's 16 bytes at 16 l (row 32 g + l % 32, bytes
+// [32 kk + 16 (l / 32), +16) of the row); an FP8 fragment is 2 KiB, the first
+// 1 KiB holding each lane's bytes [64 kk + 16 h, +16) and the second its bytes
+// [64 kk + 32 + 16 h, +16). Scales: for group g and quad q (4 k-steps) 64
+// lanes x 4 bytes, byte u of lane l = the E8M0 byte of block 8 q + 2 u + l / 32
+// of row 32 g + l % 32, so the MFMA's byte select (op_sel) picks k-step u.
+// Weights get this copy once (prepare); activations are requantized straight
+// into it. Every load is then a 1 KiB coalesced burst straight into the
+// registers the matrix core reads: no LDS and no barriers in the main loop.
+//
+// Kernel: a wave owns a (32 TM) x (32 TN) output tile over its K range and
+// keeps a ring of Q slots of U k-steps of fragments in flight (the register
+// file is the prefetch buffer). Four waves per workgroup: 2 x 2 tiles, or (for
+// KSPLIT = 2) two tiles x two K halves whose partial tiles meet in LDS at the
+// end. Each fragment row-group gets its own buffer resource bounded to the
+// wave's K range, so the prefetch beyond it reads zeros without touching memory.
 #include "mx4_device.h"
 #include "mx4_kernels.h"
 
@@ -42,180 +58,285 @@ __device__ __forceinline__ void mfma_drain() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-constexpr int BM = 128, BN = 128, KS = 256;   // tile rows, cols, K per stage
-constexpr int kFmtFp8 = 0, kFmtFp4 = 4;        // MFMA operand format codes (cbsz / blgp)
+constexpr int kFmtFp8 = 0, kFmtFp4 = 4;  // MFMA operand format codes (cbsz / blgp)
 
-template <bool A_FP8>
-struct Cfg {
-    static constexpr uint32_t a_row = A_FP8 ? KS : KS / 2;  // bytes of A per row per stage
-    static constexpr uint32_t b_row = KS / 2;
-    static constexpr uint32_t a_pitch = a_row + 16;          // LDS row pitch (bank spread)
-    static constexpr uint32_t b_pitch = b_row + 16;
-    static constexpr uint32_t a_bytes = BM * a_pitch;
-    static constexpr uint32_t b_bytes = BN * b_pitch;
-    static constexpr uint32_t a_loads = BM * a_row / (256 * 16);  // 16-byte loads per thread
-    static constexpr uint32_t b_loads = BN * b_row / (256 * 16);
+template <bool A_FP8, int TM, int TN, int U>
+struct Slot {
+    u32x4 a[U][TM][A_FP8 ? 2 : 1];
+    u32x4 b[U][TN];
 };
 
-template <bool A_FP8>
-__global__ __launch_bounds__(256) void prefill_kernel(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ ws,
-                                                      const uint8_t* __restrict__ xq, const uint8_t* __restrict__ xs,
-                                                      float* __restrict__ y, uint32_t m, uint32_t n, uint32_t k) {
-    using C = Cfg<A_FP8>;
+// One k-step of the wave tile: TM x TN MFMAs; OPSEL picks the scale byte (the
+// k-step within its quad).
+template <int OPSEL, bool A_FP8, int TM, int TN>
+__device__ __forceinline__ void kstep(const u32x4 (&a)[TM][A_FP8 ? 2 : 1], const u32x4 (&b)[TN],
+                                      const uint32_t (&sa)[TM], const uint32_t (&sb)[TN], f32x16 (&acc)[TM][TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        i32x8 av;
+        if constexpr (A_FP8) {
+            const u32x4 lo = a[i][0], hi = a[i][1];
+            av = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        } else {
+            const u32x4 v = a[i][0];
+            av = i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const u32x4 w = b[j];
+            const i32x8 bv = i32x8{(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, acc[i][j], A_FP8 ? kFmtFp8 : kFmtFp4,
+                                                                        kFmtFp4, OPSEL, (int)sa[i], OPSEL, (int)sb[j]);
+        }
+    }
+}
+
+// Bytes from `base` to the end of an allocation of `total` bytes, at most `want`.
+__device__ __forceinline__ uint32_t clamp_bytes(uint64_t want, uint64_t base, uint64_t total) {
+    return (uint32_t)(base >= total ? 0 : (total - base < want ? total - base : want));
+}
+
+// TM x TN tiles of 32 x 32 per wave; U k-steps per slot; Q slots in flight;
+// KSPLIT K halves per workgroup; RS scale quads in flight; NKC = k-steps per
+// wave when fixed at compile time (fully unrolled), 0 for a loop.
+template <bool A_FP8, int TM, int TN, int U, int Q, int KSPLIT, int RS, int NKC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_kernel(
+    const uint8_t* __restrict__ wf, const uint8_t* __restrict__ wsf, const uint8_t* __restrict__ xf,
+    const uint8_t* __restrict__ xsf, float* __restrict__ y, uint32_t m, uint32_t n, uint32_t k) {
+    static_assert((Q * U) % 4 == 0 && ((Q * U) / 4) % RS == 0, "slots must cover whole scale quads");
+    constexpr int WM = KSPLIT == 1 ? 2 : 1;
+    constexpr uint32_t BM = WM * 32 * TM, BN = 2 * 32 * TN;
+    constexpr uint32_t AF = A_FP8 ? 2048 : 1024;  // bytes of one A fragment
     const uint32_t t = threadIdx.x, lane = t % 64;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t / 64);
-    const uint32_t wm = wave / 2, wn = wave % 2;  // wave position in the 2 x 2 grid
-    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const uint32_t stages = k / KS;
-    const uint32_t a_rowbytes = A_FP8 ? k : k / 2, b_rowbytes = k / 2, sblk = k / 32;
+    const uint32_t wn = wave % 2;
+    const uint32_t wm = KSPLIT == 1 ? wave / 2 : 0;
+    const uint32_t kh = KSPLIT == 1 ? 0 : wave / 2;
+    const uint32_t m0 = blockIdx.y * BM + wm * 32 * TM;
+    const uint32_t n0 = blockIdx.x * BN + wn * 32 * TN;
+    const uint32_t nk_all = k / 64, nq_all = k / 256;
+    const uint32_t nk = NKC ? (uint32_t)NKC : nk_all / KSPLIT;  // k-steps of this wave
+    const uint32_t k0 = kh * nk;
+    const uint32_t ga = m0 / 32, gb = n0 / 32;  // first row groups
+    const uint64_t a_total = (uint64_t)((m + 31) / 32) * nk_all * AF;
+    const uint64_t b_total = (uint64_t)((n + 31) / 32) * nk_all * 1024;
+    const uint64_t as_total = (uint64_t)((m + 31) / 32) * nq_all * 256;
+    const uint64_t bs_total = (uint64_t)((n + 31) / 32) * nq_all * 256;
 
-    // bounded views: rows past m or n read as zeros
-    const uint32_t arows = m - m0 < (uint32_t)BM ? m - m0 : (uint32_t)BM;
-    const uint32_t brows = n - n0 < (uint32_t)BN ? n - n0 : (uint32_t)BN;
-    const __amdgpu_buffer_rsrc_t ar = rsrc(xq + (size_t)m0 * a_rowbytes, arows * a_rowbytes);
-    const __amdgpu_buffer_rsrc_t br = rsrc(wq + (size_t)n0 * b_rowbytes, brows * b_rowbytes);
-    const __amdgpu_buffer_rsrc_t asr = rsrc(xs + (size_t)m0 * sblk, arows * sblk);
-    const __amdgpu_buffer_rsrc_t bsr = rsrc(ws + (size_t)n0 * sblk, brows * sblk);
+    // one resource per row group, bounded to this wave's K range
+    __amdgpu_buffer_rsrc_t ar[TM], asr[TM], br[TN], bsr[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const uint64_t base = ((uint64_t)(ga + i) * nk_all + k0) * AF;
+        const uint64_t sbase = ((uint64_t)(ga + i) * nq_all + k0 / 4) * 256;
+        ar[i] = rsrc(xf + (base < a_total ? base : 0), clamp_bytes((uint64_t)nk * AF, base, a_total));
+        asr[i] = rsrc(xsf + (sbase < as_total ? sbase : 0), clamp_bytes((uint64_t)nk / 4 * 256, sbase, as_total));
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const uint64_t base = ((uint64_t)(gb + j) * nk_all + k0) * 1024;
+        const uint64_t sbase = ((uint64_t)(gb + j) * nq_all + k0 / 4) * 256;
+        br[j] = rsrc(wf + (base < b_total ? base : 0), clamp_bytes((uint64_t)nk * 1024, base, b_total));
+        bsr[j] = rsrc(wsf + (sbase < bs_total ? sbase : 0), clamp_bytes((uint64_t)nk / 4 * 256, sbase, bs_total));
+    }
 
-    __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][C::a_bytes];
-    __shared__ __attribute__((aligned(16))) uint8_t lds_b[2][C::b_bytes];
-    __shared__ uint32_t lds_as[2][BM * (KS / 32) / 4];  // scale bytes, [row][8 blocks]
-    __shared__ uint32_t lds_bs[2][BN * (KS / 32) / 4];
-
-    // global -> register staging: thread t covers 16-byte pieces of the tile
-    struct Stage {
-        u32x4 a[C::a_loads];
-        u32x4 b[C::b_loads];
-        uint32_t as, bs;
+    using S = Slot<A_FP8, TM, TN, U>;
+    constexpr uint32_t kSlots = NKC ? (uint32_t)NKC / U : 0xffffffffu;  // slots that exist (unrolled form)
+    auto issue = [&](uint32_t slot, S& s) {
+        if (slot >= kSlots) return;  // folded away when unrolled; never taken in the loop form
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t kk = slot * U + u;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                s.a[u][i][0] = __builtin_amdgcn_raw_buffer_load_b128(ar[i], kk * AF + 16 * lane, 0, 0);
+                if constexpr (A_FP8)
+                    s.a[u][i][1] = __builtin_amdgcn_raw_buffer_load_b128(ar[i], kk * AF + 1024 + 16 * lane, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                s.b[u][j] = __builtin_amdgcn_raw_buffer_load_b128(br[j], kk * 1024 + 16 * lane, 0, 0);
+        }
     };
-    constexpr uint32_t a_pieces = C::a_row / 16, b_pieces = C::b_row / 16;
-    auto gload = [&](uint32_t s, Stage& st) {
-        const uint32_t aoff = s * C::a_row, boff = s * C::b_row, soff = s * (KS / 32);
+    uint32_t sa[RS][TM], sb[RS][TN];
+    auto issue_scales = [&](uint32_t quad, uint32_t (&a)[TM], uint32_t (&b)[TN]) {
 #pragma unroll
-        for (uint32_t i = 0; i < C::a_loads; ++i) {
-            const uint32_t p = t + 256 * i, row = p / a_pieces, piece = p % a_pieces;
-            st.a[i] = __builtin_amdgcn_raw_buffer_load_b128(ar, row * a_rowbytes + aoff + 16 * piece, 0, 0);
-        }
+        for (int i = 0; i < TM; ++i) a[i] = __builtin_amdgcn_raw_buffer_load_b32(asr[i], quad * 256 + 4 * lane, 0, 0);
 #pragma unroll
-        for (uint32_t i = 0; i < C::b_loads; ++i) {
-            const uint32_t p = t + 256 * i, row = p / b_pieces, piece = p % b_pieces;
-            st.b[i] = __builtin_amdgcn_raw_buffer_load_b128(br, row * b_rowbytes + boff + 16 * piece, 0, 2);
-        }
-        // 8 scale bytes per row per stage: thread t takes row t / 2, half t % 2
-        st.as = __builtin_amdgcn_raw_buffer_load_b32(asr, (t / 2) * sblk + soff + 4 * (t % 2), 0, 0);
-        st.bs = __builtin_amdgcn_raw_buffer_load_b32(bsr, (t / 2) * sblk + soff + 4 * (t % 2), 0, 0);
-    };
-    auto lstore = [&](uint32_t buf, const Stage& st) {
-#pragma unroll
-        for (uint32_t i = 0; i < C::a_loads; ++i) {
-            const uint32_t p = t + 256 * i, row = p / a_pieces, piece = p % a_pieces;
-            *reinterpret_cast<u32x4*>(&lds_a[buf][row * C::a_pitch + 16 * piece]) = st.a[i];
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < C::b_loads; ++i) {
-            const uint32_t p = t + 256 * i, row = p / b_pieces, piece = p % b_pieces;
-            *reinterpret_cast<u32x4*>(&lds_b[buf][row * C::b_pitch + 16 * piece]) = st.b[i];
-        }
-        lds_as[buf][t] = st.as;
-        lds_bs[buf][t] = st.bs;
+        for (int j = 0; j < TN; ++j) b[j] = __builtin_amdgcn_raw_buffer_load_b32(bsr[j], quad * 256 + 4 * lane, 0, 0);
     };
 
-    f32x16 acc[2][2];
+    f32x16 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    const uint32_t r32 = lane % 32, h = lane / 32;
-    auto compute = [&](uint32_t buf) {
-        const uint8_t* la = lds_a[buf];
-        const uint8_t* lb = lds_b[buf];
-        const uint8_t* las = reinterpret_cast<const uint8_t*>(lds_as[buf]);
-        const uint8_t* lbs = reinterpret_cast<const uint8_t*>(lds_bs[buf]);
+    S sl[Q];
 #pragma unroll
-        for (uint32_t ks = 0; ks < KS / 64; ++ks) {
-            i32x8 af[2], bf[2];
-            int32_t sa[2], sb[2];
+    for (int r = 0; r < RS - 1; ++r) issue_scales(r, sa[r], sb[r]);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const uint32_t row = wm * 64 + i * 32 + r32;
-                if constexpr (A_FP8) {
-                    // 8-bit operands interleave the K halves: lane group h holds K
-                    // [16h, 16h + 16) in registers 0-3 and [32 + 16h, +16) in 4-7;
-                    // the scale of K block b still comes from lane group b.
-                    const uint8_t* p = la + row * C::a_pitch + ks * 64 + h * 16;
-                    const u32x4 lo = *reinterpret_cast<const u32x4*>(p);
-                    const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 32);
-                    af[i] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-                } else {
-                    const u32x4 v = *reinterpret_cast<const u32x4*>(la + row * C::a_pitch + ks * 32 + h * 16);
-                    af[i] = i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
+    for (int j = 0; j < Q; ++j) issue(j, sl[j]);
+#pragma unroll
+    for (uint32_t base = 0; base < nk; base += Q * U) {
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int kl = j * U + u;
+                const int g = kl / 4, o = kl % 4;
+                if (o == 0) issue_scales(base / 4 + g + RS - 1, sa[(g + RS - 1) % RS], sb[(g + RS - 1) % RS]);
+                switch (o) {
+                    case 0: kstep<0, A_FP8, TM, TN>(sl[j].a[u], sl[j].b[u], sa[g % RS], sb[g % RS], acc); break;
+                    case 1: kstep<1, A_FP8, TM, TN>(sl[j].a[u], sl[j].b[u], sa[g % RS], sb[g % RS], acc); break;
+                    case 2: kstep<2, A_FP8, TM, TN>(sl[j].a[u], sl[j].b[u], sa[g % RS], sb[g % RS], acc); break;
+                    default: kstep<3, A_FP8, TM, TN>(sl[j].a[u], sl[j].b[u], sa[g % RS], sb[g % RS], acc); break;
                 }
-                sa[i] = las[row * 8 + ks * 2 + h];
             }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint32_t row = wn * 64 + j * 32 + r32;
-                const u32x4 v = *reinterpret_cast<const u32x4*>(lb + row * C::b_pitch + ks * 32 + h * 16);
-                bf[j] = i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
-                sb[j] = lbs[row * 8 + ks * 2 + h];
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        af[i], bf[j], acc[i][j], A_FP8 ? kFmtFp8 : kFmtFp4, kFmtFp4, 0, sa[i], 0, sb[j]);
+            // refill this slot only after its MFMAs were issued: otherwise the
+            // scheduler hoists every refill to the end of the ring turn
+            __builtin_amdgcn_sched_barrier(0);
+            issue(base / U + j + Q, sl[j]);
+            __builtin_amdgcn_sched_barrier(0);
         }
-    };
-
-    Stage st;
-    gload(0, st);
-    lstore(0, st);
-    __syncthreads();
-    for (uint32_t s = 0; s < stages; ++s) {
-        const uint32_t buf = s & 1;
-        const bool more = s + 1 < stages;
-        if (more) gload(s + 1, st);
-        compute(buf);
-        if (more) lstore(buf ^ 1, st);
-        __syncthreads();
     }
     mfma_drain();
 
-    // write the 64 x 64 wave tile
+    if constexpr (KSPLIT == 2) {
+        __shared__ float red[2][TM * TN * 16][64];
+        if (kh == 1) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t col = n0 + wn * 64 + j * 32 + r32;
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) red[wn][(i * TN + j) * 16 + v][lane] = acc[i][j][v];
+        }
+        __syncthreads();
+        if (kh == 1) return;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][j][v] += red[wn][(i * TN + j) * 16 + v][lane];
+    }
+    const uint32_t r32 = lane % 32, h = lane / 32;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint32_t col = n0 + 32 * j + r32;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const uint32_t row = m0 + wm * 64 + i * 32 + 8 * (v / 4) + 4 * h + (v % 4);
+                const uint32_t row = m0 + 32 * i + 8 * (v / 4) + 4 * h + (v % 4);
                 if (row < m && col < n) y[(size_t)row * n + col] = acc[i][j][v];
             }
         }
 }
 
+// Row-major codes -> fragment-native order. One thread per 16-byte output
+// chunk; rows past `rows` (the padding of the last group) are zero.
+template <bool FP8>
+__global__ __launch_bounds__(256) void to_fragments_kernel(const uint8_t* __restrict__ src, uint32_t rows,
+                                                           uint32_t k, uint64_t chunks, uint8_t* __restrict__ dst) {
+    const uint64_t c = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= chunks) return;
+    const uint32_t nk = k / 64, lane = (uint32_t)(c % 64);
+    uint64_t rest = c / 64;
+    uint32_t half = 0;
+    if constexpr (FP8) {
+        half = (uint32_t)(rest % 2);
+        rest /= 2;
+    }
+    const uint32_t kk = (uint32_t)(rest % nk);
+    const uint64_t g = rest / nk;
+    const uint64_t row = 32 * g + lane % 32;
+    const uint32_t h = lane / 32;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (row < rows) {
+        const uint64_t off = FP8 ? row * k + 64 * kk + 32 * half + 16 * h : row * (k / 2) + 32 * kk + 16 * h;
+        v = *reinterpret_cast<const u32x4*>(src + off);
+    }
+    *reinterpret_cast<u32x4*>(dst + 16 * c) = v;
+}
+
+// Row-major E8M0 bytes [rows][k/32] -> fragment-native scale words.
+__global__ __launch_bounds__(256) void scales_to_fragments_kernel(const uint8_t* __restrict__ src, uint32_t rows,
+                                                                  uint32_t k, uint64_t words,
+                                                                  uint32_t* __restrict__ dst) {
+    const uint64_t d = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= words) return;
+    const uint32_t nq = k / 256, lane = (uint32_t)(d % 64);
+    const uint64_t rest = d / 64;
+    const uint32_t q = (uint32_t)(rest % nq);
+    const uint64_t row = 32 * (rest / nq) + lane % 32;
+    const uint32_t h = lane / 32;
+    uint32_t v = 0;
+    if (row < rows) {
+        const uint8_t* s = src + row * (k / 32) + 8 * q + h;
+        v = (uint32_t)s[0] | ((uint32_t)s[2] << 8) | ((uint32_t)s[4] << 16) | ((uint32_t)s[6] << 24);
+    }
+    dst[d] = v;
+}
+
+template <bool A_FP8, int TM, int TN, int U, int Q, int KSPLIT, int RS, int NKC>
+hipError_t go(const PrefillArgs& a) {
+    constexpr uint32_t BM = (KSPLIT == 1 ? 2 : 1) * 32 * TM, BN = 64 * TN;
+    dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM);
+    hipLaunchKernelGGL((prefill_kernel<A_FP8, TM, TN, U, Q, KSPLIT, RS, NKC>), grid, dim3(256), 0, a.stream, a.wf,
+                       a.wsf, a.xf, a.xsf, a.y, a.m, a.n, a.k);
+    return hipGetLastError();
+}
+
+template <bool A_FP8>
+hipError_t dispatch(const PrefillArgs& a) {
+    // measured on MI355X at M = 512 (Qwen3-8B shapes): wide N keeps 2 x 3 tiles
+    // per wave over the full K; otherwise 2 x 2 tiles with K split in two
+    // inside the workgroup, fully unrolled for the model's K sizes
+    if constexpr (!A_FP8) {
+        if (a.n >= 8192 && a.n % 192 == 0 && a.k % 512 == 0) return go<false, 2, 3, 2, 4, 1, 2, 0>(a);
+    }
+    if (a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 2, 2, 32>(a);
+    if (a.k == 12288) return go<A_FP8, 2, 2, 2, 4, 2, 2, 96>(a);
+    if (a.k % 512 == 0) return go<A_FP8, 2, 2, 2, 4, 2, 2, 0>(a);
+    return go<A_FP8, 2, 2, 2, 2, 1, 1, 0>(a);
+}
+
 }  // namespace
 
 bool prefill_supported(uint32_t m, uint32_t n, uint32_t k) {
-    return m >= 1 && n >= 1 && k % KS == 0 && k >= KS && (uint64_t)n * (k / 2) < (1ull << 31) &&
-           (uint64_t)m * k < (1ull << 31);
+    // fragment buffers are addressed with 32-bit offsets
+    const uint64_t mp = ((uint64_t)m + 31) / 32 * 32, np = ((uint64_t)n + 31) / 32 * 32;
+    return m >= 1 && n >= 1 && k % 256 == 0 && np * (k / 2) < (1ull << 31) && mp * k < (1ull << 31);
+}
+
+uint64_t fragment_bytes(uint32_t rows, uint32_t k, bool fp8) {
+    return ((uint64_t)rows + 31) / 32 * 32 * k / (fp8 ? 1 : 2);
+}
+
+uint64_t fragment_scale_bytes(uint32_t rows, uint32_t k) { return ((uint64_t)rows + 31) / 32 * 32 * (k / 32); }
+
+hipError_t launch_to_fragments(const uint8_t* codes, const uint8_t* scales, uint32_t rows, uint32_t k, bool fp8,
+                               uint8_t* codes_f, uint8_t* scales_f, hipStream_t s) {
+    const uint64_t chunks = fragment_bytes(rows, k, fp8) / 16, words = fragment_scale_bytes(rows, k) / 4;
+    if (chunks == 0) return hipSuccess;
+    if (fp8)
+        hipLaunchKernelGGL(to_fragments_kernel<true>, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s, codes,
+                           rows, k, chunks, codes_f);
+    else
+        hipLaunchKernelGGL(to_fragments_kernel<false>, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s,
+                           codes, rows, k, chunks, codes_f);
+    hipLaunchKernelGGL(scales_to_fragments_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s, scales,
+                       rows, k, words, reinterpret_cast<uint32_t*>(scales_f));
+    return hipGetLastError();
 }
 
 hipError_t launch_prefill(const PrefillArgs& a, int) {
     if (!prefill_supported(a.m, a.n, a.k)) return hipErrorNotSupported;
-    dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM);
-    if (a.fp8)
-        hipLaunchKernelGGL(prefill_kernel<true>, grid, dim3(256), 0, a.stream, a.packed, a.scales, a.xq, a.xs, a.y,
-                           a.m, a.n, a.k);
-    else
-        hipLaunchKernelGGL(prefill_kernel<false>, grid, dim3(256), 0, a.stream, a.packed, a.scales, a.xq, a.xs, a.y,
-                           a.m, a.n, a.k);
-    return hipGetLastError();
+    return a.fp8 ? dispatch<true>(a) : dispatch<false>(a);
 }
 
 }  // namespace mx4

@@ -174,6 +174,84 @@ hipError_t launch_quantize_fp8(const void* in, bool in_bf16, uint64_t rows, uint
     return hipGetLastError();
 }
 
+// Fragment-native output (prefill.hip): the same rules as above, one thread
+// per 32-element block, stores addressed for the matrix-core fragments.
+template <bool BF16, bool FP8>
+__global__ __launch_bounds__(256) void quantize_fragments_kernel(const void* __restrict__ in, uint64_t blocks,
+                                                                 uint32_t cols, uint8_t* __restrict__ codes,
+                                                                 uint8_t* __restrict__ scales,
+                                                                 uint32_t* __restrict__ bad) {
+    const uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= blocks) return;
+    float v[32];
+    load_block32<BF16>(in, b, v);
+    float amax = 0.0f;
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        float a = __builtin_fabsf(v[i]);
+        finite &= a <= 3.40282347e38f;
+        amax = a > amax ? a : amax;
+    }
+    if (!finite) atomicOr(bad, 1u);
+    const uint32_t nblk = cols / 32, nk = cols / 64, nq = cols / 256;
+    const uint64_t row = b / nblk;
+    const uint32_t blk = (uint32_t)(b % nblk);
+    const uint64_t g = row / 32;
+    const uint32_t r32 = (uint32_t)(row % 32), kk = blk / 2, half = blk % 2;
+    uint32_t s;
+    if constexpr (FP8) {
+        s = fp8_scale_byte(amax);
+        // bytes [16p, 16p + 16) of the block belong to lane group p, in the
+        // first (block 2kk) or second (block 2kk + 1) KiB of the fragment
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            u32x4 out;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) word |= e4m3_code(v[16 * p + 4 * d + i], s) << (8 * i);
+                out[d] = word;
+            }
+            *reinterpret_cast<u32x4*>(codes + (g * nk + kk) * 2048 + half * 1024 + (32 * p + r32) * 16) = out;
+        }
+    } else {
+        s = mxfp4_scale_byte(amax);
+        u32x4 out;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) word |= mxfp4_code(v[8 * d + i], s) << (4 * i);
+            out[d] = word;
+        }
+        *reinterpret_cast<u32x4*>(codes + ((g * nk + kk) * 64 + 32 * half + r32) * 16) = out;
+    }
+    // block 8q + 2u + h: byte u of lane 32h + r32 of quad q
+    const uint32_t q = blk / 8, u = (blk % 8) / 2, h = blk % 2;
+    scales[((g * nq + q) * 64 + 32 * h + r32) * 4 + u] = (uint8_t)s;
+}
+
+hipError_t launch_quantize_fragments(const void* in, bool in_bf16, uint32_t rows, uint32_t cols, bool fp8,
+                                     uint8_t* codes_f, uint8_t* scales_f, uint32_t* bad, hipStream_t s) {
+    const uint64_t blocks = (uint64_t)rows * (cols / 32);
+    if (blocks == 0) return hipSuccess;
+    dim3 grid((unsigned)((blocks + 255) / 256));
+    if (in_bf16) {
+        if (fp8)
+            hipLaunchKernelGGL((quantize_fragments_kernel<true, true>), grid, dim3(256), 0, s, in, blocks, cols, codes_f, scales_f, bad);
+        else
+            hipLaunchKernelGGL((quantize_fragments_kernel<true, false>), grid, dim3(256), 0, s, in, blocks, cols, codes_f, scales_f, bad);
+    } else {
+        if (fp8)
+            hipLaunchKernelGGL((quantize_fragments_kernel<false, true>), grid, dim3(256), 0, s, in, blocks, cols, codes_f, scales_f, bad);
+        else
+            hipLaunchKernelGGL((quantize_fragments_kernel<false, false>), grid, dim3(256), 0, s, in, blocks, cols, codes_f, scales_f, bad);
+    }
+    return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ dequantize
 
 // engine/src/mxfp4.rs:35-49: one thread per packed byte -> two f32 values.

@@ -65,6 +65,10 @@ struct mx4_weight {
     uint8_t* scales;
     void* allocation;  // owned device memory, or nullptr when wrapped
     uint32_t min_scale, max_scale;
+    // fragment-native copy for the block-scaled MFMA path (built on first use
+    // or by mx4_weight_prepare_prefill): codes, then scales at frag_scales
+    uint8_t* frag = nullptr;
+    uint8_t* frag_scales = nullptr;
 };
 
 struct mx4_pass {
@@ -145,10 +149,35 @@ mx4_status ensure_buffer(mx4_context* ctx, void** buf, uint64_t* cap, uint64_t n
     return MX4_OK;
 }
 
-// requantized activations (FP4 or FP8 codes, 256-byte aligned) followed by their scales
+// requantized activations in the fragment-native layout (FP4 or FP8 codes,
+// 256-byte aligned) followed by their scales
 uint64_t prefill_workspace_bytes(uint64_t m, uint64_t cols, bool fp8) {
-    const uint64_t qbytes = m * cols / (fp8 ? 1 : 2);
-    return ((qbytes + 255) & ~255ull) + m * cols / 32;
+    const uint64_t qbytes = mx4::fragment_bytes((uint32_t)m, (uint32_t)cols, fp8);
+    return ((qbytes + 255) & ~255ull) + mx4::fragment_scale_bytes((uint32_t)m, (uint32_t)cols);
+}
+
+// The weight's fragment-native copy: built once, outside any recorded pass.
+mx4_status prepare_fragments(mx4_context* ctx, mx4_weight* w) {
+    if (w->frag) return MX4_OK;
+    if (w->cols % 256 != 0) return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return fail(MX4_ERR_NO_MEMORY,
+                    "the weight's MFMA layout is built on first use; call mx4_weight_prepare_prefill before recording");
+    const uint64_t cbytes = (mx4::fragment_bytes(w->rows, w->cols, false) + 255) & ~255ull;
+    const uint64_t total = cbytes + mx4::fragment_scale_bytes(w->rows, w->cols);
+    void* p = nullptr;
+    if (hipMalloc(&p, total) != hipSuccess)
+        return fail(MX4_ERR_NO_MEMORY, "could not allocate %llu bytes of device memory", (unsigned long long)total);
+    uint8_t* f = static_cast<uint8_t*>(p);
+    hipError_t e = mx4::launch_to_fragments(w->packed, w->scales, w->rows, w->cols, false, f, f + cbytes, ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return fail(MX4_ERR_DEVICE, "layout launch failed: %s", hipGetErrorString(e));
+    }
+    w->frag = f;
+    w->frag_scales = f + cbytes;
+    return MX4_OK;
 }
 
 mx4_status check_matmul_args(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
@@ -430,12 +459,19 @@ mx4_status mx4_weight_wrap(mx4_context* ctx, const uint8_t* packed_dev, const ui
 
 void mx4_weight_release(mx4_weight* w) {
     if (!w) return;
-    if (w->allocation) {
+    if (w->allocation || w->frag) {
         DeviceGuard g(w->ctx->device);
         (void)hipStreamSynchronize(w->ctx->stream);
-        (void)hipFree(w->allocation);
+        if (w->allocation) (void)hipFree(w->allocation);
+        if (w->frag) (void)hipFree(w->frag);
     }
     delete w;
+}
+
+mx4_status mx4_weight_prepare_prefill(mx4_weight* w) {
+    if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
+    DeviceGuard g(w->ctx->device);
+    return prepare_fragments(w->ctx, w);
 }
 
 mx4_status mx4_weight_info(const mx4_weight* w, uint32_t* rows, uint32_t* cols, const uint8_t** packed_dev,
@@ -540,16 +576,17 @@ mx4_status mx4_matmul_prefill(mx4_context* ctx, const void* x, mx4_dtype xt, uin
         return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
     DeviceGuard g(ctx->device);
     const bool fp8 = act == MX4_ACT_MXFP8;
-    const uint64_t qbytes = (uint64_t)m * w->cols / (fp8 ? 1 : 2);
-    const uint64_t qoff = (qbytes + 255) & ~255ull;
+    mx4_weight* wm = const_cast<mx4_weight*>(w);  // the fragment copy is a cache of the weight
+    st = prepare_fragments(ctx, wm);
+    if (st != MX4_OK) return st;
+    const uint64_t qoff = (mx4::fragment_bytes(m, w->cols, fp8) + 255) & ~255ull;
     st = ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(m, w->cols, fp8));
     if (st != MX4_OK) return st;
-    uint8_t* xq = static_cast<uint8_t*>(ctx->work);
-    uint8_t* xs = xq + qoff;
-    hipError_t e = fp8 ? mx4::launch_quantize_fp8(x, xt == MX4_BF16, m, w->cols, xq, xs, ctx->flags, ctx->stream)
-                       : mx4::launch_quantize_mxfp4(x, xt == MX4_BF16, m, w->cols, xq, xs, ctx->flags, ctx->stream);
+    uint8_t* xf = static_cast<uint8_t*>(ctx->work);
+    uint8_t* xsf = xf + qoff;
+    hipError_t e = mx4::launch_quantize_fragments(x, xt == MX4_BF16, m, w->cols, fp8, xf, xsf, ctx->flags, ctx->stream);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "requantize launch failed: %s", hipGetErrorString(e));
-    mx4::PrefillArgs a{w->packed, w->scales, xq, xs, y, m, w->rows, w->cols, fp8, ctx->stream};
+    mx4::PrefillArgs a{wm->frag, wm->frag_scales, xf, xsf, y, m, w->rows, w->cols, fp8, ctx->stream};
     e = mx4::launch_prefill(a, ctx->cus);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
     return MX4_OK;
@@ -630,7 +667,62 @@ mx4_status mx4_matmul_mx(mx4_context* ctx, const uint8_t* xq, const uint8_t* xs,
     if (!mx4::prefill_supported(m, w->rows, w->cols))
         return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
     DeviceGuard g(ctx->device);
-    mx4::PrefillArgs a{w->packed, w->scales, xq, xs, y, m, w->rows, w->cols, act == MX4_ACT_MXFP8, ctx->stream};
+    const bool fp8 = act == MX4_ACT_MXFP8;
+    mx4_weight* wm = const_cast<mx4_weight*>(w);
+    mx4_status st = prepare_fragments(ctx, wm);
+    if (st != MX4_OK) return st;
+    const uint64_t qoff = (mx4::fragment_bytes(m, w->cols, fp8) + 255) & ~255ull;
+    st = ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(m, w->cols, fp8));
+    if (st != MX4_OK) return st;
+    uint8_t* xf = static_cast<uint8_t*>(ctx->work);
+    uint8_t* xsf = xf + qoff;
+    hipError_t e = mx4::launch_to_fragments(xq, xs, m, w->cols, fp8, xf, xsf, ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "layout launch failed: %s", hipGetErrorString(e));
+    mx4::PrefillArgs a{wm->frag, wm->frag_scales, xf, xsf, y, m, w->rows, w->cols, fp8, ctx->stream};
+    e = mx4::launch_prefill(a, ctx->cus);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status mx4_prefill_act_bytes(uint32_t m, uint32_t cols, mx4_act_format act, uint64_t* codes_bytes,
+                                 uint64_t* scales_bytes) {
+    if (!codes_bytes || !scales_bytes) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
+    if (m == 0 || cols % 256 != 0) return fail(MX4_ERR_SHAPE, "need m >= 1 and cols %% 256 == 0");
+    *codes_bytes = mx4::fragment_bytes(m, cols, act == MX4_ACT_MXFP8);
+    *scales_bytes = mx4::fragment_scale_bytes(m, cols);
+    return MX4_OK;
+}
+
+mx4_status mx4_prefill_quantize(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, uint32_t cols,
+                                mx4_act_format act, uint8_t* codes, uint8_t* scales) {
+    if (!ctx || !x || !codes || !scales) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (xt != MX4_F32 && xt != MX4_BF16) return fail(MX4_ERR_ARGUMENT, "bad activation dtype %d", (int)xt);
+    if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
+    if (m == 0 || cols % 256 != 0) return fail(MX4_ERR_SHAPE, "need m >= 1 and cols %% 256 == 0");
+    if (((uintptr_t)x & 15) != 0 || ((uintptr_t)codes & 15) != 0 || ((uintptr_t)scales & 3) != 0)
+        return fail(MX4_ERR_ARGUMENT, "x and codes must be 16-byte aligned, scales 4-byte aligned");
+    DeviceGuard g(ctx->device);
+    hipError_t e = mx4::launch_quantize_fragments(x, xt == MX4_BF16, m, cols, act == MX4_ACT_MXFP8, codes, scales,
+                                                  ctx->flags, ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "requantize launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status mx4_prefill_matmul(mx4_context* ctx, const uint8_t* codes, const uint8_t* scales, mx4_act_format act,
+                              uint32_t m, const mx4_weight* w, float* y) {
+    if (!ctx || !codes || !scales || !w || !y) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
+    if (m == 0) return fail(MX4_ERR_ARGUMENT, "m must be at least 1");
+    if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
+    if (!mx4::prefill_supported(m, w->rows, w->cols))
+        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
+    DeviceGuard g(ctx->device);
+    mx4_weight* wm = const_cast<mx4_weight*>(w);
+    mx4_status st = prepare_fragments(ctx, wm);
+    if (st != MX4_OK) return st;
+    mx4::PrefillArgs a{wm->frag, wm->frag_scales, codes, scales, y, m, w->rows, w->cols, act == MX4_ACT_MXFP8,
+                       ctx->stream};
     hipError_t e = mx4::launch_prefill(a, ctx->cus);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
     return MX4_OK;

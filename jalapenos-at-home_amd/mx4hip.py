@@ -65,6 +65,10 @@ SIGNATURES = {
     "mx4_matmul_batch": (_int, [_vp, _vp, _u32]),
     "mx4_matmul_mx": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
     "mx4_reserve_prefill": (_int, [_vp, _u32, _u32]),
+    "mx4_weight_prepare_prefill": (_int, [_vp]),
+    "mx4_prefill_act_bytes": (_int, [_u32, _u32, _int, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "mx4_prefill_quantize": (_int, [_vp, _vp, _int, _u32, _u32, _int, _vp, _vp]),
+    "mx4_prefill_matmul": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
     "mx4_pass_begin": (_int, [_vp]),
     "mx4_pass_end": (_int, [_vp, ctypes.POINTER(_vp)]),
     "mx4_pass_launch": (_int, [_vp, _vp]),
@@ -186,6 +190,10 @@ class Weight:
     @property
     def nbytes(self) -> int:
         return self.rows * self.cols // 2 + self.rows * self.cols // 32
+
+    def prepare_prefill(self) -> None:
+        """Build the matrix-core operand copy now (needed before recording prefill into a pass)."""
+        check(lib().mx4_weight_prepare_prefill(self.handle))
 
     def release(self) -> None:
         # a weight never outlives its context (release after destroy is a use-after-free)
@@ -315,10 +323,14 @@ class Context:
         check(lib().mx4_pass_begin(self.handle))
         try:
             fn()
-        finally:
+        except BaseException:
+            # end the capture and drop what was recorded
             h = _vp()
-            st = lib().mx4_pass_end(self.handle, ctypes.byref(h))
-        check(st)
+            if lib().mx4_pass_end(self.handle, ctypes.byref(h)) == 0 and h.value:
+                lib().mx4_pass_release(h.value)
+            raise
+        h = _vp()
+        check(lib().mx4_pass_end(self.handle, ctypes.byref(h)))
         return Pass(self, h.value)
 
     def reserve_prefill(self, max_m: int, max_cols: int) -> None:
@@ -326,6 +338,20 @@ class Context:
 
     def matmul_mx(self, xq: DeviceBuffer, xs: DeviceBuffer, act: int, m: int, w: Weight, y: DeviceBuffer) -> None:
         check(lib().mx4_matmul_mx(self.handle, xq.ptr, xs.ptr, act, m, w.handle, y.ptr))
+
+    def prefill_act_buffers(self, m: int, cols: int, act: int) -> "tuple[DeviceBuffer, DeviceBuffer]":
+        """Device buffers for activations requantized in the matrix-core layout."""
+        cb, sb = ctypes.c_uint64(), ctypes.c_uint64()
+        check(lib().mx4_prefill_act_bytes(m, cols, act, ctypes.byref(cb), ctypes.byref(sb)))
+        return self.buffer(cb.value), self.buffer(sb.value)
+
+    def prefill_quantize(self, x: DeviceBuffer, xtype: int, m: int, cols: int, act: int, codes: DeviceBuffer,
+                         scales: DeviceBuffer) -> None:
+        check(lib().mx4_prefill_quantize(self.handle, x.ptr, xtype, m, cols, act, codes.ptr, scales.ptr))
+
+    def prefill_matmul(self, codes: DeviceBuffer, scales: DeviceBuffer, act: int, m: int, w: Weight,
+                       y: DeviceBuffer) -> None:
+        check(lib().mx4_prefill_matmul(self.handle, codes.ptr, scales.ptr, act, m, w.handle, y.ptr))
 
     def dequantize(self, w: Weight, out: DeviceBuffer) -> None:
         check(lib().mx4_dequantize(self.handle, w.handle, out.ptr))

@@ -532,7 +532,8 @@ def test_prefill_identity_is_exact(mx4, ctx, oracle, act):
 
 
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
-@pytest.mark.parametrize("m,n,k", [(1, 32, 256), (7, 200, 512), (64, 128, 1024), (130, 96, 256), (256, 256, 4096)])
+@pytest.mark.parametrize("m,n,k", [(1, 32, 256), (7, 200, 512), (64, 128, 1024), (130, 96, 256), (256, 256, 4096),
+                                   (70, 8256, 512), (33, 64, 12288)])
 def test_prefill_matches_oracle_on_requantized_x(mx4, ctx, oracle, act, m, n, k):
     rng = np.random.default_rng(m * 7 + n)
     w = ctx.synth_weight(50 + m, n, k, 0.02)
@@ -542,6 +543,67 @@ def test_prefill_matches_oracle_on_requantized_x(mx4, ctx, oracle, act, m, n, k)
     for xtype in (mx4.BF16, mx4.F32):
         y = _run_prefill(mx4, ctx, x, w, act, xtype)
         assert_close(y, ref, f"prefill {act} m={m} n={n} k={k} xtype={xtype}")
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+def test_prefill_mx_entry_matches_prefill(mx4, ctx, oracle, act):
+    """mx4_matmul_mx takes row-major requantized activations (what mx4_quantize
+    writes) and rearranges them for the matrix core itself: same bits as the
+    fused requantize + GEMM of mx4_matmul_prefill."""
+    m, n, k = 45, 160, 1024
+    w = ctx.synth_weight(71, n, k, 0.02)
+    x = oracle.bf16_to_f32(oracle.synth_bf16(72, 1.0, m * k)).reshape(m, k)
+    y_ref = _run_prefill(mx4, ctx, x, w, act, mx4.F32)
+    xb = ctx.to_device(np.ascontiguousarray(x, np.float32))
+    fp8 = act == "mxfp8"
+    xq = ctx.buffer(m * k if fp8 else m * k // 2)
+    xs = ctx.buffer(m * k // 32)
+    (ctx.quantize_fp8 if fp8 else ctx.quantize)(xb, mx4.F32, m, k, xq, xs)
+    yb = ctx.buffer(m * n * 4)
+    ctx.matmul_mx(xq, xs, mx4.ACT_MXFP8 if fp8 else mx4.ACT_MXFP4, m, w, yb)
+    assert np.array_equal(yb.download(np.float32).reshape(m, n), y_ref)
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+def test_prefill_quantize_once_matmul_many(mx4, ctx, oracle, act):
+    """Requantize x once in the matrix-core layout and reuse it for two weights
+    (q|k|v style): each product equals the fused mx4_matmul_prefill bit for bit."""
+    m, k = 77, 2048
+    code = mx4.ACT_MXFP4 if act == "mxfp4" else mx4.ACT_MXFP8
+    x = oracle.bf16_to_f32(oracle.synth_bf16(91, 1.0, m * k)).reshape(m, k)
+    xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+    codes, scales = ctx.prefill_act_buffers(m, k, code)
+    ctx.prefill_quantize(xb, mx4.BF16, m, k, code, codes, scales)
+    for seed, n in ((92, 320), (93, 96)):
+        w = ctx.synth_weight(seed, n, k, 0.02)
+        yb = ctx.buffer(m * n * 4)
+        ctx.prefill_matmul(codes, scales, code, m, w, yb)
+        assert np.array_equal(yb.download(np.float32).reshape(m, n), _run_prefill(mx4, ctx, x, w, act, mx4.BF16))
+
+
+def test_prefill_recorded_pass_after_prepare(mx4, ctx, oracle):
+    """The matrix-core copy of a weight is built outside the pass
+    (mx4_weight_prepare_prefill) and the workspace reserved; every replay of the
+    recorded prefill equals the eager result. Without the prepare the recording
+    fails with an error instead of allocating."""
+    m, n, k = 96, 256, 2048
+    w = ctx.synth_weight(81, n, k, 0.02)
+    x = oracle.bf16_to_f32(oracle.synth_bf16(82, 1.0, m * k)).reshape(m, k)
+    xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+    yb = ctx.buffer(m * n * 4)
+    w2 = ctx.synth_weight(83, n, k, 0.02)
+    ctx.reserve_prefill(m, k)
+    with pytest.raises(mx4.Mx4Error, match="prepare"):
+        ctx.record(lambda: ctx.matmul_prefill(xb, mx4.BF16, m, w2, mx4.ACT_MXFP4, yb))
+    w.prepare_prefill()
+    eager = _run_prefill(mx4, ctx, x, w, "mxfp4", mx4.BF16)
+    p = ctx.record(lambda: ctx.matmul_prefill(xb, mx4.BF16, m, w, mx4.ACT_MXFP4, yb))
+    for _ in range(3):
+        yb.upload(np.zeros(m * n, np.float32))
+        p.launch()
+        ctx.synchronize()
+        assert np.array_equal(yb.download(np.float32).reshape(m, n), eager)
+    p.release()
 
 
 def test_prefill_8b_shapes_sampled(mx4, ctx, oracle):
