@@ -227,6 +227,9 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--profile-traffic", action="store_true",
                     help="for counter runs: 2 eager grouped steps, then a 1 GiB device copy as the byte calibration")
+    ap.add_argument("--profile-prefill", action="store_true",
+                    help="for profiler runs: only the M=512 prefill GEMMs (q, o, gate, up, down; MXFP4 and "
+                         "MX-FP8 activations), 5 launches each on requantized activations")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -275,6 +278,27 @@ def main() -> int:
     else:
         enqueue = enqueue_grouped
         launches = LAYERS * 4 + 1
+    if args.profile_prefill:
+        m = 512
+        by = {}
+        for (nm, n, k, w) in weights:
+            by.setdefault(nm, (n, k, w))
+        for name in ("q", "o", "gate", "up", "down"):
+            n, k, w = by[name]
+            w.prepare_prefill()
+            xb = ctx.buffer(m * k * 2)
+            ctx.synth_bf16(3, 1.0, m * k, xb)
+            yb = ctx.buffer(m * n * 4)
+            for code in (mx4hip.ACT_MXFP4, mx4hip.ACT_MXFP8):
+                xq, xsc = ctx.prefill_act_buffers(m, k, code)
+                ctx.prefill_quantize(xb, mx4hip.BF16, m, k, code, xq, xsc)
+                for _ in range(5):
+                    ctx.prefill_matmul(xq, xsc, code, m, w, yb)
+            ctx.synchronize()
+        print(json.dumps({"profile_prefill": True, "m": m, "launches_per_shape_and_format": 5}), flush=True)
+        ctx.close()
+        return 0
+
     if args.profile_traffic:
         for _ in range(2):
             enqueue()
