@@ -83,7 +83,7 @@ void qwen_hip_destroy(void *context);
 /* Replaces qwen_metal_matmul (engine/src/metal.rs:9-18, engine/src/metal.m:54-117).
  * y[rows][cols] = x[rows][inner] . W[cols][inner]^T. scales != NULL: w is packed
  * MXFP4 [cols][inner/2] with scales [cols][inner/32]; scales == NULL: w is bf16
- * [cols][inner]. Device copies of w and scales are cached by host pointer (the
+ * [cols][inner] (both arms supported). Device copies of w and scales are cached by host pointer (the
  * caller keeps them immutable, engine/src/metal.rs:33). Synchronous: y is valid
  * on return. Returns false on any failure. */
 bool qwen_hip_matmul(void *context, const float *x, const void *w, const uint8_t *scales,
@@ -129,6 +129,13 @@ mx4_status mx4_copy(mx4_context *ctx, void *dev_dst, const void *dev_src, uint64
  * copies packed + scales into HBM once; the weight stays resident. */
 mx4_status mx4_weight_upload(mx4_context *ctx, const uint8_t *packed, const uint8_t *scales,
                              uint32_t rows, uint32_t cols, mx4_weight **out);
+/* Tensor::bf16 (engine/src/lib.rs:43-49): a bf16 weight [rows][cols], copied
+ * into HBM once. mx4_matmul / mx4_matmul_group multiply with it exactly as the
+ * reference's bf16 arm (engine/src/lib.rs:255) does, f32 accumulation; the
+ * MXFP4-only entry points (GEMV configurations, prefill, dequantize) reject it,
+ * and mx4_weight_info reports null packed/scales for it. */
+mx4_status mx4_weight_upload_bf16(mx4_context *ctx, const uint16_t *data, uint32_t rows, uint32_t cols,
+                                  mx4_weight **out);
 /* Wrap packed/scales already in HBM (not copied, not freed by release). The
  * scale bytes are scanned on device; a 255 byte fails with MX4_ERR_NAN_SCALE. */
 mx4_status mx4_weight_wrap(mx4_context *ctx, const uint8_t *packed_dev, const uint8_t *scales_dev,

@@ -44,6 +44,10 @@ hipError_t launch_gemv_generic(const GemvArgs& a);
 bool skinny_supported(uint32_t m, uint32_t k);
 hipError_t launch_skinny(const GemvArgs& a, int cus);
 
+// bf16 weights [n][k] (engine/src/lib.rs:255, None arm), any m, f32 accumulation.
+hipError_t launch_bf16_matmul(const uint16_t* w, const void* x, bool x_bf16, float* y, uint32_t m, uint32_t n,
+                              uint32_t k, hipStream_t s);
+
 // Block-scaled MFMA prefill on requantized activations. Both operands are in
 // the fragment-native layout of prefill.hip (launch_to_fragments, or the
 // quantizers' fragment output).

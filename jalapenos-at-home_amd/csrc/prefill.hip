@@ -179,8 +179,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int r = 0; r < RS - 1; ++r) issue_scales(r, sa[r], sb[r]);
 #pragma unroll
     for (int j = 0; j < Q; ++j) issue(j, sl[j]);
-#pragma unroll
-    for (uint32_t base = 0; base < nk; base += Q * U) {
+    // one turn of the ring: Q slots of U k-steps starting at k-step `base`
+    auto turn = [&](uint32_t base) {
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
 #pragma unroll
@@ -201,6 +201,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             issue(base / U + j + Q, sl[j]);
             __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    if constexpr (NKC != 0) {
+        // straight-line code: the wait counts stay exact (in a loop the compiler
+        // waits for every outstanding load at the loop head)
+#pragma unroll
+        for (uint32_t base = 0; base < (uint32_t)NKC; base += Q * U) turn(base);
+    } else {
+        for (uint32_t base = 0; base < nk; base += Q * U) turn(base);
     }
     mfma_drain();
 

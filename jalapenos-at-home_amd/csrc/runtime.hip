@@ -69,6 +69,9 @@ struct mx4_weight {
     // or by mx4_weight_prepare_prefill): codes, then scales at frag_scales
     uint8_t* frag = nullptr;
     uint8_t* frag_scales = nullptr;
+    // bf16 weight [rows][cols] (a Tensor::bf16 of the reference); packed and
+    // scales are null for such a weight
+    uint16_t* bf16 = nullptr;
 };
 
 struct mx4_pass {
@@ -159,6 +162,7 @@ uint64_t prefill_workspace_bytes(uint64_t m, uint64_t cols, bool fp8) {
 // The weight's fragment-native copy: built once, outside any recorded pass.
 mx4_status prepare_fragments(mx4_context* ctx, mx4_weight* w) {
     if (w->frag) return MX4_OK;
+    if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
     if (w->cols % 256 != 0) return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
@@ -200,6 +204,14 @@ bool scales_foldable(const mx4_weight* w) { return w->min_scale >= 2 && w->max_s
 
 mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, const mx4_weight* w,
                       float* y, mx4_path path) {
+    if (w->bf16) {
+        // engine/src/lib.rs:255 `None` arm: one exact kernel for every M
+        if (path != MX4_PATH_AUTO && path != MX4_PATH_GENERIC)
+            return fail(MX4_ERR_UNSUPPORTED, "bf16 weights run on the generic path only");
+        hipError_t e = mx4::launch_bf16_matmul(w->bf16, x, xt == MX4_BF16, y, m, w->rows, w->cols, ctx->stream);
+        if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
+        return MX4_OK;
+    }
     mx4::GemvArgs a{w->packed, w->scales, x, y, m, w->rows, w->cols, xt == MX4_BF16, ctx->stream};
     if (path == MX4_PATH_AUTO) {
         if (m == 1 && mx4::gemv_m1_supported(w->cols) && scales_foldable(w))
@@ -474,6 +486,33 @@ mx4_status mx4_weight_prepare_prefill(mx4_weight* w) {
     return prepare_fragments(w->ctx, w);
 }
 
+mx4_status mx4_weight_upload_bf16(mx4_context* ctx, const uint16_t* data, uint32_t rows, uint32_t cols,
+                                  mx4_weight** out) {
+    if (!ctx || !out || !data) return fail(MX4_ERR_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (rows == 0 || cols == 0) return fail(MX4_ERR_SHAPE, "empty weight");
+    const uint64_t bytes = (uint64_t)rows * cols * 2;
+    DeviceGuard g(ctx->device);
+    void* mem = nullptr;
+    if (hipMalloc(&mem, bytes) != hipSuccess)
+        return fail(MX4_ERR_NO_MEMORY, "could not allocate %llu bytes for a weight", (unsigned long long)bytes);
+    if (hipMemcpyAsync(mem, data, bytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        (void)hipFree(mem);
+        return fail(MX4_ERR_DEVICE, "weight upload failed");
+    }
+    mx4_weight* w = nullptr;
+    mx4_status st = new_weight(ctx, rows, cols, &w);
+    if (st != MX4_OK) {
+        (void)hipFree(mem);
+        return st;
+    }
+    w->allocation = mem;
+    w->bf16 = static_cast<uint16_t*>(mem);
+    *out = w;
+    return MX4_OK;
+}
+
 mx4_status mx4_weight_info(const mx4_weight* w, uint32_t* rows, uint32_t* cols, const uint8_t** packed_dev,
                            const uint8_t** scales_dev) {
     if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
@@ -543,6 +582,7 @@ mx4_status mx4_gemv_config(mx4_context* ctx, const void* x, mx4_dtype xt, const 
         mx4_status st = check_matmul_args(ctx, x, xt, 1, w[i], y[i]);
         if (st != MX4_OK) return st;
         if (w[i]->cols != w[0]->cols) return fail(MX4_ERR_SHAPE, "grouped weights must share their width");
+        if (w[i]->bf16) return fail(MX4_ERR_UNSUPPORTED, "the GEMV configurations are for MXFP4 weights");
         if (!scales_foldable(w[i])) return fail(MX4_ERR_UNSUPPORTED, "scale bytes outside 2..252 need the generic kernel");
         gg.packed[i] = w[i]->packed;
         gg.scales[i] = w[i]->scales;
@@ -572,6 +612,7 @@ mx4_status mx4_matmul_prefill(mx4_context* ctx, const void* x, mx4_dtype xt, uin
     mx4_status st = check_matmul_args(ctx, x, xt, m, w, y);
     if (st != MX4_OK) return st;
     if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
+    if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
     if (!mx4::prefill_supported(m, w->rows, w->cols))
         return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
     DeviceGuard g(ctx->device);
@@ -664,6 +705,7 @@ mx4_status mx4_matmul_mx(mx4_context* ctx, const uint8_t* xq, const uint8_t* xs,
     if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
     if (m == 0) return fail(MX4_ERR_ARGUMENT, "m must be at least 1");
     if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
+    if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
     if (!mx4::prefill_supported(m, w->rows, w->cols))
         return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
     DeviceGuard g(ctx->device);
@@ -715,6 +757,7 @@ mx4_status mx4_prefill_matmul(mx4_context* ctx, const uint8_t* codes, const uint
     if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
     if (m == 0) return fail(MX4_ERR_ARGUMENT, "m must be at least 1");
     if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
+    if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
     if (!mx4::prefill_supported(m, w->rows, w->cols))
         return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
     DeviceGuard g(ctx->device);
@@ -730,6 +773,7 @@ mx4_status mx4_prefill_matmul(mx4_context* ctx, const uint8_t* codes, const uint
 
 mx4_status mx4_dequantize(mx4_context* ctx, const mx4_weight* w, float* out) {
     if (!ctx || !w || !out) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "not an MXFP4 weight");
     DeviceGuard g(ctx->device);
     hipError_t e = mx4::launch_dequantize(w->packed, w->scales, (uint64_t)w->rows * w->cols, out, ctx->stream);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "dequantize launch failed: %s", hipGetErrorString(e));
@@ -853,18 +897,16 @@ bool qwen_hip_matmul(void* context, const float* x, const void* w, const uint8_t
         fail(MX4_ERR_ARGUMENT, "empty matmul");
         return false;
     }
-    if (!scales) {
-        fail(MX4_ERR_UNSUPPORTED, "bf16 weights (scales == NULL) are not supported by this backend yet");
-        return false;
-    }
     DeviceGuard g(ctx->device);
     CacheKey key{w, scales, cols, inner};
     auto it = ctx->cache.find(key);
     mx4_weight* weight = nullptr;
     if (it == ctx->cache.end()) {
-        if (mx4_weight_upload(ctx, static_cast<const uint8_t*>(w), scales, cols, inner, &weight) != MX4_OK)
-            return false;
-        uint64_t bytes = (uint64_t)cols * inner / 2 + (uint64_t)cols * inner / 32;
+        // scales == NULL: w is bf16 [cols][inner] (engine/src/metal.rs:45-50)
+        const mx4_status up = scales ? mx4_weight_upload(ctx, static_cast<const uint8_t*>(w), scales, cols, inner, &weight)
+                                     : mx4_weight_upload_bf16(ctx, static_cast<const uint16_t*>(w), cols, inner, &weight);
+        if (up != MX4_OK) return false;
+        uint64_t bytes = scales ? (uint64_t)cols * inner / 2 + (uint64_t)cols * inner / 32 : (uint64_t)cols * inner * 2;
         ctx->lru.push_front(key);
         ctx->cache.emplace(key, CacheEntry{weight, bytes, ctx->lru.begin()});
         ctx->cache_bytes += bytes;

@@ -30,6 +30,7 @@ ACT_MXFP4, ACT_MXFP8 = 1, 2
 _vp = ctypes.c_void_p
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _f32p = ctypes.POINTER(ctypes.c_float)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
 _u32 = ctypes.c_uint32
 _u64 = ctypes.c_uint64
 _int = ctypes.c_int
@@ -66,6 +67,7 @@ SIGNATURES = {
     "mx4_matmul_mx": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
     "mx4_reserve_prefill": (_int, [_vp, _u32, _u32]),
     "mx4_weight_prepare_prefill": (_int, [_vp]),
+    "mx4_weight_upload_bf16": (_int, [_vp, _vp, _u32, _u32, ctypes.POINTER(_vp)]),
     "mx4_prefill_act_bytes": (_int, [_u32, _u32, _int, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
     "mx4_prefill_quantize": (_int, [_vp, _vp, _int, _u32, _u32, _int, _vp, _vp]),
     "mx4_prefill_matmul": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
@@ -248,6 +250,13 @@ class Context:
                                       ctypes.byref(h)))
         return self._track(Weight(self, h.value, rows, cols))
 
+    def upload_weight_bf16(self, bits: np.ndarray, rows: int, cols: int) -> Weight:
+        """Tensor::bf16: bf16 bit patterns [rows][cols], resident in HBM."""
+        bits = np.ascontiguousarray(bits, dtype=np.uint16)
+        h = _vp()
+        check(lib().mx4_weight_upload_bf16(self.handle, _ptr(bits, _u16p), rows, cols, ctypes.byref(h)))
+        return self._track(Weight(self, h.value, rows, cols))
+
     def _track(self, w: Weight) -> Weight:
         self._weights.add(w)
         return w
@@ -413,13 +422,22 @@ class Hip:
         if not self.handle:
             raise RuntimeError(f"could not initialize HIP: {last_error()}")
 
-    def matmul(self, x: np.ndarray, packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    def matmul(self, x: np.ndarray, w: np.ndarray, scales=None) -> np.ndarray:
+        """w: packed MXFP4 bytes with `scales`, or (scales None) bf16 bits [cols][inner]
+        -- the two arms of engine/src/metal.rs:40-51. The arrays must stay alive and
+        unchanged while cached: the device copies are keyed by their address."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         rows, inner = x.shape
-        cols = packed.size * 2 // inner
+        if scales is None:
+            if w.dtype != np.uint16:
+                raise TypeError("bf16 weights are uint16 bit patterns")
+            cols = w.size // inner
+            sp = None
+        else:
+            cols = w.size * 2 // inner
+            sp = _ptr(scales, _u8p)
         y = np.empty((rows, cols), dtype=np.float32)
-        ok = lib().qwen_hip_matmul(self.handle, _ptr(x, _f32p), _ptr(packed), _ptr(scales, _u8p),
-                                   _ptr(y, _f32p), rows, cols, inner)
+        ok = lib().qwen_hip_matmul(self.handle, _ptr(x, _f32p), _ptr(w), sp, _ptr(y, _f32p), rows, cols, inner)
         if not ok:
             raise RuntimeError(f"HIP projection failed: {last_error()}")
         return y

@@ -251,6 +251,50 @@ def test_dropin_matches_cpu_for_decode_and_prefill(mx4, oracle):
         hip.close()
 
 
+def test_dropin_bf16_weights_match_cpu(mx4, oracle):
+    """engine/src/metal.rs:86-114, the bf16 arm: the decoded quantized weight as
+    Tensor::bf16 (scales == NULL), for the same rows, against the reference's
+    bf16 matmul (engine/src/lib.rs:255) and within the test's tolerance."""
+    hip = mx4.Hip()
+    try:
+        packed = (np.arange(21 * 32) % 256).astype(np.uint8)
+        scales = (122 + np.arange(21 * 2) % 7).astype(np.uint8)
+        decoded = oracle.dequantize(packed.reshape(21, 32), scales.reshape(21, 2)).reshape(21, 64)
+        bf16 = (f32_bits(decoded) >> 16).astype(np.uint16)
+        for rows in [1, 2, 4, 8, 16, 19, 33]:
+            x = (((np.arange(rows * 64) % 37) - 18.0) / 19.0).astype(np.float32).reshape(rows, 64)
+            expected = oracle.matmul_bf16(x, bf16)
+            actual = hip.matmul(x, bf16)
+            assert actual.shape == expected.shape
+            assert np.all(np.abs(actual - expected) < 1e-3 + np.abs(expected) * 1e-5), rows
+            # both arms of the same weight agree (the decode is exact in bf16 here)
+            assert np.all(np.abs(actual - hip.matmul(x, packed, scales)) < 1e-3 + np.abs(expected) * 1e-5), rows
+    finally:
+        hip.close()
+
+
+@pytest.mark.parametrize("k", [64, 100, 2048])
+def test_bf16_weight_resident(mx4, ctx, oracle, k):
+    """Tensor::bf16 weights resident in HBM: M in {1, 3, 19, 64}, f32 and bf16
+    activations, against the reference's bf16 arm; K = 100 takes the element-wise
+    form (rows not 16-byte aligned)."""
+    rng = np.random.default_rng(k)
+    n = 150
+    w_bits = (f32_bits(rng.standard_normal((n, k)).astype(np.float32) * 0.05) >> 16).astype(np.uint16)
+    w = ctx.upload_weight_bf16(w_bits, n, k)
+    for m in (1, 3, 19, 64):
+        xf = rng.standard_normal((m, k)).astype(np.float32)
+        xbits = (f32_bits(xf) >> 16).astype(np.uint16)
+        xb16 = (xbits.astype(np.uint32) << 16).view(np.float32)
+        for xt, host, dev in ((mx4.F32, xf, ctx.to_device(xf)), (mx4.BF16, xb16, ctx.to_device(xbits))):
+            yb = ctx.buffer(m * n * 4)
+            ctx.matmul(dev, xt, m, w, yb)
+            assert_close(yb.download(np.float32).reshape(m, n), oracle.matmul_bf16(host, w_bits), f"bf16 k={k} m={m}")
+    with pytest.raises(mx4.Mx4Error, match="MXFP4"):
+        ctx.matmul_prefill(ctx.to_device(np.zeros((4, k), np.float32)), mx4.F32, 4, w, mx4.ACT_MXFP4,
+                           ctx.buffer(4 * n * 4))
+
+
 # ------------------------------------------------------------------ GEMV at model shapes
 
 def _sample_rows(n, count, rng):
