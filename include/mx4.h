@@ -164,11 +164,13 @@ mx4_status mx4_matmul_group(mx4_context *ctx, const void *x_dev, mx4_dtype x_typ
 /* Tuning hook for the M == 1 GEMV over a group of 1 to 4 weights (as
  * mx4_matmul_group): waves per team (the team splits each row's K; K/32 must
  * be a multiple of 64*team), rows per team per iteration (1, 2, 4 or 8, with
- * rows * K/(2048*team) <= 8), and workgroups (0: the default grid). Zero team
- * or rows keep the defaults. */
+ * rows * K/(2048*team) <= 8), teams per workgroup (x is staged once per
+ * workgroup in LDS when more than one; at most 512 threads), and the number of
+ * teams (0: one row-set each). Zero team, rows or teams_per_workgroup keep the
+ * defaults. */
 mx4_status mx4_gemv_config(mx4_context *ctx, const void *x_dev, mx4_dtype x_type,
                            const mx4_weight *const *w, float *const *y_dev, uint32_t count,
-                           int team_waves, int rows_per_team, uint32_t workgroups);
+                           int team_waves, int rows_per_team, int teams_per_workgroup, uint32_t teams);
 
 /* Prefill on CDNA4 block-scaled MFMA (V_MFMA_SCALE_F32_*_F8F6F4): x is
  * requantized per 32 along K (MXFP4 by python/quantize_mxfp4.py:18-39, or MX

@@ -44,6 +44,21 @@ struct LaneX<true, BPL> {
             }
         }
     }
+    // the same blocks from a copy of x staged in LDS
+    __device__ __forceinline__ void load_lds(const uint8_t* xl, uint32_t blk0, uint32_t stride) {
+#pragma unroll
+        for (int j = 0; j < BPL; ++j) {
+            const uint8_t* src = xl + (size_t)(blk0 + j * stride) * 64;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(src + 16 * q);
+                p[j][4 * q + 0] = v[0];
+                p[j][4 * q + 1] = v[1];
+                p[j][4 * q + 2] = v[2];
+                p[j][4 * q + 3] = v[3];
+            }
+        }
+    }
     __device__ __forceinline__ float dot(int j, const u32x4 w) const { return block_dot_bf16(w, p[j]); }
 };
 
@@ -58,6 +73,20 @@ struct LaneX<false, BPL> {
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
                 f32x4 v = *reinterpret_cast<const f32x4*>(src + 4 * q);
+                f[j][4 * q + 0] = v[0];
+                f[j][4 * q + 1] = v[1];
+                f[j][4 * q + 2] = v[2];
+                f[j][4 * q + 3] = v[3];
+            }
+        }
+    }
+    __device__ __forceinline__ void load_lds(const uint8_t* xl, uint32_t blk0, uint32_t stride) {
+#pragma unroll
+        for (int j = 0; j < BPL; ++j) {
+            const float* src = reinterpret_cast<const float*>(xl) + (size_t)(blk0 + j * stride) * 32;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(src + 4 * q);
                 f[j][4 * q + 0] = v[0];
                 f[j][4 * q + 1] = v[1];
                 f[j][4 * q + 2] = v[2];
@@ -283,7 +312,7 @@ __device__ __forceinline__ float row_dot(const LaneX<XBF16, BPL>& xr, const u32x
 template <bool XBF16, int WG, int BPL, int R>
 __device__ __forceinline__ void finish_rowset(const Segs& sg, uint32_t rs, const LaneX<XBF16, BPL>& xr,
                                               const RowSet<XBF16, BPL, R>& cur, uint32_t t,
-                                              float (&red)[2][WG][R], uint32_t& parity) {
+                                              float (*red)[WG][R], uint32_t& parity) {
     const uint32_t wave = t / 64, lane = t % 64;
     float acc[R];
 #pragma unroll
@@ -310,14 +339,24 @@ __device__ __forceinline__ void finish_rowset(const Segs& sg, uint32_t rs, const
     }
 }
 
+// A workgroup holds `tpw` = blockDim.x / (64 WG) independent teams. With more
+// than one, x is staged once per workgroup in LDS and every team reads its
+// blocks from there: each workgroup loads the whole activation row, so fewer,
+// larger workgroups cut that L2 traffic (for o at K = 4096 it matched the
+// weight bytes with one team per workgroup). Dynamic LDS: x (k elements), then
+// the cross-wave partial sums [tpw][2][WG][R].
 template <bool XBF16, int WG, int BPL, int R>
-__global__ __launch_bounds__(64 * WG) void gemv_m1_kernel(Segs sg, const void* __restrict__ x, uint32_t k) {
-    constexpr uint32_t T = 64 * WG;
-    const uint32_t t = threadIdx.x;
+__global__ __launch_bounds__(512) void gemv_m1_kernel(Segs sg, const void* __restrict__ x, uint32_t k) {
+    constexpr uint32_t T = 64 * WG;  // threads per team
+    const uint32_t tpw = blockDim.x / T;
+    const uint32_t team = __builtin_amdgcn_readfirstlane(threadIdx.x / T);
+    const uint32_t t = threadIdx.x % T;
     const uint32_t row_bytes = k / 2;
     const uint32_t nblk = k / 32;
     const uint32_t rowsets = sg.rowsets;
-    uint32_t rs = blockIdx.x;  // the host launches at most `rowsets` teams
+    const uint32_t stride = gridDim.x * tpw;
+    const uint32_t first = blockIdx.x * tpw;  // the workgroup's first team visits the most row-sets
+    uint32_t rs = first + team;               // the host launches at most `rowsets` teams per row-set turn
 
     // Every kernel argument is needed before the first load. Pinning them in
     // SGPRs here makes the compiler fetch them in one scalar round trip
@@ -331,21 +370,37 @@ __global__ __launch_bounds__(64 * WG) void gemv_m1_kernel(Segs sg, const void* _
     RowSet<XBF16, BPL, R> a, b;
     load_rowset<XBF16, WG, BPL, R>(sg, rs, rowsets, t, row_bytes, nblk, a);
     LaneX<XBF16, BPL> xr;
-    xr.load(x, t, T);
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const uint32_t xbytes = k * (XBF16 ? 2 : 4);
+    // the host sizes dynamic LDS as (tpw > 1 ? x : nothing) + tpw * 2 * WG * R floats
+    float(*red)[WG][R] = reinterpret_cast<float(*)[WG][R]>(smem + (tpw > 1 ? xbytes : 0)) + 2 * team;
+    if (tpw == 1) {
+        xr.load(x, t, T);
+    } else {
+        const uint8_t* xg = static_cast<const uint8_t*>(x);
+        for (uint32_t c = threadIdx.x; c < xbytes / 16; c += blockDim.x)
+            *reinterpret_cast<u32x4*>(smem + 16 * c) = load_u32x4(xg + 16 * c);
+        __syncthreads();
+        xr.load_lds(smem, t, T);
+    }
 
-    __shared__ float red[2][WG][R];
     uint32_t parity = 0;
-    // ping-pong: the next row-set streams in while the current one is reduced
-    for (;;) {
-        uint32_t nxt = rs + gridDim.x;
+    // ping-pong: the next row-set streams in while the current one is reduced.
+    // Every team of the workgroup runs as many turns as the first one (the
+    // cross-wave reduction has a workgroup barrier); a team past the end
+    // loads zeros and writes nothing.
+    for (uint32_t rf = first;;) {
+        uint32_t nxt = rs + stride;
         load_rowset<XBF16, WG, BPL, R>(sg, nxt, rowsets, t, row_bytes, nblk, b);
         finish_rowset<XBF16, WG, BPL, R>(sg, rs, xr, a, t, red, parity);
-        if (nxt >= rowsets) break;
+        rf += stride;
+        if (rf >= rowsets) break;
         rs = nxt;
-        nxt = rs + gridDim.x;
+        nxt = rs + stride;
         load_rowset<XBF16, WG, BPL, R>(sg, nxt, rowsets, t, row_bytes, nblk, a);
         finish_rowset<XBF16, WG, BPL, R>(sg, rs, xr, b, t, red, parity);
-        if (nxt >= rowsets) break;
+        rf += stride;
+        if (rf >= rowsets) break;
         rs = nxt;
     }
 }
@@ -415,30 +470,31 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* __rest
 // ------------------------------------------------------------------ launchers
 
 template <bool XBF16, int WG, int BPL, int R>
-static hipError_t go_m1(const Segs& sg, const void* x, uint32_t k, uint32_t grid, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_m1_kernel<XBF16, WG, BPL, R>), dim3(grid), dim3(64 * WG), 0, st, sg, x, k);
+static hipError_t go_m1(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int tpw, hipStream_t st) {
+    const size_t lds = (tpw > 1 ? (size_t)k * (XBF16 ? 2 : 4) : 0) + (size_t)tpw * 2 * WG * R * sizeof(float);
+    hipLaunchKernelGGL((gemv_m1_kernel<XBF16, WG, BPL, R>), dim3(grid), dim3(64 * WG * tpw), lds, st, sg, x, k);
     return hipGetLastError();
 }
 
 // Rows per team allowed for a blocks-per-lane count: R * BPL <= 8 keeps the
 // double-buffered weights within 64 VGPRs.
 template <bool XBF16, int WG, int BPL>
-static hipError_t go_r(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int r, hipStream_t st) {
+static hipError_t go_r(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int r, int tpw, hipStream_t st) {
     switch (r) {
-        case 1: return go_m1<XBF16, WG, BPL, 1>(sg, x, k, grid, st);
-        case 2: if constexpr (BPL <= 4) return go_m1<XBF16, WG, BPL, 2>(sg, x, k, grid, st); break;
-        case 4: if constexpr (BPL <= 2) return go_m1<XBF16, WG, BPL, 4>(sg, x, k, grid, st); break;
-        case 8: if constexpr (BPL <= 1) return go_m1<XBF16, WG, BPL, 8>(sg, x, k, grid, st); break;
+        case 1: return go_m1<XBF16, WG, BPL, 1>(sg, x, k, grid, tpw, st);
+        case 2: if constexpr (BPL <= 4) return go_m1<XBF16, WG, BPL, 2>(sg, x, k, grid, tpw, st); break;
+        case 4: if constexpr (BPL <= 2) return go_m1<XBF16, WG, BPL, 4>(sg, x, k, grid, tpw, st); break;
+        case 8: if constexpr (BPL <= 1) return go_m1<XBF16, WG, BPL, 8>(sg, x, k, grid, tpw, st); break;
         default: break;
     }
     return hipErrorNotSupported;
 }
 
 template <bool XBF16>
-static hipError_t go_cfg(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int wg, int bpl, int r,
+static hipError_t go_cfg(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int wg, int bpl, int r, int tpw,
                          hipStream_t st) {
 #define MX4_M1_CASE(W, B) \
-    if (wg == W && bpl == B) return go_r<XBF16, W, B>(sg, x, k, grid, r, st);
+    if (wg == W && bpl == B) return go_r<XBF16, W, B>(sg, x, k, grid, r, tpw, st);
     MX4_M1_CASE(1, 1) MX4_M1_CASE(1, 2) MX4_M1_CASE(2, 1) MX4_M1_CASE(1, 3) MX4_M1_CASE(3, 1)
     MX4_M1_CASE(1, 4) MX4_M1_CASE(2, 2) MX4_M1_CASE(4, 1) MX4_M1_CASE(1, 6) MX4_M1_CASE(2, 3)
     MX4_M1_CASE(3, 2) MX4_M1_CASE(6, 1)
@@ -453,31 +509,33 @@ bool gemv_m1_supported(uint32_t k) {
 
 // Default configuration, from sweeps on MI355X over the launches of the Qwen3
 // 1.7B and 8B decode steps (q|k|v and gate|up grouped, cold weights, recorded
-// passes). One wave per team for K <= 4096 (1-2 blocks per lane); for long K
-// a 3-wave team and few workgroups, because every workgroup loads the whole
-// activation row (24 KiB at K = 12288) and the number of workgroups, not the
-// number of rows, sets that cost. Grids are in teams per CU.
+// passes). One wave per team for K <= 4096 (1-2 blocks per lane), several
+// teams per workgroup for the wide matrices; for long K a 3-wave team and few
+// workgroups, because every workgroup loads the whole activation row (24 KiB
+// at K = 12288). Grids are in teams per CU.
 static void default_m1_config(uint32_t k, uint32_t rows, int cus, M1Config& c) {
     const uint32_t nblk = k / 32;
     const uint32_t scale = (uint32_t)(cus > 0 ? cus : 256);  // the table is for 256 CUs
+    c.tpw = 1;
     switch (nblk) {
         case 64:  // K = 2048
             c.wg = 1; c.r = rows > 2048 ? 4 : 2; c.grid = (rows > 65536 ? 8 : 12) * scale;
+            if (rows > 8192) { c.r = 2; c.tpw = rows > 65536 ? 8 : 4; c.grid = 16 * scale; }
             break;
         case 128:  // K = 4096
-            c.wg = 1; c.r = rows > 65536 ? 4 : 2; c.grid = (rows > 65536 || rows <= 8192 ? 4 : 8) * scale;
+            c.wg = 1; c.r = rows > 65536 ? 4 : 2; c.grid = (rows > 65536 || rows <= 8192 ? 4 : 16) * scale;
+            if (rows > 8192) c.tpw = rows > 65536 ? 4 : 8;
             break;
         case 192:  // K = 6144
-            c.wg = 3; c.r = 2; c.grid = 3 * scale;
+            c.wg = 3; c.r = 2; c.grid = 2 * scale;
             break;
         case 256:  // K = 8192
             c.wg = 2; c.r = 4; c.grid = 8 * scale;
             break;
         default:  // K = 12288
-            c.wg = 3; c.r = 4; c.grid = scale;
+            c.wg = 3; c.r = 2; c.grid = 2 * scale;
             break;
     }
-    c.waves_per_cu = 0;
 }
 
 hipError_t launch_gemv_m1_group(const GemvGroup& g, int cus, const M1Config* forced) {
@@ -489,10 +547,15 @@ hipError_t launch_gemv_m1_group(const GemvGroup& g, int cus, const M1Config* for
     if (forced) {
         if (forced->wg) c.wg = forced->wg;
         if (forced->r) c.r = forced->r;
+        if (forced->tpw) c.tpw = forced->tpw;
         if (forced->wg || forced->r || forced->grid) c.grid = forced->grid;
     }
     const uint32_t nblk = g.k / 32;
     if (c.wg < 1 || nblk % (64u * c.wg) != 0) return hipErrorNotSupported;
+    if (c.tpw < 1 || 64 * c.wg * c.tpw > 512) return hipErrorNotSupported;
+    // x staged in LDS with the partial sums: at most 64 KiB
+    if (c.tpw > 1 && (uint64_t)g.k * (g.x_bf16 ? 2 : 4) + (uint64_t)c.tpw * 2 * c.wg * c.r * 4 > 65536)
+        return hipErrorNotSupported;
     const int bpl = (int)(nblk / (64u * c.wg));
     Segs sg{};
     sg.count = g.count;
@@ -507,13 +570,14 @@ hipError_t launch_gemv_m1_group(const GemvGroup& g, int cus, const M1Config* for
     for (uint32_t s = g.count; s < (uint32_t)kMaxSegs; ++s) sg.first[s + 1] = sg.first[g.count];
     const uint32_t rowsets = sg.first[g.count];
     sg.rowsets = rowsets;
-    // grid 0 (a forced configuration without a grid): one row-set per team
-    uint32_t grid = c.grid == 0 || c.grid > rowsets ? rowsets : c.grid;
+    // c.grid counts teams; grid 0 (a forced configuration without a grid): one row-set per team
+    uint32_t teams = c.grid == 0 || c.grid > rowsets ? rowsets : c.grid;
     // even split: every team visits the same number of row-sets (+-1)
-    const uint32_t per = (rowsets + grid - 1) / grid;
-    grid = (rowsets + per - 1) / per;
-    return g.x_bf16 ? go_cfg<true>(sg, g.x, g.k, grid, c.wg, bpl, c.r, g.stream)
-                    : go_cfg<false>(sg, g.x, g.k, grid, c.wg, bpl, c.r, g.stream);
+    const uint32_t per = (rowsets + teams - 1) / teams;
+    teams = (rowsets + per - 1) / per;
+    const uint32_t grid = (teams + c.tpw - 1) / c.tpw;
+    return g.x_bf16 ? go_cfg<true>(sg, g.x, g.k, grid, c.wg, bpl, c.r, c.tpw, g.stream)
+                    : go_cfg<false>(sg, g.x, g.k, grid, c.wg, bpl, c.r, c.tpw, g.stream);
 }
 
 hipError_t launch_gemv_m1(const GemvArgs& a, int cus) {

@@ -34,8 +34,9 @@ struct GemvGroup {
 // Kernel configuration of the M == 1 GEMV: waves per team (the team splits a
 // row's K), rows per team per iteration, teams in the grid (0: one row-set each).
 struct M1Config {
-    int wg = 0, r = 0, waves_per_cu = 0;
-    uint32_t grid = 0;
+    int wg = 0, r = 0;      // waves per team, rows per team
+    int tpw = 0;            // teams per workgroup (x staged in LDS when > 1)
+    uint32_t grid = 0;      // teams in the launch (0: one row-set each)
 };
 hipError_t launch_gemv_m1_group(const GemvGroup& g, int cus, const M1Config* forced);
 hipError_t launch_gemv_generic(const GemvArgs& a);

@@ -573,10 +573,12 @@ mx4_status mx4_matmul_group(mx4_context* ctx, const void* x, mx4_dtype xt, uint3
 }
 
 mx4_status mx4_gemv_config(mx4_context* ctx, const void* x, mx4_dtype xt, const mx4_weight* const* w,
-                           float* const* y, uint32_t count, int team_waves, int rows_per_team, uint32_t workgroups) {
+                           float* const* y, uint32_t count, int team_waves, int rows_per_team, int teams_per_workgroup,
+                           uint32_t teams) {
     if (!ctx || !w || !y) return fail(MX4_ERR_ARGUMENT, "null argument");
     if (count < 1 || count > 4) return fail(MX4_ERR_ARGUMENT, "a group holds 1 to 4 weights");
-    if (team_waves < 0 || rows_per_team < 0) return fail(MX4_ERR_ARGUMENT, "negative configuration");
+    if (team_waves < 0 || rows_per_team < 0 || teams_per_workgroup < 0)
+        return fail(MX4_ERR_ARGUMENT, "negative configuration");
     mx4::GemvGroup gg{};
     for (uint32_t i = 0; i < count; ++i) {
         mx4_status st = check_matmul_args(ctx, x, xt, 1, w[i], y[i]);
@@ -600,7 +602,8 @@ mx4_status mx4_gemv_config(mx4_context* ctx, const void* x, mx4_dtype xt, const 
     mx4::M1Config c;
     c.wg = team_waves;
     c.r = rows_per_team;
-    c.grid = workgroups;
+    c.tpw = teams_per_workgroup;
+    c.grid = teams;
     hipError_t e = mx4::launch_gemv_m1_group(gg, ctx->cus, &c);
     if (e == hipErrorNotSupported) return fail(MX4_ERR_UNSUPPORTED, "configuration not instantiated");
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));

@@ -62,7 +62,7 @@ SIGNATURES = {
     "mx4_matmul_path": (_int, [_vp, _vp, _int, _u32, _vp, _vp, _int]),
     "mx4_matmul_prefill": (_int, [_vp, _vp, _int, _u32, _vp, _int, _vp]),
     "mx4_matmul_group": (_int, [_vp, _vp, _int, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32]),
-    "mx4_gemv_config": (_int, [_vp, _vp, _int, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32, _int, _int, _u32]),
+    "mx4_gemv_config": (_int, [_vp, _vp, _int, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32, _int, _int, _int, _u32]),
     "mx4_matmul_batch": (_int, [_vp, _vp, _u32]),
     "mx4_matmul_mx": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
     "mx4_reserve_prefill": (_int, [_vp, _u32, _u32]),
@@ -305,13 +305,15 @@ class Context:
         check(lib().mx4_matmul_group(self.handle, xptr, xtype, m, wa, ya, n))
 
     def gemv_config(self, xptr: int, xtype: int, ws, yptrs, team: int = 0, rows: int = 0,
-                    groups: int = 0) -> None:
+                    teams: int = 0, tpw: int = 0) -> None:
+        """M = 1 GEMV with an explicit configuration: waves per team, rows per team,
+        number of teams, teams per workgroup (0 keeps a default)."""
         if isinstance(ws, Weight):
             ws, yptrs = [ws], [yptrs]
         n = len(ws)
         wa = (_vp * n)(*[w.handle for w in ws])
         ya = (_vp * n)(*yptrs)
-        check(lib().mx4_gemv_config(self.handle, xptr, xtype, wa, ya, n, team, rows, groups))
+        check(lib().mx4_gemv_config(self.handle, xptr, xtype, wa, ya, n, team, rows, tpw, teams))
 
     def matmul_prefill(self, x: DeviceBuffer, xtype: int, m: int, w: Weight, act: int, y: DeviceBuffer) -> None:
         check(lib().mx4_matmul_prefill(self.handle, x.ptr, xtype, m, w.handle, act, y.ptr))

@@ -406,8 +406,9 @@ CONFIG_SHAPES = [(1000, 2048), (1000, 4096), (700, 6144), (999, 8192), (700, 122
 
 @pytest.mark.parametrize("n,k", CONFIG_SHAPES)
 def test_gemv_every_configuration(mx4, ctx, oracle, n, k):
-    """Every instantiated (team, rows, grid) of the M = 1 kernel agrees with the oracle,
-    including ragged tails (n not a multiple of the rows per team)."""
+    """Every instantiated (team, rows, teams, teams per workgroup) of the M = 1 kernel
+    agrees with the oracle, including ragged tails (n not a multiple of the rows per
+    team) and workgroups whose later teams run past the last row-set."""
     say(f"gemv configurations {k}->{n}")
     w = ctx.synth_weight(77, n, k, 0.02)
     packed, scales = ctx.download_weight(w)
@@ -425,13 +426,19 @@ def test_gemv_every_configuration(mx4, ctx, oracle, n, k):
         for rows in (1, 2, 4, 8):
             if rows * bpl > 8:
                 continue
-            for groups in (0, 1, 7, 64):
-                for xt in (mx4.BF16, mx4.F32):
-                    ctx.gemv_config(xdev[xt].ptr, xt, w, y.ptr, team, rows, groups)
-                    got = y.download(np.float32).reshape(1, n)
-                    assert_close(got, ref, f"team={team} rows={rows} groups={groups} xt={xt}")
-                    tried += 1
-    assert tried >= 16
+            for teams in (0, 1, 7, 64):
+                for tpw in (1, 2, 4, 8):
+                    if 64 * team * tpw > 512:
+                        continue
+                    for xt in (mx4.BF16, mx4.F32):
+                        if tpw > 1 and k * (2 if xt == mx4.BF16 else 4) + tpw * 2 * team * rows * 4 > 65536:
+                            continue
+                        y.upload(np.full(n, np.nan, np.float32))
+                        ctx.gemv_config(xdev[xt].ptr, xt, w, y.ptr, team, rows, teams, tpw)
+                        got = y.download(np.float32).reshape(1, n)
+                        assert_close(got, ref, f"team={team} rows={rows} teams={teams} tpw={tpw} xt={xt}")
+                        tried += 1
+    assert tried >= 64
 
 
 def test_group_equals_individual(mx4, ctx, oracle):
