@@ -145,4 +145,21 @@ std::vector<uint32_t> Hip::argmax_rows(const TensorF32& logits) const {
     return out;
 }
 
+std::pair<std::vector<uint8_t>, std::vector<uint8_t>> Hip::quantize(const std::vector<uint16_t>& bf16, size_t rows,
+                                                                    size_t cols) const {
+    if (cols % 32 != 0) throw HipError("row width must be divisible by 32");
+    require(bf16.size() == rows * cols && rows <= UINT32_MAX && cols <= UINT32_MAX, "bad quantize shape");
+    const uint64_t n = (uint64_t)rows * cols;
+    std::pair<std::vector<uint8_t>, std::vector<uint8_t>> out{std::vector<uint8_t>(n / 2), std::vector<uint8_t>(n / 32)};
+    if (n == 0) return out;
+    DeviceBuffer in(resident_, n * 2), packed(resident_, n / 2), scales(resident_, n / 32);
+    check(mx4_upload(resident_, in.ptr, bf16.data(), n * 2), "upload");
+    check(mx4_quantize(resident_, in.ptr, MX4_BF16, rows, (uint32_t)cols, static_cast<uint8_t*>(packed.ptr),
+                       static_cast<uint8_t*>(scales.ptr)),
+          "quantize");
+    check(mx4_download(resident_, out.first.data(), packed.ptr, n / 2), "download");
+    check(mx4_download(resident_, out.second.data(), scales.ptr, n / 32), "download");
+    return out;
+}
+
 }  // namespace jalapenos

@@ -17,6 +17,7 @@
 #include <optional>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "mx4.h"
@@ -79,6 +80,12 @@ class Hip {
 
     // argmax over each row of logits (engine/src/model.rs:288-296), on the device.
     std::vector<uint32_t> argmax_rows(const TensorF32& logits) const;
+
+    // python/quantize_mxfp4.py:18-39 on the device, bit-exact: bf16 bits
+    // [rows][cols] -> packed [rows][cols/2] and scales [rows][cols/32]. Throws
+    // on a width not divisible by 32 or non-finite input (the reference raises).
+    std::pair<std::vector<uint8_t>, std::vector<uint8_t>> quantize(const std::vector<uint16_t>& bf16, size_t rows,
+                                                                   size_t cols) const;
 
    private:
     explicit Hip(void* context, mx4_context* resident);

@@ -8,12 +8,17 @@
 // Usage: test_engine [--cpu-only]   (--cpu-only: the host-logic tests, no GPU)
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <filesystem>
+#include <fstream>
 #include <functional>
 #include <string>
 #include <vector>
 
+#include "checkpoint.hpp"
 #include "engine.hpp"
+#include "json.hpp"
 
 extern "C" {
 #include "mx4_oracle.h"
@@ -191,6 +196,202 @@ Reg argmax_rows_first_maximum("argmax_rows_first_maximum", true, [] {
     CHECK(idx[0] == 17 && idx[1] == 999 && idx[2] == 0);
 });
 
+// ------------------------------------------------------------------ checkpoint format
+
+namespace fs = std::filesystem;
+
+std::vector<std::string>& temp_dirs() {
+    static std::vector<std::string> dirs;
+    return dirs;
+}
+
+std::string temp_dir() {
+    char tmpl[] = "/tmp/mx4ckpt-XXXXXX";
+    if (!mkdtemp(tmpl)) throw Failure{"mkdtemp failed"};
+    temp_dirs().push_back(tmpl);
+    return tmpl;
+}
+
+RawTensor u8(std::vector<size_t> shape, std::vector<uint8_t> bytes) { return RawTensor{"U8", std::move(shape), std::move(bytes)}; }
+
+RawTensor u16(const char* dtype, std::vector<size_t> shape, const std::vector<uint16_t>& v) {
+    RawTensor t{dtype, std::move(shape), {}};
+    for (uint16_t x : v) {
+        t.bytes.push_back((uint8_t)(x & 0xff));
+        t.bytes.push_back((uint8_t)(x >> 8));
+    }
+    return t;
+}
+
+std::string load_error(const std::string& dir) {
+    try {
+        (void)load(dir);
+    } catch (const std::runtime_error& e) {
+        return e.what();
+    }
+    return "";
+}
+
+const std::map<std::string, std::string> kQuantized = {{"format", kMxfp4Format}};
+
+// engine/src/lib.rs:89-202: every rejection, with the reference's message
+Reg load_rejects_malformed_checkpoints("load_rejects_malformed_checkpoints", false, [] {
+    const std::vector<uint8_t> p16(16 * 2, 0x21), s2{127, 127};
+    {
+        const std::string d = temp_dir();
+        CHECK(load_error(d) == "model directory has no safetensors files");
+    }
+    {
+        const std::string d = temp_dir();
+        std::ofstream(d + "/a.safetensors", std::ios::binary) << std::string("\xff\xff\xff\xff\x00\x00\x00\x00{}", 10);
+        CHECK(load_error(d) == "invalid safetensors header length");
+    }
+    auto one = [&](std::vector<std::pair<std::string, RawTensor>> ts, std::map<std::string, std::string> meta) {
+        const std::string d = temp_dir();
+        save_safetensors(d + "/model.safetensors", ts, meta);
+        return d;
+    };
+    CHECK(load_error(one({{"w.mxfp4_packed", u8({2, 16}, p16)}, {"w.mxfp4_scales", u8({2, 1}, s2)}, {"x", u8({2}, {1, 2})}},
+                         kQuantized)) == "unexpected U8 tensor: x");
+    CHECK(load_error(one({{"w.mxfp4_packed", u8({2, 16}, p16)}}, kQuantized)) == "missing MXFP4 scales");
+    CHECK(load_error(one({{"w.mxfp4_packed", u8({2, 16}, p16)}, {"w.mxfp4_scales", u8({1, 2}, s2)}}, kQuantized)) ==
+          "invalid MXFP4 tensor shape: w");
+    CHECK(load_error(one({{"w.mxfp4_packed", u8({2, 16}, p16)}, {"w.mxfp4_scales", u8({2, 1}, {127, 255})}}, kQuantized)) ==
+          "MXFP4 checkpoint contains a NaN scale");
+    CHECK(load_error(one({{"w.mxfp4_scales", u8({2, 1}, s2)}}, kQuantized)) == "MXFP4 scales have no matching packed weights");
+    CHECK(load_error(one({{"w.mxfp4_packed", u8({2, 16}, std::vector<uint8_t>(31))}}, kQuantized)) ==
+          "invalid packed tensor size: w.mxfp4_packed");
+    CHECK(load_error(one({{"n", u16("U16", {4}, {1, 2, 3, 4})}}, {})) == "expected BF16 tensor: n");  // U16 only when quantized
+    CHECK(load_error(one({{"n", u16("BF16", {4}, {1, 2, 3})}}, {})) == "expected BF16 tensor: n");
+    {
+        // offsets past the end of the file
+        const std::string d = one({{"n", u16("BF16", {2}, {1, 2})}}, {});
+        fs::resize_file(d + "/model.safetensors", fs::file_size(d + "/model.safetensors") - 2);
+        CHECK(load_error(d) == "invalid tensor offsets: n");
+    }
+    {
+        // the same name in two shards
+        const std::string d = temp_dir();
+        save_safetensors(d + "/a.safetensors", {{"n", u16("BF16", {2}, {1, 2})}}, {});
+        save_safetensors(d + "/b.safetensors", {{"n", u16("BF16", {2}, {3, 4})}}, {});
+        CHECK(load_error(d) == "duplicate tensor");
+    }
+});
+
+Reg load_reads_quantized_and_bf16_shards("load_reads_quantized_and_bf16_shards", false, [] {
+    const std::string d = temp_dir();
+    std::vector<uint8_t> packed(3 * 32), scales(3 * 2);
+    for (size_t i = 0; i < packed.size(); ++i) packed[i] = (uint8_t)(i * 37);
+    for (size_t i = 0; i < scales.size(); ++i) scales[i] = (uint8_t)(120 + i);
+    save_safetensors(d + "/model-00001.safetensors",
+                     {{"layer.norm", u16("U16", {3}, {0x3f80, 0xbf80, 0x0001})},
+                      {"layer.proj.mxfp4_packed", u8({3, 32}, packed)},
+                      {"layer.proj.mxfp4_scales", u8({3, 2}, scales)}},
+                     kQuantized);
+    save_safetensors(d + "/model-00002.safetensors", {{"lm.bias", u16("BF16", {2}, {0x4000, 0xc000})}}, {});
+    const Weights w = load(d);
+    CHECK(w.tensors.size() == 3);
+    const Tensor& proj = w.tensors.at("layer.proj");
+    CHECK((proj.shape == std::vector<size_t>{3, 64}));
+    CHECK(proj.data.empty() && proj.mxfp4 && proj.mxfp4->packed == packed && proj.mxfp4->scales == scales);
+    const Tensor& norm = w.tensors.at("layer.norm");
+    CHECK(!norm.mxfp4 && (norm.data == std::vector<uint16_t>{0x3f80, 0xbf80, 0x0001}));
+    CHECK((w.tensors.at("lm.bias").data == std::vector<uint16_t>{0x4000, 0xc000}));
+});
+
+Reg json_round_trip("json_round_trip", false, [] {
+    const std::string text =
+        "{\"a\":[1,2.5,-3e2,true,false,null],\"b\":{\"s\":\"q\\\"\\\\\\n\\u00e9\\ud83d\\ude00\",\"n\":18446744073709551615}}";
+    const json::Value v = json::parse(text);
+    CHECK(v.find("b")->find("n")->as_u64() == 18446744073709551615ull);
+    CHECK(v.find("b")->find("s")->str == "q\"\\\n\xc3\xa9\xf0\x9f\x98\x80");
+    CHECK(json::parse(json::dump(v)).find("a")->arr.size() == 6);
+    CHECK(json::dump(json::parse(json::dump(v, 2))) == json::dump(v));
+    bool threw = false;
+    try {
+        (void)json::parse("{\"a\":1,}");
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    CHECK(threw);
+});
+
+// python/quantize_mxfp4.py:52-119 on the device, then engine/src/lib.rs:89-202
+Reg convert_then_load_then_project("convert_then_load_then_project", true, [] {
+    const std::string root = temp_dir();
+    const std::string src = root + "/tiny-model";
+    fs::create_directory(src);
+    auto bf16_of = [](float f) { return (uint16_t)(bits(f) >> 16); };
+    std::vector<uint16_t> w1(64 * 96), w2(33 * 64), norm(96);
+    for (size_t i = 0; i < w1.size(); ++i) w1[i] = bf16_of(0.02f * std::sin(0.7f * (float)i) * (float)(1 + i % 5));
+    for (size_t i = 0; i < w2.size(); ++i) w2[i] = bf16_of(std::cos(0.31f * (float)i) * (i % 97 == 0 ? 0.0f : 1.0f));
+    for (size_t i = 0; i < norm.size(); ++i) norm[i] = bf16_of(1.0f + 0.01f * (float)i);
+    save_safetensors(src + "/model-00001-of-00002.safetensors",
+                     {{"model.layers.0.mlp.up_proj.weight", u16("BF16", {64, 96}, w1)},
+                      {"model.norm.weight", u16("BF16", {96}, norm)}}, {});
+    save_safetensors(src + "/model-00002-of-00002.safetensors", {{"lm_head.weight", u16("BF16", {33, 64}, w2)}}, {});
+    std::ofstream(src + "/config.json") << "{\"hidden_size\": 96, \"torch_dtype\": \"bfloat16\"}";
+    std::ofstream(src + "/tokenizer.json") << "{}";
+    std::ofstream(src + "/model.safetensors.index.json") << "{}";
+
+    const std::string dst = convert(device(), src);
+    CHECK(dst == root + "/tiny-model-MXFP4");
+    CHECK(fs::exists(dst + "/tokenizer.json") && !fs::exists(dst + "/model.safetensors.index.json"));
+    std::ifstream cin(dst + "/config.json");
+    const json::Value config = json::parse(std::string(std::istreambuf_iterator<char>(cin), {}));
+    CHECK(config.find("hidden_size")->as_u64() == 96);
+    const json::Value* qc = config.find("quantization_config");
+    CHECK(qc && qc->find("format")->str == kMxfp4Format && qc->find("block_size")->as_u64() == 32);
+
+    const Weights w = load(dst);
+    CHECK(w.tensors.size() == 3);
+    auto check_quantized = [&](const char* name, const std::vector<uint16_t>& src_bits, size_t rows, size_t cols) {
+        const Tensor& t = w.tensors.at(name);
+        CHECK((t.shape == std::vector<size_t>{rows, cols}) && t.mxfp4);
+        std::vector<float> f(rows * cols);
+        for (size_t i = 0; i < f.size(); ++i) f[i] = oracle_bf16_to_f32(src_bits[i]);
+        std::vector<uint8_t> packed(rows * cols / 2), scales(rows * cols / 32);
+        CHECK(oracle_quantize(f.data(), rows, cols, packed.data(), scales.data()) == 0);
+        CHECK(t.mxfp4->packed == packed && t.mxfp4->scales == scales);  // the device quantizer is the rule, bit for bit
+    };
+    check_quantized("model.layers.0.mlp.up_proj.weight", w1, 64, 96);
+    check_quantized("lm_head.weight", w2, 33, 64);
+    CHECK(w.tensors.at("model.norm.weight").data == norm);
+
+    // the loaded tensors feed the projection unchanged
+    const Tensor& up = w.tensors.at("model.layers.0.mlp.up_proj.weight");
+    TensorF32 x{{3, 96}, std::vector<float>(3 * 96)};
+    for (size_t i = 0; i < x.data.size(); ++i) x.data[i] = std::sin(0.13f * (float)i);
+    std::vector<float> expected(3 * 64);
+    oracle_matmul(x.data.data(), 3, 96, up.mxfp4->packed.data(), up.mxfp4->scales.data(), 64, expected.data());
+    const TensorF32 y = device().matmul(x, up);
+    for (size_t i = 0; i < expected.size(); ++i) CHECK(std::fabs(y.data[i] - expected[i]) < 1e-3f + 1e-5f * std::fabs(expected[i]));
+
+    bool threw = false;
+    try {
+        (void)convert(device(), src);
+    } catch (const std::runtime_error& e) {
+        threw = std::string(e.what()).find("destination already exists") == 0;
+    }
+    CHECK(threw);
+    // a 2-D tensor whose width is not a multiple of 32 fails and leaves no partial output
+    const std::string bad = root + "/bad";
+    fs::create_directory(bad);
+    save_safetensors(bad + "/m.safetensors", {{"w", u16("BF16", {2, 40}, std::vector<uint16_t>(80, 0x3f80))}}, {});
+    std::ofstream(bad + "/config.json") << "{}";
+    threw = false;
+    try {
+        (void)convert(device(), bad);
+    } catch (const std::runtime_error& e) {
+        threw = std::string(e.what()) == "row width must be divisible by 32: w";
+    }
+    CHECK(threw && !fs::exists(root + "/bad-MXFP4"));
+    size_t leftovers = 0;
+    for (const auto& item : fs::directory_iterator(root)) leftovers += item.path().filename().string().rfind(".bad", 0) == 0;
+    CHECK(leftovers == 0);
+    fs::remove_all(root);
+});
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -212,6 +413,10 @@ int main(int argc, char** argv) {
             ++failed;
         }
         std::fflush(stdout);
+    }
+    for (const std::string& d : temp_dirs()) {
+        std::error_code ec;
+        std::filesystem::remove_all(d, ec);
     }
     std::printf("%d tests, %d failed\n", ran, failed);
     return failed ? 1 : 0;
