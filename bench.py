@@ -146,6 +146,36 @@ def time_skinny(ctx, weights, ms=(1, 2, 4, 8, 16), reps: int = 3):
     return out
 
 
+def time_lm_head_argmax(ctx, weights, xs, reps: int = 5):
+    """Greedy pick after the lm_head (engine/src/model.rs:228-238, :288-296) at
+    M = 1: the projection followed by a separate argmax over the 151936 logits,
+    against the fused epilogue with and without writing the logits. 8 calls
+    per recorded pass; per-call GPU time."""
+    _, n, k, w = weights[-1]
+    y = ctx.buffer(n * 4)
+    idx = ctx.buffer(4)
+    x = xs[k]
+    forms = (("projection", lambda: ctx.matmul_ptr(x.ptr, mx4hip.BF16, 1, w, y.ptr)),
+             ("projection+argmax_rows", lambda: (ctx.matmul_ptr(x.ptr, mx4hip.BF16, 1, w, y.ptr),
+                                                 ctx.argmax_rows(y, 1, n, idx))),
+             ("fused, logits written", lambda: ctx.matmul_argmax(x, mx4hip.BF16, w, y, idx)),
+             ("fused, no logits", lambda: ctx.matmul_argmax(x, mx4hip.BF16, w, None, idx)))
+    out = {}
+    for label, fn in forms:
+        p = ctx.record(lambda: [fn() for _ in range(8)])
+        p.launch()
+        best = None
+        for _ in range(reps):
+            ctx.synchronize()
+            ctx.timer_begin()
+            p.launch()
+            t = ctx.timer_end() / 8
+            best = t if best is None else min(best, t)
+        p.release()
+        out[label] = round(best * 1e3, 2)
+    return {"n": n, "k": k, "us": out}
+
+
 def time_prefill(ctx, weights, m: int = 512, reps: int = 5):
     """Prefill on block-scaled MFMA: each 8B q/o/gate/up/down shape at M = 512,
     activations bf16 N(0, 1) requantized per 32 along K (MXFP4, and MX-FP8).
@@ -339,6 +369,9 @@ def main() -> int:
     if not args.no_shapes:
         log("per-shape timing")
         extra["shapes"] = time_shapes(ctx, weights, xs, ys)
+
+        log("lm_head + greedy argmax timing")
+        extra["lm_head_argmax"] = time_lm_head_argmax(ctx, weights, xs)
 
     if not args.no_skinny:
         log("skinny (speculative verify) timing")

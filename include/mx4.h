@@ -251,6 +251,23 @@ mx4_status mx4_quantize_fp8(mx4_context *ctx, const void *in_dev, mx4_dtype in_t
 mx4_status mx4_argmax_rows(mx4_context *ctx, const float *x_dev, uint32_t rows, uint32_t width,
                            uint32_t *out_dev);
 
+/* The lm_head of a greedy decode step (engine/src/model.rs:228-238): the
+ * M == 1 projection y_dev = x . W^T and the first index of its maximum
+ * (engine/src/model.rs:288-296) into idx_dev[0], fused: every GEMV workgroup
+ * reduces its rows to one key and a second tiny kernel picks the winner, so
+ * the logits need not be written (y_dev may be NULL) or read back. Shapes
+ * without a fused instance run the projection and mx4_argmax_rows. */
+mx4_status mx4_matmul_argmax(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, const mx4_weight *w,
+                             float *y_dev, uint32_t *idx_dev);
+
+/* Embedding lookup (engine/src/lib.rs:222-227, engine/src/gpu.metal:43-55):
+ * out_dev[t][cols] = row ids_dev[t] of the table, decoded and cut to bf16 (the
+ * low 16 bits dropped, as both reference paths do); MXFP4 or bf16 tables,
+ * cols % 32 == 0. An id >= rows gives a zero row. A tied lm_head
+ * (engine/src/gpu.rs:341-357) is the same mx4_weight used for both. */
+mx4_status mx4_embed(mx4_context *ctx, const mx4_weight *w, const uint32_t *ids_dev, uint32_t count,
+                     uint16_t *out_dev);
+
 /* Synthetic inputs (the reference defines none): element i of stream `seed`
  * is bf16(RNE(f32(RNE(sigma * z_i)))) with z_i a Box-Muller normal from
  * SplitMix64 outputs 2i and 2i+1. */

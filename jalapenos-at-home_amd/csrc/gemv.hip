@@ -109,6 +109,7 @@ struct Segs {
     uint32_t first[kMaxSegs + 1];
     uint32_t count;
     uint32_t rowsets;  // first[count], passed directly so no argument load depends on another
+    uint64_t* am_partial;  // greedy-argmax epilogue: one key per workgroup (unused otherwise)
 };
 
 // Sum R per-lane values over the 64 lanes of a wave in log2(64) exchange
@@ -203,11 +204,6 @@ __device__ __forceinline__ bool row_writer(uint32_t lane) {
     return (lane & ~row_bits) == 0;
 }
 
-// Buffer resource over [base, base + bytes): loads past the end return zero
-// without touching memory, which bounds the tail row-set in hardware.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
 
 constexpr int kNonTemporal = 2;  // streamed once per pass: do not keep in the caches
 
@@ -309,10 +305,10 @@ __device__ __forceinline__ float row_dot(const LaneX<XBF16, BPL>& xr, const u32x
     return acc;
 }
 
-template <bool XBF16, int WG, int BPL, int R>
+template <bool XBF16, int WG, int BPL, int R, bool AM>
 __device__ __forceinline__ void finish_rowset(const Segs& sg, uint32_t rs, const LaneX<XBF16, BPL>& xr,
                                               const RowSet<XBF16, BPL, R>& cur, uint32_t t,
-                                              float (*red)[WG][R], uint32_t& parity) {
+                                              float (*red)[WG][R], uint32_t& parity, uint64_t& best) {
     const uint32_t wave = t / 64, lane = t % 64;
     float acc[R];
 #pragma unroll
@@ -325,7 +321,14 @@ __device__ __forceinline__ void finish_rowset(const Segs& sg, uint32_t rs, const
     const uint32_t myrow = reduced_row_of_lane<R>(lane);
     const bool writer = row_writer<R>(lane);
     if constexpr (WG == 1) {
-        if (writer && row0 + myrow < n) y[row0 + myrow] = total;
+        if (writer && row0 + myrow < n) {
+            if constexpr (AM) {
+                if (y) y[row0 + myrow] = total;
+                best = max_u64(best, argmax_key(total, row0 + myrow));
+            } else {
+                y[row0 + myrow] = total;
+            }
+        }
     } else {
         if (writer) red[parity][wave][myrow] = total;
         __syncthreads();
@@ -333,7 +336,14 @@ __device__ __forceinline__ void finish_rowset(const Segs& sg, uint32_t rs, const
             float v = 0.0f;
 #pragma unroll
             for (int w = 0; w < WG; ++w) v += red[parity][w][t];
-            if (row0 + t < n) y[row0 + t] = v;
+            if (row0 + t < n) {
+                if constexpr (AM) {
+                    if (y) y[row0 + t] = v;
+                    best = max_u64(best, argmax_key(v, row0 + t));
+                } else {
+                    y[row0 + t] = v;
+                }
+            }
         }
         parity ^= 1;
     }
@@ -345,7 +355,7 @@ __device__ __forceinline__ void finish_rowset(const Segs& sg, uint32_t rs, const
 // larger workgroups cut that L2 traffic (for o at K = 4096 it matched the
 // weight bytes with one team per workgroup). Dynamic LDS: x (k elements), then
 // the cross-wave partial sums [tpw][2][WG][R].
-template <bool XBF16, int WG, int BPL, int R>
+template <bool XBF16, int WG, int BPL, int R, bool AM>
 __global__ __launch_bounds__(512) void gemv_m1_kernel(Segs sg, const void* __restrict__ x, uint32_t k) {
     constexpr uint32_t T = 64 * WG;  // threads per team
     const uint32_t tpw = blockDim.x / T;
@@ -385,6 +395,7 @@ __global__ __launch_bounds__(512) void gemv_m1_kernel(Segs sg, const void* __res
     }
 
     uint32_t parity = 0;
+    uint64_t best = 0;  // greedy-argmax key of the rows this thread finished
     // ping-pong: the next row-set streams in while the current one is reduced.
     // Every team of the workgroup runs as many turns as the first one (the
     // cross-wave reduction has a workgroup barrier); a team past the end
@@ -392,16 +403,32 @@ __global__ __launch_bounds__(512) void gemv_m1_kernel(Segs sg, const void* __res
     for (uint32_t rf = first;;) {
         uint32_t nxt = rs + stride;
         load_rowset<XBF16, WG, BPL, R>(sg, nxt, rowsets, t, row_bytes, nblk, b);
-        finish_rowset<XBF16, WG, BPL, R>(sg, rs, xr, a, t, red, parity);
+        finish_rowset<XBF16, WG, BPL, R, AM>(sg, rs, xr, a, t, red, parity, best);
         rf += stride;
         if (rf >= rowsets) break;
         rs = nxt;
         nxt = rs + stride;
         load_rowset<XBF16, WG, BPL, R>(sg, nxt, rowsets, t, row_bytes, nblk, a);
-        finish_rowset<XBF16, WG, BPL, R>(sg, rs, xr, b, t, red, parity);
+        finish_rowset<XBF16, WG, BPL, R, AM>(sg, rs, xr, b, t, red, parity, best);
         rf += stride;
         if (rf >= rowsets) break;
         rs = nxt;
+    }
+    if constexpr (AM) {
+        // the workgroup's best key -> am_partial[blockIdx.x]
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const uint32_t lo = __shfl_xor((uint32_t)best, off, kWave), hi = __shfl_xor((uint32_t)(best >> 32), off, kWave);
+            best = max_u64(best, ((uint64_t)hi << 32) | lo);
+        }
+        __shared__ uint64_t wbest[8];
+        if (threadIdx.x % 64 == 0) wbest[threadIdx.x / 64] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t m = 0;
+            for (uint32_t w = 0; w < blockDim.x / 64; ++w) m = max_u64(m, wbest[w]);
+            sg.am_partial[blockIdx.x] = m;
+        }
     }
 }
 
@@ -472,7 +499,7 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* __rest
 template <bool XBF16, int WG, int BPL, int R>
 static hipError_t go_m1(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int tpw, hipStream_t st) {
     const size_t lds = (tpw > 1 ? (size_t)k * (XBF16 ? 2 : 4) : 0) + (size_t)tpw * 2 * WG * R * sizeof(float);
-    hipLaunchKernelGGL((gemv_m1_kernel<XBF16, WG, BPL, R>), dim3(grid), dim3(64 * WG * tpw), lds, st, sg, x, k);
+    hipLaunchKernelGGL((gemv_m1_kernel<XBF16, WG, BPL, R, false>), dim3(grid), dim3(64 * WG * tpw), lds, st, sg, x, k);
     return hipGetLastError();
 }
 
@@ -578,6 +605,57 @@ hipError_t launch_gemv_m1_group(const GemvGroup& g, int cus, const M1Config* for
     const uint32_t grid = (teams + c.tpw - 1) / c.tpw;
     return g.x_bf16 ? go_cfg<true>(sg, g.x, g.k, grid, c.wg, bpl, c.r, c.tpw, g.stream)
                     : go_cfg<false>(sg, g.x, g.k, grid, c.wg, bpl, c.r, c.tpw, g.stream);
+}
+
+// M = 1 projection with the greedy-argmax epilogue (the lm_head of a greedy
+// decode step): y is optional (nullptr: logits are not written), *idx gets the
+// first index of the maximum. Instantiated for the lm_head configurations
+// (one-wave teams, 1-2 blocks per lane, 2 or 4 rows); others report
+// hipErrorNotSupported and the caller runs the projection and argmax_rows.
+template <bool XBF16, int BPL, int R>
+static hipError_t go_am(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int tpw, uint32_t* idx, hipStream_t st) {
+    const size_t lds = (tpw > 1 ? (size_t)k * (XBF16 ? 2 : 4) : 0) + (size_t)tpw * 2 * R * sizeof(float);
+    hipLaunchKernelGGL((gemv_m1_kernel<XBF16, 1, BPL, R, true>), dim3(grid), dim3(64 * tpw), lds, st, sg, x, k);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_argmax_reduce(sg.am_partial, 1, grid, idx, st);
+}
+
+hipError_t launch_gemv_m1_argmax(const GemvArgs& a, uint64_t* partial, uint32_t max_partials, uint32_t* idx,
+                                 int cus) {
+    if (!gemv_m1_supported(a.k) || a.n == 0) return hipErrorNotSupported;
+    M1Config c;
+    default_m1_config(a.k, a.n, cus, c);
+    const uint32_t nblk = a.k / 32;
+    const int bpl = (int)(nblk / 64);
+    if ((bpl != 1 && bpl != 2) || (c.r != 2 && c.r != 4)) return hipErrorNotSupported;
+    Segs sg{};
+    sg.count = 1;
+    sg.packed[0] = a.packed;
+    sg.scales[0] = a.scales;
+    sg.y[0] = a.y;
+    sg.n[0] = a.n;
+    const uint32_t rowsets = (a.n + c.r - 1) / c.r;
+    for (int q = 1; q <= kMaxSegs; ++q) sg.first[q] = rowsets;
+    sg.rowsets = rowsets;
+    sg.am_partial = partial;
+    const int tpw = c.tpw < 1 ? 1 : c.tpw;
+    if (tpw > 1 && (uint64_t)a.k * (a.x_bf16 ? 2 : 4) + (uint64_t)tpw * 2 * c.r * 4 > 65536) return hipErrorNotSupported;
+    uint32_t teams = c.grid == 0 || c.grid > rowsets ? rowsets : c.grid;
+    const uint32_t per = (rowsets + teams - 1) / teams;
+    teams = (rowsets + per - 1) / per;
+    const uint32_t grid = (teams + tpw - 1) / tpw;
+    if (grid > max_partials) return hipErrorNotSupported;
+    if (a.x_bf16) {
+        if (bpl == 1) return c.r == 2 ? go_am<true, 1, 2>(sg, a.x, a.k, grid, tpw, idx, a.stream)
+                                      : go_am<true, 1, 4>(sg, a.x, a.k, grid, tpw, idx, a.stream);
+        return c.r == 2 ? go_am<true, 2, 2>(sg, a.x, a.k, grid, tpw, idx, a.stream)
+                        : go_am<true, 2, 4>(sg, a.x, a.k, grid, tpw, idx, a.stream);
+    }
+    if (bpl == 1) return c.r == 2 ? go_am<false, 1, 2>(sg, a.x, a.k, grid, tpw, idx, a.stream)
+                                  : go_am<false, 1, 4>(sg, a.x, a.k, grid, tpw, idx, a.stream);
+    return c.r == 2 ? go_am<false, 2, 2>(sg, a.x, a.k, grid, tpw, idx, a.stream)
+                    : go_am<false, 2, 4>(sg, a.x, a.k, grid, tpw, idx, a.stream);
 }
 
 hipError_t launch_gemv_m1(const GemvArgs& a, int cus) {

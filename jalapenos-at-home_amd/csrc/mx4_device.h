@@ -21,6 +21,37 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// Buffer resource over [base, base + bytes): loads past the end return zero
+// without touching memory, so tail loads can be issued unconditionally.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// Greedy argmax of the logits (engine/src/model.rs:288-296: the first index of
+// the maximum under a strict `>` scan from index 0) as one unsigned 64-bit key
+// per row, so that the largest key is the answer: the value in an order-
+// preserving integer form above the complemented row, so equal values favour
+// the lower row. +0 and -0 compare equal in the scan, so both map to +0. A NaN
+// is never greater than anything and nothing is greater than a NaN: a NaN at
+// row 0 is the answer (key = all ones), a NaN elsewhere never is (key 0).
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t row) {
+    if (v != v) return row == 0 ? ~0ull : 0ull;
+    uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)b << 32) | (uint32_t)~row;
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t m) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)m, off, kWave), hi = __shfl_xor((uint32_t)(m >> 32), off, kWave);
+        m = max_u64(m, ((uint64_t)hi << 32) | lo);
+    }
+    return m;
+}
+
 // E2M1 magnitude levels (engine/src/mxfp4.rs:3).
 __device__ __forceinline__ float level_of(uint32_t code) {
     // Built from bits like gpu.metal's mxfp4_level, independent of a table:

@@ -40,6 +40,15 @@ struct M1Config {
 };
 hipError_t launch_gemv_m1_group(const GemvGroup& g, int cus, const M1Config* forced);
 hipError_t launch_gemv_generic(const GemvArgs& a);
+// M = 1 projection + greedy argmax epilogue (a.y may be null); hipErrorNotSupported
+// for configurations without the epilogue instance. partial: max_partials keys.
+hipError_t launch_gemv_m1_argmax(const GemvArgs& a, uint64_t* partial, uint32_t max_partials, uint32_t* idx,
+                                 int cus);
+// Embedding rows (engine/src/lib.rs:222-227, engine/src/gpu.metal:43-55): out
+// [count][cols] bf16 = decoded row ids[t] truncated to bf16; MXFP4 (packed,
+// scales) or bf16 (bf16 != null) table; ids >= rows give zero rows.
+hipError_t launch_embed(const uint8_t* packed, const uint8_t* scales, const uint16_t* bf16, const uint32_t* ids,
+                        uint32_t count, uint32_t rows, uint32_t cols, uint16_t* out, hipStream_t s);
 
 // Exact skinny path (2 <= m <= 16) on bf16 MFMA with decoded weights.
 bool skinny_supported(uint32_t m, uint32_t k);
@@ -86,9 +95,13 @@ hipError_t launch_quantize_fragments(const void* in, bool in_bf16, uint32_t rows
 // engine/src/mxfp4.rs:35-49 on device: packed/scales -> f32 [elements]
 hipError_t launch_dequantize(const uint8_t* packed, const uint8_t* scales, uint64_t elements,
                              float* out, hipStream_t s);
-// engine/src/model.rs:288-296 per row
-hipError_t launch_argmax_rows(const float* x, uint32_t rows, uint32_t width, uint32_t* out,
-                              hipStream_t s);
+// engine/src/model.rs:288-296 per row; `partial` holds max_partials keys of
+// scratch for rows split over several blocks.
+hipError_t launch_argmax_rows(const float* x, uint32_t rows, uint32_t width, uint32_t* out, uint64_t* partial,
+                              uint32_t max_partials, int cus, hipStream_t s);
+// Row r's index from the keys partial[r * count .. + count) (0 when all are 0).
+hipError_t launch_argmax_reduce(const uint64_t* partial, uint32_t rows, uint32_t count, uint32_t* out,
+                                hipStream_t s);
 // Synthetic inputs (SplitMix64 -> Box-Muller -> sigma -> f32 -> bf16)
 hipError_t launch_synth_bf16(uint64_t seed, double sigma, uint64_t start, uint64_t count,
                              uint16_t* out, hipStream_t s);

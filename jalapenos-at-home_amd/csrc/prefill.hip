@@ -47,9 +47,6 @@ namespace mx4 {
 
 namespace {
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
 
 // See skinny.hip: drain the matrix pipe before accumulators are read after a branch.
 __device__ __forceinline__ void mfma_drain() {

@@ -252,6 +252,58 @@ hipError_t launch_quantize_fragments(const void* in, bool in_bf16, uint32_t rows
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------------ embedding
+
+// engine/src/lib.rs:222-227 (embed): row ids[t] of the table, each value
+// decoded exactly (engine/src/mxfp4.rs:35-49) and cut to bf16 by dropping the
+// low 16 bits, as both the CPU path (`to_bits() >> 16`) and the Metal kernel
+// (engine/src/gpu.metal:43-55, `& 0xffff0000`) do. One thread per 32 values.
+__global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ packed, const uint8_t* __restrict__ scales,
+                                                    const uint16_t* __restrict__ bf16, const uint32_t* __restrict__ ids,
+                                                    uint32_t count, uint32_t rows, uint32_t cols,
+                                                    uint16_t* __restrict__ out) {
+    const uint32_t nblk = cols / 32;
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (uint64_t)count * nblk) return;
+    const uint32_t tok = (uint32_t)(t / nblk), b = (uint32_t)(t % nblk);
+    const uint32_t id = ids[tok];
+    uint32_t words[16];
+    if (id >= rows) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) words[i] = 0;
+    } else if (bf16) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(bf16 + (uint64_t)id * cols + 32 * (uint64_t)b);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x4 v = src[q];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) words[4 * q + e] = v[e];
+        }
+    } else {
+        const u32x4 w = load_u32x4(packed + ((uint64_t)id * nblk + b) * 16);
+        const uint32_t s = scales[(uint64_t)id * nblk + b];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t byte = (w[e / 4] >> (8 * (e % 4))) & 0xffu;
+            const uint32_t lo = __float_as_uint(decode_exact(byte & 15u, s)) >> 16;
+            const uint32_t hi = __float_as_uint(decode_exact(byte >> 4, s)) >> 16;
+            words[e] = lo | (hi << 16);
+        }
+    }
+    u32x4* dst = reinterpret_cast<u32x4*>(out + (uint64_t)tok * cols + 32 * (uint64_t)b);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dst[q] = u32x4{words[4 * q], words[4 * q + 1], words[4 * q + 2], words[4 * q + 3]};
+}
+
+hipError_t launch_embed(const uint8_t* packed, const uint8_t* scales, const uint16_t* bf16, const uint32_t* ids,
+                        uint32_t count, uint32_t rows, uint32_t cols, uint16_t* out, hipStream_t s) {
+    const uint64_t threads = (uint64_t)count * (cols / 32);
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, packed, scales, bf16, ids,
+                       count, rows, cols, out);
+    return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ dequantize
 
 // engine/src/mxfp4.rs:35-49: one thread per packed byte -> two f32 values.
@@ -338,55 +390,103 @@ hipError_t launch_min_max_scale(const uint8_t* scales, uint64_t count, uint32_t*
 
 // ------------------------------------------------------------------ argmax
 
-// engine/src/model.rs:288-296 per row: first index of the maximum with a
-// strict >, so NaN never wins, ties go to the lowest index and a NaN in
-// column 0 pins the answer to 0 (the sequential loop compares against it).
-__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* __restrict__ x, uint32_t width,
-                                                           uint32_t* __restrict__ out) {
-    const float* row = x + (size_t)blockIdx.x * width;
+// engine/src/model.rs:288-296 per row: the first index of the maximum under a
+// strict `>` scan from column 0, so a NaN never wins unless it sits in column 0
+// (nothing compares greater than it), and ties go to the lowest index. Row r is
+// cut into `chunks` pieces of `chunk` columns; block (r, c) reduces its piece to
+// one argmax_key. A thread scans its columns in increasing order with a strict
+// `>` (first maximum within the thread); keys order the threads and blocks.
+// With one chunk per row the block writes the index; otherwise its key goes to
+// partial[r * chunks + c] for argmax_reduce_kernel. Each trip issues four
+// unconditional loads per thread (4 KiB per block in flight) through a buffer
+// resource bounded to the piece; loads past its end return zero and are masked.
+template <bool FINAL>
+__global__ __launch_bounds__(256) void argmax_chunk_kernel(const float* __restrict__ x, uint32_t width,
+                                                           uint32_t chunk, uint32_t chunks,
+                                                           uint64_t* __restrict__ partial, uint32_t* __restrict__ out) {
+    const uint32_t row = blockIdx.x / chunks, c = blockIdx.x % chunks;
+    const uint32_t start = c * chunk;  // < width: the host makes every piece non-empty
+    const uint32_t len = min(chunk, width - start);
+    const float* base = x + (size_t)row * width + start;
+    const __amdgpu_buffer_rsrc_t r = rsrc(base, len * 4u);
     float best = -__builtin_inff();
-    uint32_t idx = 0xffffffffu;
-    for (uint32_t i = threadIdx.x; i < width; i += blockDim.x) {
-        float v = row[i];
-        if (v > best) {
-            best = v;
-            idx = i;
-        }
-    }
+    uint32_t at = 0xffffffffu;
+    for (uint32_t i = threadIdx.x; i < len; i += 256 * 4) {
+        float v[4];
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        float ob = __shfl_xor(best, off, 64);
-        uint32_t oi = __shfl_xor(idx, off, 64);
-        if (ob > best || (ob == best && oi < idx)) {
-            best = ob;
-            idx = oi;
-        }
-    }
-    __shared__ float sb[16];
-    __shared__ uint32_t si[16];
-    const uint32_t wave = threadIdx.x / 64;
-    if (threadIdx.x % 64 == 0) {
-        sb[wave] = best;
-        si[wave] = idx;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (uint32_t w = 1; w < blockDim.x / 64; ++w) {
-            if (sb[w] > best || (sb[w] == best && si[w] < idx)) {
-                best = sb[w];
-                idx = si[w];
+        for (int j = 0; j < 4; ++j) v[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, 4 * (i + 256 * j), 0, 0));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (i + 256 * j < len && v[j] > best) {
+                best = v[j];
+                at = i + 256 * j;
             }
         }
-        float first = row[0];
-        if (first != first || idx == 0xffffffffu) idx = 0;
-        out[blockIdx.x] = idx;
+    }
+    uint64_t key = at == 0xffffffffu ? 0ull : argmax_key(best, start + at);
+    if (c == 0 && threadIdx.x == 0 && base[0] != base[0]) key = ~0ull;  // NaN in column 0
+    key = wave_max_u64(key);
+    __shared__ uint64_t wm[4];
+    if (threadIdx.x % 64 == 0) wm[threadIdx.x / 64] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        key = max_u64(max_u64(wm[0], wm[1]), max_u64(wm[2], wm[3]));
+        if constexpr (FINAL) {
+            out[row] = key == 0 ? 0u : ~(uint32_t)key;  // key 0: no candidate (all -inf or NaN) -> column 0
+        } else {
+            partial[blockIdx.x] = key;
+        }
     }
 }
 
-hipError_t launch_argmax_rows(const float* x, uint32_t rows, uint32_t width, uint32_t* out, hipStream_t s) {
+// Block r reduces the `count` keys partial[r * count ..] of row r to its index.
+__global__ __launch_bounds__(256) void argmax_reduce_kernel(const uint64_t* __restrict__ partial, uint32_t count,
+                                                            uint32_t* __restrict__ out) {
+    const uint64_t* p = partial + (size_t)blockIdx.x * count;
+    uint64_t m = 0;
+    for (uint32_t i = threadIdx.x; i < count; i += 256) m = max_u64(m, p[i]);
+    m = wave_max_u64(m);
+    __shared__ uint64_t wm[4];
+    if (threadIdx.x % 64 == 0) wm[threadIdx.x / 64] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = max_u64(max_u64(wm[0], wm[1]), max_u64(wm[2], wm[3]));
+        out[blockIdx.x] = m == 0 ? 0u : ~(uint32_t)m;
+    }
+}
+
+hipError_t launch_argmax_reduce(const uint64_t* partial, uint32_t rows, uint32_t count, uint32_t* out, hipStream_t s) {
     if (rows == 0) return hipSuccess;
-    hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(1024), 0, s, x, width, out);
+    hipLaunchKernelGGL(argmax_reduce_kernel, dim3(rows), dim3(256), 0, s, partial, count, out);
     return hipGetLastError();
+}
+
+hipError_t launch_argmax_rows(const float* x, uint32_t rows, uint32_t width, uint32_t* out, uint64_t* partial,
+                              uint32_t max_partials, int cus, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    if (width == 0) return hipErrorInvalidValue;
+    // About 4 blocks per CU over all rows, at least 1024 columns (one trip) per
+    // block, and no more keys than the partial buffer holds.
+    uint64_t per_row = ((uint64_t)4 * (cus > 0 ? cus : 256) + rows - 1) / rows;
+    const uint64_t trips = ((uint64_t)width + 1023) / 1024;
+    if (per_row > trips) per_row = trips;
+    if (per_row > max_partials / rows) per_row = max_partials / rows;
+    if (per_row < 1) per_row = 1;
+    uint32_t chunk = (uint32_t)(((uint64_t)width + per_row - 1) / per_row);
+    if (chunk > (1u << 28)) return hipErrorInvalidValue;  // buffer-resource range of one piece
+    const uint32_t chunks = (width + chunk - 1) / chunk;  // every piece starts below width
+    const uint64_t grid = (uint64_t)rows * chunks;
+    if (grid > 0x7fffffffu) return hipErrorInvalidValue;
+    if (chunks == 1) {
+        hipLaunchKernelGGL(argmax_chunk_kernel<true>, dim3((uint32_t)grid), dim3(256), 0, s, x, width, chunk, 1u,
+                           partial, out);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(argmax_chunk_kernel<false>, dim3((uint32_t)grid), dim3(256), 0, s, x, width, chunk, chunks,
+                       partial, out);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_argmax_reduce(partial, rows, chunks, out, s);
 }
 
 // ------------------------------------------------------------------ generator

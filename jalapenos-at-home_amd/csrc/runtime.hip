@@ -104,7 +104,15 @@ struct mx4_context {
     // prefill workspace: requantized activations + their scales
     void* work = nullptr;
     uint64_t work_cap = 0;
+    // greedy-argmax keys: one per workgroup of the fused lm_head GEMV, or one
+    // per piece of a row split over several blocks by mx4_argmax_rows
+    uint64_t* am_partial = nullptr;
+    // logits of mx4_matmul_argmax when the caller does not want them
+    void* logits = nullptr;
+    uint64_t logits_cap = 0;
 };
+
+constexpr uint32_t kArgmaxPartials = 8192;
 
 namespace mx4 {
 hipError_t launch_fill_u32(uint32_t* p, uint32_t count, uint32_t value, hipStream_t s);
@@ -314,7 +322,8 @@ mx4_status mx4_create(int device, mx4_context** out) {
     if (hipGetDeviceProperties(&prop, device) == hipSuccess) ctx->cus = prop.multiProcessorCount;
     if (hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&ctx->ev0) != hipSuccess || hipEventCreate(&ctx->ev1) != hipSuccess ||
-        hipMalloc((void**)&ctx->flags, 256) != hipSuccess) {
+        hipMalloc((void**)&ctx->flags, 256) != hipSuccess ||
+        hipMalloc((void**)&ctx->am_partial, kArgmaxPartials * sizeof(uint64_t)) != hipSuccess) {
         mx4_destroy(ctx);
         return fail(MX4_ERR_DEVICE, "could not create stream, events or scratch on device %d", device);
     }
@@ -333,6 +342,8 @@ void mx4_destroy(mx4_context* ctx) {
     if (ctx->y_stage) (void)hipFree(ctx->y_stage);
     if (ctx->work) (void)hipFree(ctx->work);
     if (ctx->flags) (void)hipFree(ctx->flags);
+    if (ctx->am_partial) (void)hipFree(ctx->am_partial);
+    if (ctx->logits) (void)hipFree(ctx->logits);
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
@@ -774,6 +785,46 @@ mx4_status mx4_prefill_matmul(mx4_context* ctx, const uint8_t* codes, const uint
     return MX4_OK;
 }
 
+mx4_status mx4_matmul_argmax(mx4_context* ctx, const void* x, mx4_dtype xt, const mx4_weight* w, float* y,
+                             uint32_t* idx) {
+    if (!ctx || !x || !w || !idx) return fail(MX4_ERR_ARGUMENT, "null x, weight or index");
+    if (xt != MX4_F32 && xt != MX4_BF16) return fail(MX4_ERR_ARGUMENT, "bad activation dtype %d", (int)xt);
+    if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
+    if (((uintptr_t)x & 15) != 0) return fail(MX4_ERR_ARGUMENT, "x must be 16-byte aligned");
+    if (y && ((uintptr_t)y & 3) != 0) return fail(MX4_ERR_ARGUMENT, "y must be 4-byte aligned");
+    DeviceGuard g(ctx->device);
+    if (!w->bf16 && mx4::gemv_m1_supported(w->cols) && scales_foldable(w)) {
+        mx4::GemvArgs a{w->packed, w->scales, x, y, 1, w->rows, w->cols, xt == MX4_BF16, ctx->stream};
+        hipError_t e = mx4::launch_gemv_m1_argmax(a, ctx->am_partial, kArgmaxPartials, idx, ctx->cus);
+        if (e == hipSuccess) return MX4_OK;
+        if (e != hipErrorNotSupported) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
+    }
+    // no fused instance for this shape: the projection, then the argmax kernel
+    float* logits = y;
+    if (!logits) {
+        mx4_status st = ensure_buffer(ctx, &ctx->logits, &ctx->logits_cap, (uint64_t)w->rows * 4);
+        if (st != MX4_OK) return st;
+        logits = static_cast<float*>(ctx->logits);
+    }
+    mx4_status st = run_matmul(ctx, x, xt, 1, w, logits, MX4_PATH_AUTO);
+    if (st != MX4_OK) return st;
+    hipError_t e = mx4::launch_argmax_rows(logits, 1, w->rows, idx, ctx->am_partial, kArgmaxPartials, ctx->cus,
+                                           ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "argmax launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status mx4_embed(mx4_context* ctx, const mx4_weight* w, const uint32_t* ids, uint32_t count, uint16_t* out) {
+    if (!ctx || !w || (count && (!ids || !out))) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
+    if (w->cols % 32 != 0) return fail(MX4_ERR_SHAPE, "embedding rows must be a multiple of 32 wide");
+    if (((uintptr_t)out & 15) != 0) return fail(MX4_ERR_ARGUMENT, "out must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    hipError_t e = mx4::launch_embed(w->packed, w->scales, w->bf16, ids, count, w->rows, w->cols, out, ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "embed launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
 mx4_status mx4_dequantize(mx4_context* ctx, const mx4_weight* w, float* out) {
     if (!ctx || !w || !out) return fail(MX4_ERR_ARGUMENT, "null argument");
     if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "not an MXFP4 weight");
@@ -815,7 +866,8 @@ mx4_status mx4_argmax_rows(mx4_context* ctx, const float* x, uint32_t rows, uint
     if (!ctx || !x || !out) return fail(MX4_ERR_ARGUMENT, "null argument");
     if (width == 0) return fail(MX4_ERR_ARGUMENT, "argmax of an empty row");
     DeviceGuard g(ctx->device);
-    hipError_t e = mx4::launch_argmax_rows(x, rows, width, out, ctx->stream);
+    hipError_t e = mx4::launch_argmax_rows(x, rows, width, out, ctx->am_partial, kArgmaxPartials, ctx->cus,
+                                           ctx->stream);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "argmax launch failed: %s", hipGetErrorString(e));
     return MX4_OK;
 }

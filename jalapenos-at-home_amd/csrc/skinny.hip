@@ -28,9 +28,6 @@ namespace mx4 {
 
 namespace {
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
 
 constexpr int kNT = 2;  // streamed once: do not keep in the caches
 

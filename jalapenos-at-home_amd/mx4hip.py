@@ -67,6 +67,8 @@ SIGNATURES = {
     "mx4_matmul_mx": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
     "mx4_reserve_prefill": (_int, [_vp, _u32, _u32]),
     "mx4_weight_prepare_prefill": (_int, [_vp]),
+    "mx4_matmul_argmax": (_int, [_vp, _vp, _int, _vp, _vp, _vp]),
+    "mx4_embed": (_int, [_vp, _vp, _vp, _u32, _vp]),
     "mx4_weight_upload_bf16": (_int, [_vp, _vp, _u32, _u32, ctypes.POINTER(_vp)]),
     "mx4_prefill_act_bytes": (_int, [_u32, _u32, _int, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
     "mx4_prefill_quantize": (_int, [_vp, _vp, _int, _u32, _u32, _int, _vp, _vp]),
@@ -363,6 +365,13 @@ class Context:
     def prefill_matmul(self, codes: DeviceBuffer, scales: DeviceBuffer, act: int, m: int, w: Weight,
                        y: DeviceBuffer) -> None:
         check(lib().mx4_prefill_matmul(self.handle, codes.ptr, scales.ptr, act, m, w.handle, y.ptr))
+
+    def matmul_argmax(self, x: DeviceBuffer, xtype: int, w: Weight, y, idx: DeviceBuffer) -> None:
+        """M = 1 projection + greedy argmax into idx (uint32); y: DeviceBuffer or None."""
+        check(lib().mx4_matmul_argmax(self.handle, x.ptr, xtype, w.handle, y.ptr if y is not None else None, idx.ptr))
+
+    def embed(self, w: Weight, ids: DeviceBuffer, count: int, out: DeviceBuffer) -> None:
+        check(lib().mx4_embed(self.handle, w.handle, ids.ptr, count, out.ptr))
 
     def dequantize(self, w: Weight, out: DeviceBuffer) -> None:
         check(lib().mx4_dequantize(self.handle, w.handle, out.ptr))

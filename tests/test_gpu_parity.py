@@ -355,6 +355,77 @@ def test_lm_head_greedy_argmax_identical(mx4, ctx, oracle):
         assert_close(y, ref, "lm_head")
         assert int(idx.download(np.uint32, 1)[0]) == oracle.argmax(ref[0])
         assert oracle.argmax(y[0]) == oracle.argmax(ref[0])
+        # the fused lm_head + argmax, with and without writing the logits
+        y2 = ctx.buffer(n * 4)
+        for yy in (y2, None):
+            idx.upload(np.full(4, 0xFFFFFFFF, np.uint32))
+            ctx.matmul_argmax(xb, mx4.BF16, w, yy, idx)
+            assert int(idx.download(np.uint32, 1)[0]) == oracle.argmax(ref[0])
+        assert np.array_equal(y2.download(np.float32).reshape(1, n), y)
+
+
+@pytest.mark.parametrize("k", [2048, 4096])
+def test_matmul_argmax_first_max_rule(mx4, ctx, oracle, k):
+    """The fused argmax keeps engine/src/model.rs:288-296 exactly: ties go to the
+    lowest row, a maximum in the last row is found, NaN logits never win unless
+    in row 0 (then row 0 is the answer), +0 and -0 are equal."""
+    n = 3001
+    rng = np.random.default_rng(k)
+    idx = ctx.buffer(16)
+
+    def run(packed, scales, x, xt=mx4.F32):
+        w = ctx.upload_weight(packed, scales, n, k)
+        xb = ctx.to_device(np.ascontiguousarray(x, np.float32))
+        ctx.matmul_argmax(xb, xt, w, None, idx)
+        got = int(idx.download(np.uint32, 1)[0])
+        ref = oracle.matmul(np.asarray(x, np.float32).reshape(1, k), packed.reshape(-1), scales.reshape(-1))[0]
+        w.release()
+        return got, ref
+
+    scales = np.full((n, k // 32), 120, np.uint8)
+    x = rng.standard_normal(k).astype(np.float32)
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    got, ref = run(packed, scales, x)
+    assert got == oracle.argmax(ref)
+    # the same maximal row planted at 5, 1700 and the last row: 5 wins; then only the last row
+    p2 = packed.copy()
+    p2[[5, 1700, n - 1]] = 0x77
+    got, ref = run(p2, scales, np.abs(x))
+    assert ref[5] == ref[1700] == ref[n - 1] and got == oracle.argmax(ref) == 5
+    p3 = packed.copy()
+    p3[n - 1] = 0x77
+    got, ref = run(p3, scales, np.abs(x))
+    assert got == oracle.argmax(ref) == n - 1
+    # all-zero weights: every logit is +0 or -0 -> row 0
+    got, ref = run(np.zeros_like(packed), scales, x)
+    assert got == oracle.argmax(ref) == 0
+    # NaN activations: every logit NaN -> row 0
+    xn = x.copy()
+    xn[3] = np.nan
+    got, ref = run(packed, scales, xn)
+    assert np.all(np.isnan(ref)) and got == oracle.argmax(ref) == 0
+
+
+@pytest.mark.parametrize("kind", ["mxfp4", "bf16"])
+def test_embed_rows(mx4, ctx, oracle, kind):
+    """engine/src/lib.rs:222-227: decoded rows cut to bf16 (low 16 bits dropped),
+    bit for bit; ids past the table give zero rows."""
+    rows, cols = 777, 2048
+    rng = np.random.default_rng(9)
+    if kind == "mxfp4":
+        w = ctx.synth_weight(55, rows, cols, 0.02)
+        packed, scales = ctx.download_weight(w)
+        table = (f32_bits(oracle.dequantize(packed, scales)) >> 16).astype(np.uint16)
+    else:
+        table = rng.integers(0, 1 << 16, (rows, cols), dtype=np.uint16)
+        w = ctx.upload_weight_bf16(table, rows, cols)
+    ids = np.array([0, rows - 1, 5, 5, 400, rows, 2 ** 31], np.uint32)
+    out = ctx.buffer(len(ids) * cols * 2)
+    ctx.embed(w, ctx.to_device(ids), len(ids), out)
+    got = out.download(np.uint16).reshape(len(ids), cols)
+    for t, i in enumerate(ids):
+        expected = table[i] if i < rows else np.zeros(cols, np.uint16)
+        assert np.array_equal(got[t], expected), (t, i)
 
 
 def test_argmax_rows_first_max_rule(mx4, ctx, oracle):
@@ -368,6 +439,32 @@ def test_argmax_rows_first_max_rule(mx4, ctx, oracle):
     ctx.argmax_rows(xb, 4, x.shape[1], out)
     got = out.download(np.uint32).tolist()
     assert got == [oracle.argmax(r) for r in x]
+
+
+@pytest.mark.parametrize("rows,width", [(1, 1), (3, 100), (2, 1024), (2, 1025), (1, 1 << 20), (5, 70001),
+                                        (9000, 64), (600, 3000)])
+def test_argmax_rows_pieces(mx4, ctx, oracle, rows, width):
+    """Rows split over one or many blocks (one launch or keys + reduction),
+    with the rule's corner cases planted where pieces meet."""
+    rng = np.random.default_rng(rows * 7919 + width)
+    x = rng.standard_normal((rows, width)).astype(np.float32)
+    x[0, rng.integers(0, width)] = np.nan
+    if width > 2:
+        r = rows // 2
+        x[r, [width // 2, width - 1]] = 50.0                   # tie across pieces -> the lower
+        x[r, 0] = np.nan if rows > 1 else x[r, 0]               # NaN in column 0 wins row r
+    if rows > 2:
+        x[1, :] = -np.inf
+        x[1, width - 1] = -0.0
+        x[1, width // 3] = 0.0                                  # +0 and -0 tie -> the lower
+    if rows > 3:
+        x[2, :] = np.nan                                        # all NaN -> 0
+        x[3, :] = -np.inf                                       # all -inf -> 0
+    xb, out = ctx.to_device(x), ctx.buffer(4 * rows)
+    ctx.argmax_rows(xb, rows, width, out)
+    got = out.download(np.uint32)
+    want = np.array([oracle.argmax(row) for row in x], np.uint32)
+    assert np.array_equal(got, want), np.nonzero(got != want)[0][:10]
 
 
 # ------------------------------------------------------------------ generic / odd shapes
