@@ -70,6 +70,9 @@ struct PrefillArgs {
     uint32_t m, n, k;
     bool fp8;                 // activations are MX-FP8 (E4M3) instead of MXFP4
     hipStream_t stream;
+    // 0: the default for the shape; else the workgroup tile (rows, columns)
+    // and K split inside it of a compiled instance (hipErrorNotSupported if none)
+    uint32_t tile_m = 0, tile_n = 0, split_k = 0;
 };
 bool prefill_supported(uint32_t m, uint32_t n, uint32_t k);
 hipError_t launch_prefill(const PrefillArgs& a, int cus);

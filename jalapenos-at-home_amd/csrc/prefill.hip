@@ -228,18 +228,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[i][j][v] += red[wn][(i * TN + j) * 16 + v][lane];
     }
+    // Branch-free stores through a resource over y (prefill_supported keeps
+    // row n 4 + 4 col below 2^31 over the whole grid): rows past m fall
+    // outside it, and a column past n is biased by 2^31, past its end, so the
+    // hardware drops both. (Guarded stores cost a branch per element.)
     const uint32_t r32 = lane % 32, h = lane / 32;
+    const __amdgpu_buffer_rsrc_t yr = rsrc(y, m * n * 4);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int j = 0; j < TN; ++j) {
+        const uint32_t col = n0 + 32 * j + r32;
+        const uint32_t cb = 4 * col + (col < n ? 0u : 0x80000000u);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const uint32_t col = n0 + 32 * j + r32;
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const uint32_t row = m0 + 32 * i + 8 * (v / 4) + 4 * h + (v % 4);
-                if (row < m && col < n) y[(size_t)row * n + col] = acc[i][j][v];
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][v]), yr, row * n * 4 + cb, 0, 0);
             }
-        }
+    }
 }
 
 // Row-major codes -> fragment-native order. One thread per 16-byte output
@@ -298,6 +304,20 @@ hipError_t go(const PrefillArgs& a) {
 
 template <bool A_FP8>
 hipError_t dispatch(const PrefillArgs& a) {
+    if (a.tile_m != 0) {
+        // tuning: one explicit instance. Workgroup tiles: 128 x 192 and
+        // 128 x 128 over the full K; 64 x 128 with K halves inside it.
+        if (a.tile_m == 128 && a.tile_n == 192 && a.split_k == 1 && a.k % 512 == 0)
+            return go<A_FP8, 2, 3, 2, 4, 1, 2, 0>(a);
+        if (a.tile_m == 128 && a.tile_n == 128 && a.split_k == 1)
+            return a.k % 512 == 0 ? go<A_FP8, 2, 2, 2, 4, 1, 2, 0>(a) : go<A_FP8, 2, 2, 2, 2, 1, 1, 0>(a);
+        if (a.tile_m == 64 && a.tile_n == 128 && a.split_k == 2) {
+            if (a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 2, 2, 32>(a);
+            if (a.k == 12288) return go<A_FP8, 2, 2, 2, 4, 2, 2, 96>(a);
+            if (a.k % 512 == 0) return go<A_FP8, 2, 2, 2, 4, 2, 2, 0>(a);
+        }
+        return hipErrorNotSupported;
+    }
     // measured on MI355X at M = 512 (Qwen3-8B shapes): wide N keeps 2 x 3 tiles
     // per wave over the full K; otherwise 2 x 2 tiles with K split in two
     // inside the workgroup, fully unrolled for the model's K sizes
@@ -313,9 +333,12 @@ hipError_t dispatch(const PrefillArgs& a) {
 }  // namespace
 
 bool prefill_supported(uint32_t m, uint32_t n, uint32_t k) {
-    // fragment buffers are addressed with 32-bit offsets
+    // fragment buffers are addressed with 32-bit offsets, and so is y over
+    // the whole grid (workgroup tiles of at most 128 rows and 192 columns)
     const uint64_t mp = ((uint64_t)m + 31) / 32 * 32, np = ((uint64_t)n + 31) / 32 * 32;
-    return m >= 1 && n >= 1 && k % 256 == 0 && np * (k / 2) < (1ull << 31) && mp * k < (1ull << 31);
+    const uint64_t y_span = ((uint64_t)m + 128) * n * 4 + ((uint64_t)n + 192) * 4;
+    return m >= 1 && n >= 1 && k % 256 == 0 && np * (k / 2) < (1ull << 31) && mp * k < (1ull << 31) &&
+           y_span < (1ull << 31);
 }
 
 uint64_t fragment_bytes(uint32_t rows, uint32_t k, bool fp8) {

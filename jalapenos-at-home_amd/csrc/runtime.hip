@@ -167,6 +167,11 @@ uint64_t prefill_workspace_bytes(uint64_t m, uint64_t cols, bool fp8) {
     return ((qbytes + 255) & ~255ull) + mx4::fragment_scale_bytes((uint32_t)m, (uint32_t)cols);
 }
 
+mx4::PrefillArgs prefill_args(mx4_context* ctx, const mx4_weight* w, const uint8_t* xf, const uint8_t* xsf,
+                              float* y, uint32_t m, bool fp8) {
+    return mx4::PrefillArgs{w->frag, w->frag_scales, xf, xsf, y, m, w->rows, w->cols, fp8, ctx->stream};
+}
+
 // The weight's fragment-native copy: built once, outside any recorded pass.
 mx4_status prepare_fragments(mx4_context* ctx, mx4_weight* w) {
     if (w->frag) return MX4_OK;
@@ -628,7 +633,7 @@ mx4_status mx4_matmul_prefill(mx4_context* ctx, const void* x, mx4_dtype xt, uin
     if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
     if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
     if (!mx4::prefill_supported(m, w->rows, w->cols))
-        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
+        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0 and operands under 2 GiB");
     DeviceGuard g(ctx->device);
     const bool fp8 = act == MX4_ACT_MXFP8;
     mx4_weight* wm = const_cast<mx4_weight*>(w);  // the fragment copy is a cache of the weight
@@ -641,8 +646,7 @@ mx4_status mx4_matmul_prefill(mx4_context* ctx, const void* x, mx4_dtype xt, uin
     uint8_t* xsf = xf + qoff;
     hipError_t e = mx4::launch_quantize_fragments(x, xt == MX4_BF16, m, w->cols, fp8, xf, xsf, ctx->flags, ctx->stream);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "requantize launch failed: %s", hipGetErrorString(e));
-    mx4::PrefillArgs a{wm->frag, wm->frag_scales, xf, xsf, y, m, w->rows, w->cols, fp8, ctx->stream};
-    e = mx4::launch_prefill(a, ctx->cus);
+    e = mx4::launch_prefill(prefill_args(ctx, wm, xf, xsf, y, m, fp8), ctx->cus);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
     return MX4_OK;
 }
@@ -721,7 +725,7 @@ mx4_status mx4_matmul_mx(mx4_context* ctx, const uint8_t* xq, const uint8_t* xs,
     if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
     if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
     if (!mx4::prefill_supported(m, w->rows, w->cols))
-        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
+        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0 and operands under 2 GiB");
     DeviceGuard g(ctx->device);
     const bool fp8 = act == MX4_ACT_MXFP8;
     mx4_weight* wm = const_cast<mx4_weight*>(w);
@@ -734,8 +738,7 @@ mx4_status mx4_matmul_mx(mx4_context* ctx, const uint8_t* xq, const uint8_t* xs,
     uint8_t* xsf = xf + qoff;
     hipError_t e = mx4::launch_to_fragments(xq, xs, m, w->cols, fp8, xf, xsf, ctx->stream);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "layout launch failed: %s", hipGetErrorString(e));
-    mx4::PrefillArgs a{wm->frag, wm->frag_scales, xf, xsf, y, m, w->rows, w->cols, fp8, ctx->stream};
-    e = mx4::launch_prefill(a, ctx->cus);
+    e = mx4::launch_prefill(prefill_args(ctx, wm, xf, xsf, y, m, fp8), ctx->cus);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
     return MX4_OK;
 }
@@ -773,14 +776,36 @@ mx4_status mx4_prefill_matmul(mx4_context* ctx, const uint8_t* codes, const uint
     if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
     if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
     if (!mx4::prefill_supported(m, w->rows, w->cols))
-        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
+        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0 and operands under 2 GiB");
     DeviceGuard g(ctx->device);
     mx4_weight* wm = const_cast<mx4_weight*>(w);
     mx4_status st = prepare_fragments(ctx, wm);
     if (st != MX4_OK) return st;
-    mx4::PrefillArgs a{wm->frag, wm->frag_scales, codes, scales, y, m, w->rows, w->cols, act == MX4_ACT_MXFP8,
-                       ctx->stream};
+    hipError_t e = mx4::launch_prefill(prefill_args(ctx, wm, codes, scales, y, m, act == MX4_ACT_MXFP8), ctx->cus);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status mx4_prefill_config(mx4_context* ctx, const uint8_t* codes, const uint8_t* scales, mx4_act_format act,
+                              uint32_t m, const mx4_weight* w, float* y, uint32_t tile_m, uint32_t tile_n,
+                              uint32_t split_k) {
+    if (!ctx || !codes || !scales || !w || !y) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
+    if (m == 0) return fail(MX4_ERR_ARGUMENT, "m must be at least 1");
+    if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
+    if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
+    if (!mx4::prefill_supported(m, w->rows, w->cols))
+        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0 and operands under 2 GiB");
+    DeviceGuard g(ctx->device);
+    mx4_weight* wm = const_cast<mx4_weight*>(w);
+    mx4_status st = prepare_fragments(ctx, wm);
+    if (st != MX4_OK) return st;
+    mx4::PrefillArgs a = prefill_args(ctx, wm, codes, scales, y, m, act == MX4_ACT_MXFP8);
+    a.tile_m = tile_m;
+    a.tile_n = tile_n;
+    a.split_k = split_k;
     hipError_t e = mx4::launch_prefill(a, ctx->cus);
+    if (e == hipErrorNotSupported) return fail(MX4_ERR_UNSUPPORTED, "no such prefill instance for this shape");
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
     return MX4_OK;
 }

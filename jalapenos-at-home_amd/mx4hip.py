@@ -23,6 +23,7 @@ STATUS = {
     4: "MX4_ERR_LENGTH", 5: "MX4_ERR_NAN_SCALE", 6: "MX4_ERR_NON_FINITE",
     7: "MX4_ERR_DEVICE", 8: "MX4_ERR_NO_MEMORY", 9: "MX4_ERR_UNSUPPORTED",
 }
+ERR_UNSUPPORTED = 9
 F32, BF16 = 0, 1
 PATH_AUTO, PATH_GEMV, PATH_SKINNY, PATH_GENERIC, PATH_PREFILL = 0, 1, 2, 3, 4
 ACT_MXFP4, ACT_MXFP8 = 1, 2
@@ -73,6 +74,7 @@ SIGNATURES = {
     "mx4_prefill_act_bytes": (_int, [_u32, _u32, _int, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
     "mx4_prefill_quantize": (_int, [_vp, _vp, _int, _u32, _u32, _int, _vp, _vp]),
     "mx4_prefill_matmul": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
+    "mx4_prefill_config": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp, _u32, _u32, _u32]),
     "mx4_pass_begin": (_int, [_vp]),
     "mx4_pass_end": (_int, [_vp, ctypes.POINTER(_vp)]),
     "mx4_pass_launch": (_int, [_vp, _vp]),
@@ -365,6 +367,12 @@ class Context:
     def prefill_matmul(self, codes: DeviceBuffer, scales: DeviceBuffer, act: int, m: int, w: Weight,
                        y: DeviceBuffer) -> None:
         check(lib().mx4_prefill_matmul(self.handle, codes.ptr, scales.ptr, act, m, w.handle, y.ptr))
+
+    def prefill_config(self, codes: DeviceBuffer, scales: DeviceBuffer, act: int, m: int, w: Weight,
+                       y: DeviceBuffer, tile_m: int, tile_n: int, split_k: int) -> int:
+        """Prefill GEMM with an explicit instance; returns the status (MX4_ERR_UNSUPPORTED if none)."""
+        return lib().mx4_prefill_config(self.handle, codes.ptr, scales.ptr, act, m, w.handle, y.ptr,
+                                        tile_m, tile_n, split_k)
 
     def matmul_argmax(self, x: DeviceBuffer, xtype: int, w: Weight, y, idx: DeviceBuffer) -> None:
         """M = 1 projection + greedy argmax into idx (uint32); y: DeviceBuffer or None."""

@@ -729,6 +729,47 @@ def test_prefill_quantize_once_matmul_many(mx4, ctx, oracle, act):
         assert np.array_equal(yb.download(np.float32).reshape(m, n), _run_prefill(mx4, ctx, x, w, act, mx4.BF16))
 
 
+PREFILL_INSTANCES = ([(4096, t) for t in ((128, 192, 1), (128, 128, 1), (64, 128, 2))] +
+                     [(12288, t) for t in ((128, 128, 1), (64, 128, 2))] +
+                     [(1536, t) for t in ((128, 192, 1), (128, 128, 1), (64, 128, 2))] +
+                     [(1280, (128, 128, 1)), (768, (128, 128, 1))])
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+@pytest.mark.parametrize("k,tile", PREFILL_INSTANCES, ids=[f"k{k}-{t[0]}x{t[1]}-ks{t[2]}" for k, t in PREFILL_INSTANCES])
+def test_prefill_instances_match_oracle(mx4, ctx, oracle, act, k, tile):
+    """Every prefill instance reachable through mx4_prefill_config (workgroup
+    tile, K halves inside the workgroup; unrolled and loop forms) on ragged m
+    and n against the oracle on dequant(requant(x)); twice, bitwise equal."""
+    tm, tn, ks = tile
+    m, n = (70, 300) if k <= 4096 else (40, 260)
+    code = mx4.ACT_MXFP4 if act == "mxfp4" else mx4.ACT_MXFP8
+    w = ctx.synth_weight(500 + tm + tn + ks, n, k, 0.02)
+    packed, scales = ctx.download_weight(w)
+    x = oracle.bf16_to_f32(oracle.synth_bf16(600 + k // 256, 1.0, m * k)).reshape(m, k)
+    ref, _ = _prefill_ref(oracle, x, packed, scales, act)
+    xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+    codes, sc = ctx.prefill_act_buffers(m, k, code)
+    ctx.prefill_quantize(xb, mx4.BF16, m, k, code, codes, sc)
+    yb = ctx.buffer(m * n * 4)
+    outs = []
+    for _ in range(2):
+        yb.upload(np.full(m * n, np.nan, np.float32))
+        assert ctx.prefill_config(codes, sc, code, m, w, yb, tm, tn, ks) == 0, mx4.last_error()
+        outs.append(yb.download(np.float32).reshape(m, n))
+    assert_close(outs[0], ref, f"prefill instance {tile} k={k} {act}")
+    assert np.array_equal(outs[0], outs[1])
+
+
+def test_prefill_config_rejects_unknown_instance(mx4, ctx):
+    m, n, k = 64, 256, 4096
+    w = ctx.synth_weight(7, n, k, 0.02)
+    codes, sc = ctx.prefill_act_buffers(m, k, mx4.ACT_MXFP4)
+    yb = ctx.buffer(m * n * 4)
+    assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 96, 256, 1) == mx4.ERR_UNSUPPORTED
+    assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 64, 128, 4) == mx4.ERR_UNSUPPORTED
+
+
 def test_prefill_recorded_pass_after_prepare(mx4, ctx, oracle):
     """The matrix-core copy of a weight is built outside the pass
     (mx4_weight_prepare_prefill) and the workspace reserved; every replay of the
