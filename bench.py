@@ -258,8 +258,8 @@ def main() -> int:
     ap.add_argument("--profile-traffic", action="store_true",
                     help="for counter runs: 2 eager grouped steps, then a 1 GiB device copy as the byte calibration")
     ap.add_argument("--profile-prefill", action="store_true",
-                    help="for profiler runs: only the M=512 prefill GEMMs (q, o, gate, up, down; MXFP4 and "
-                         "MX-FP8 activations), 5 launches each on requantized activations")
+                    help="for profiler runs: only the M=512 prefill (q, o, gate, up, down; MXFP4 and MX-FP8 "
+                         "activations): 5 GEMMs on requantized activations, then 5 requantize + GEMM calls")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -324,8 +324,11 @@ def main() -> int:
                 ctx.prefill_quantize(xb, mx4hip.BF16, m, k, code, xq, xsc)
                 for _ in range(5):
                     ctx.prefill_matmul(xq, xsc, code, m, w, yb)
+                for _ in range(5):
+                    ctx.matmul_prefill(xb, mx4hip.BF16, m, w, code, yb)
             ctx.synchronize()
-        print(json.dumps({"profile_prefill": True, "m": m, "launches_per_shape_and_format": 5}), flush=True)
+        print(json.dumps({"profile_prefill": True, "m": m, "gemm_launches_per_shape_and_format": 10,
+                          "requant_launches_per_shape_and_format": 6}), flush=True)
         ctx.close()
         return 0
 

@@ -356,7 +356,7 @@ __device__ __forceinline__ void finish_rowset(const Segs& sg, uint32_t rs, const
 // weight bytes with one team per workgroup). Dynamic LDS: x (k elements), then
 // the cross-wave partial sums [tpw][2][WG][R].
 template <bool XBF16, int WG, int BPL, int R, bool AM>
-__global__ __launch_bounds__(512) void gemv_m1_kernel(Segs sg, const void* __restrict__ x, uint32_t k) {
+__device__ __forceinline__ void gemv_m1_body(const Segs& sg, const void* __restrict__ x, uint32_t k) {
     constexpr uint32_t T = 64 * WG;  // threads per team
     const uint32_t tpw = blockDim.x / T;
     const uint32_t team = __builtin_amdgcn_readfirstlane(threadIdx.x / T);
@@ -432,6 +432,38 @@ __global__ __launch_bounds__(512) void gemv_m1_kernel(Segs sg, const void* __res
     }
 }
 
+// A group of up to four weights (their table passed by value).
+template <bool XBF16, int WG, int BPL, int R, bool AM>
+__global__ __launch_bounds__(512) void gemv_m1_kernel(Segs sg, const void* __restrict__ x, uint32_t k) {
+    gemv_m1_body<XBF16, WG, BPL, R, AM>(sg, x, k);
+}
+
+// One weight, every argument a plain scalar: this file is built with kernel
+// argument preloading, so on entry they already sit in SGPRs and the first
+// weight load issues without a scalar memory round trip (a by-value table
+// cannot be preloaded).
+template <bool XBF16, int WG, int BPL, int R, bool AM>
+__global__ __launch_bounds__(512) void gemv_m1_one_kernel(const uint8_t* __restrict__ packed,
+                                                          const uint8_t* __restrict__ scales,
+                                                          const void* __restrict__ x, float* __restrict__ y,
+                                                          uint32_t n, uint32_t k, uint32_t rowsets,
+                                                          uint64_t* __restrict__ am_partial) {
+    Segs sg;
+#pragma unroll
+    for (int q = 0; q < kMaxSegs; ++q) {
+        sg.packed[q] = packed;
+        sg.scales[q] = scales;
+        sg.y[q] = y;
+        sg.n[q] = n;
+        sg.first[q + 1] = rowsets;
+    }
+    sg.first[0] = 0;
+    sg.count = 1;
+    sg.rowsets = rowsets;
+    sg.am_partial = am_partial;
+    gemv_m1_body<XBF16, WG, BPL, R, AM>(sg, x, k);
+}
+
 // Generic exact kernel: any M (tokens processed MT at a time), any K % 32 == 0,
 // any scale byte. Every element is decoded exactly as engine/src/mxfp4.rs:27-33
 // does (level * 2^(s-127): subnormal for small bytes, inf for large levels at
@@ -499,7 +531,12 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* __rest
 template <bool XBF16, int WG, int BPL, int R>
 static hipError_t go_m1(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int tpw, hipStream_t st) {
     const size_t lds = (tpw > 1 ? (size_t)k * (XBF16 ? 2 : 4) : 0) + (size_t)tpw * 2 * WG * R * sizeof(float);
-    hipLaunchKernelGGL((gemv_m1_kernel<XBF16, WG, BPL, R, false>), dim3(grid), dim3(64 * WG * tpw), lds, st, sg, x, k);
+    if (sg.count == 1)
+        hipLaunchKernelGGL((gemv_m1_one_kernel<XBF16, WG, BPL, R, false>), dim3(grid), dim3(64 * WG * tpw), lds, st,
+                           sg.packed[0], sg.scales[0], x, sg.y[0], sg.n[0], k, sg.rowsets, (uint64_t*)nullptr);
+    else
+        hipLaunchKernelGGL((gemv_m1_kernel<XBF16, WG, BPL, R, false>), dim3(grid), dim3(64 * WG * tpw), lds, st, sg,
+                           x, k);
     return hipGetLastError();
 }
 
@@ -615,7 +652,8 @@ hipError_t launch_gemv_m1_group(const GemvGroup& g, int cus, const M1Config* for
 template <bool XBF16, int BPL, int R>
 static hipError_t go_am(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int tpw, uint32_t* idx, hipStream_t st) {
     const size_t lds = (tpw > 1 ? (size_t)k * (XBF16 ? 2 : 4) : 0) + (size_t)tpw * 2 * R * sizeof(float);
-    hipLaunchKernelGGL((gemv_m1_kernel<XBF16, 1, BPL, R, true>), dim3(grid), dim3(64 * tpw), lds, st, sg, x, k);
+    hipLaunchKernelGGL((gemv_m1_one_kernel<XBF16, 1, BPL, R, true>), dim3(grid), dim3(64 * tpw), lds, st, sg.packed[0],
+                       sg.scales[0], x, sg.y[0], sg.n[0], k, sg.rowsets, sg.am_partial);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_argmax_reduce(sg.am_partial, 1, grid, idx, st);

@@ -92,7 +92,7 @@ hipError_t launch_quantize_mxfp4(const void* in, bool in_bf16, uint64_t rows, ui
 hipError_t launch_quantize_fp8(const void* in, bool in_bf16, uint64_t rows, uint32_t cols,
                                uint8_t* codes, uint8_t* scales, uint32_t* bad, hipStream_t s);
 // The same two rules writing the fragment-native layout of prefill.hip
-// (cols % 256 == 0); rows past `rows` in the last group of 32 are left unset.
+// (cols % 256 == 0); rows past `rows` in the last group of 32 are written as zeros.
 hipError_t launch_quantize_fragments(const void* in, bool in_bf16, uint32_t rows, uint32_t cols, bool fp8,
                                      uint8_t* codes_f, uint8_t* scales_f, uint32_t* bad, hipStream_t s);
 // engine/src/mxfp4.rs:35-49 on device: packed/scales -> f32 [elements]

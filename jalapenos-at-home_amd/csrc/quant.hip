@@ -174,17 +174,33 @@ hipError_t launch_quantize_fp8(const void* in, bool in_bf16, uint64_t rows, uint
     return hipGetLastError();
 }
 
-// Fragment-native output (prefill.hip): the same rules as above, one thread
-// per 32-element block, stores addressed for the matrix-core fragments.
+// Fragment-native output (prefill.hip): the same rules as above. A workgroup
+// of four waves takes one row group g and scale quad q; wave u quantizes
+// k-step 4 q + u, lane t the block 8 q + 2 u + t / 32 of row 32 g + t % 32 --
+// exactly lane t's part of fragment (g, 4 q + u), so each wave stores one
+// contiguous 1 KiB (FP8: 2 KiB) and reads whole 128-byte spans of 32 rows
+// (lanes t and t + 32 read the two halves). The four scale bytes of lane t
+// (byte u from wave u) meet in LDS and leave as one 4-byte word, 256 bytes per
+// workgroup. Rows past `rows` in the last group are written as zero codes and
+// scales.
 template <bool BF16, bool FP8>
-__global__ __launch_bounds__(256) void quantize_fragments_kernel(const void* __restrict__ in, uint64_t blocks,
+__global__ __launch_bounds__(256) void quantize_fragments_kernel(const void* __restrict__ in, uint32_t rows,
                                                                  uint32_t cols, uint8_t* __restrict__ codes,
                                                                  uint8_t* __restrict__ scales,
                                                                  uint32_t* __restrict__ bad) {
-    const uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= blocks) return;
+    __shared__ uint32_t sbytes[4][64];
+    const uint32_t lane = threadIdx.x % 64, u = threadIdx.x / 64;
+    const uint32_t nblk = cols / 32, nk = cols / 64, nq = cols / 256;
+    const uint32_t q = blockIdx.x % nq, g = blockIdx.x / nq;
+    const uint32_t r32 = lane % 32, half = lane / 32;
+    const uint32_t row = 32 * g + r32, kk = 4 * q + u;
     float v[32];
-    load_block32<BF16>(in, b, v);
+    if (row < rows) {
+        load_block32<BF16>(in, (uint64_t)row * nblk + 2 * kk + half, v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i] = 0.0f;
+    }
     float amax = 0.0f;
     bool finite = true;
 #pragma unroll
@@ -194,11 +210,6 @@ __global__ __launch_bounds__(256) void quantize_fragments_kernel(const void* __r
         amax = a > amax ? a : amax;
     }
     if (!finite) atomicOr(bad, 1u);
-    const uint32_t nblk = cols / 32, nk = cols / 64, nq = cols / 256;
-    const uint64_t row = b / nblk;
-    const uint32_t blk = (uint32_t)(b % nblk);
-    const uint64_t g = row / 32;
-    const uint32_t r32 = (uint32_t)(row % 32), kk = blk / 2, half = blk % 2;
     uint32_t s;
     if constexpr (FP8) {
         s = fp8_scale_byte(amax);
@@ -214,7 +225,8 @@ __global__ __launch_bounds__(256) void quantize_fragments_kernel(const void* __r
                 for (int i = 0; i < 4; ++i) word |= e4m3_code(v[16 * p + 4 * d + i], s) << (8 * i);
                 out[d] = word;
             }
-            *reinterpret_cast<u32x4*>(codes + (g * nk + kk) * 2048 + half * 1024 + (32 * p + r32) * 16) = out;
+            *reinterpret_cast<u32x4*>(codes + ((uint64_t)g * nk + kk) * 2048 + half * 1024 + (32 * p + r32) * 16) =
+                out;
         }
     } else {
         s = mxfp4_scale_byte(amax);
@@ -226,28 +238,38 @@ __global__ __launch_bounds__(256) void quantize_fragments_kernel(const void* __r
             for (int i = 0; i < 8; ++i) word |= mxfp4_code(v[8 * d + i], s) << (4 * i);
             out[d] = word;
         }
-        *reinterpret_cast<u32x4*>(codes + ((g * nk + kk) * 64 + 32 * half + r32) * 16) = out;
+        *reinterpret_cast<u32x4*>(codes + (((uint64_t)g * nk + kk) * 64 + lane) * 16) = out;
     }
     // block 8q + 2u + h: byte u of lane 32h + r32 of quad q
-    const uint32_t q = blk / 8, u = (blk % 8) / 2, h = blk % 2;
-    scales[((g * nq + q) * 64 + 32 * h + r32) * 4 + u] = (uint8_t)s;
+    sbytes[u][lane] = s;
+    __syncthreads();
+    if (u == 0) {
+        const uint32_t word = sbytes[0][lane] | (sbytes[1][lane] << 8) | (sbytes[2][lane] << 16) | (sbytes[3][lane] << 24);
+        reinterpret_cast<uint32_t*>(scales)[((uint64_t)g * nq + q) * 64 + lane] = word;
+    }
 }
 
 hipError_t launch_quantize_fragments(const void* in, bool in_bf16, uint32_t rows, uint32_t cols, bool fp8,
                                      uint8_t* codes_f, uint8_t* scales_f, uint32_t* bad, hipStream_t s) {
-    const uint64_t blocks = (uint64_t)rows * (cols / 32);
-    if (blocks == 0) return hipSuccess;
-    dim3 grid((unsigned)((blocks + 255) / 256));
+    if (rows == 0 || cols == 0) return hipSuccess;
+    if (cols % 256 != 0) return hipErrorInvalidValue;
+    const uint64_t wgs = (uint64_t)((rows + 31) / 32) * (cols / 256);
+    if (wgs > 0x7fffffffu) return hipErrorInvalidValue;
+    dim3 grid((unsigned)wgs);
     if (in_bf16) {
         if (fp8)
-            hipLaunchKernelGGL((quantize_fragments_kernel<true, true>), grid, dim3(256), 0, s, in, blocks, cols, codes_f, scales_f, bad);
+            hipLaunchKernelGGL((quantize_fragments_kernel<true, true>), grid, dim3(256), 0, s, in, rows, cols, codes_f,
+                               scales_f, bad);
         else
-            hipLaunchKernelGGL((quantize_fragments_kernel<true, false>), grid, dim3(256), 0, s, in, blocks, cols, codes_f, scales_f, bad);
+            hipLaunchKernelGGL((quantize_fragments_kernel<true, false>), grid, dim3(256), 0, s, in, rows, cols, codes_f,
+                               scales_f, bad);
     } else {
         if (fp8)
-            hipLaunchKernelGGL((quantize_fragments_kernel<false, true>), grid, dim3(256), 0, s, in, blocks, cols, codes_f, scales_f, bad);
+            hipLaunchKernelGGL((quantize_fragments_kernel<false, true>), grid, dim3(256), 0, s, in, rows, cols,
+                               codes_f, scales_f, bad);
         else
-            hipLaunchKernelGGL((quantize_fragments_kernel<false, false>), grid, dim3(256), 0, s, in, blocks, cols, codes_f, scales_f, bad);
+            hipLaunchKernelGGL((quantize_fragments_kernel<false, false>), grid, dim3(256), 0, s, in, rows, cols,
+                               codes_f, scales_f, bad);
     }
     return hipGetLastError();
 }

@@ -712,6 +712,56 @@ def test_prefill_mx_entry_matches_prefill(mx4, ctx, oracle, act):
     assert np.array_equal(yb.download(np.float32).reshape(m, n), y_ref)
 
 
+def _to_fragments(codes, scales, fp8):
+    """Row-major requantized activations -> the matrix-core fragment order
+    (rows padded with zeros to a multiple of 32)."""
+    r = codes.shape[0]
+    g = (r + 31) // 32
+    cp = np.zeros((g * 32, codes.shape[1]), np.uint8)
+    cp[:r] = codes
+    sp = np.zeros((g * 32, scales.shape[1]), np.uint8)
+    sp[:r] = scales
+    nq = scales.shape[1] // 8
+    if fp8:
+        nk = codes.shape[1] // 64   # byte 32 p + 16 h + b of a k-step -> [g, kk, p, h, r32, b]
+        frag = cp.reshape(g, 32, nk, 2, 2, 16).transpose(0, 2, 3, 4, 1, 5)
+    else:
+        nk = codes.shape[1] // 32   # byte 16 h + b of a k-step -> [g, kk, h, r32, b]
+        frag = cp.reshape(g, 32, nk, 2, 16).transpose(0, 2, 3, 1, 4)
+    sfrag = sp.reshape(g, 32, nq, 4, 2).transpose(0, 2, 4, 1, 3)  # block 8q + 2u + h -> [g, q, h, r32, u]
+    return frag.reshape(-1), sfrag.reshape(-1)
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+@pytest.mark.parametrize("xtype", ["bf16", "f32"])
+def test_prefill_quantize_fragments_bit_exact(mx4, ctx, oracle, act, xtype):
+    """mx4_prefill_quantize = the oracle's quantizer (python/quantize_mxfp4.py:18-39,
+    or the E4M3 rule) permuted into the fragment order, byte for byte, with the
+    padding rows of the last group zero; ragged rows, exact midpoints, signed zeros."""
+    rng = np.random.default_rng(17)
+    m, k = 45, 768
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[3, :64] = (rng.integers(-24, 25, 64) * 0.25).astype(np.float32)
+    x[5, :32] = -0.0
+    x[7, 32:64] = rng.standard_normal(32).astype(np.float32) * 1e-38
+    if xtype == "bf16":
+        bits = (f32_bits(x) >> 16).astype(np.uint16)
+        x = oracle.bf16_to_f32(bits).reshape(m, k)
+        xb, t = ctx.to_device(bits), mx4.BF16
+    else:
+        xb, t = ctx.to_device(x), mx4.F32
+    fp8 = act == "mxfp8"
+    code = mx4.ACT_MXFP8 if fp8 else mx4.ACT_MXFP4
+    codes, sc = ctx.prefill_act_buffers(m, k, code)
+    codes.upload(np.full(codes.nbytes, 0xA5, np.uint8))
+    sc.upload(np.full(sc.nbytes, 0xA5, np.uint8))
+    ctx.prefill_quantize(xb, t, m, k, code, codes, sc)
+    want_c, want_s = (oracle.quantize_fp8 if fp8 else oracle.quantize)(x)
+    frag, sfrag = _to_fragments(want_c, want_s, fp8)
+    assert np.array_equal(codes.download(np.uint8), frag)
+    assert np.array_equal(sc.download(np.uint8), sfrag)
+
+
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
 def test_prefill_quantize_once_matmul_many(mx4, ctx, oracle, act):
     """Requantize x once in the matrix-core layout and reuse it for two weights
