@@ -182,7 +182,7 @@ hipError_t launch_quantize_fp8(const void* in, bool in_bf16, uint64_t rows, uint
 // (lanes t and t + 32 read the two halves). The four scale bytes of lane t
 // (byte u from wave u) meet in LDS and leave as one 4-byte word, 256 bytes per
 // workgroup. Rows past `rows` in the last group are written as zero codes and
-// scales.
+// scales; a block with a non-finite value gets scale byte 0xff (E8M0 NaN).
 template <bool BF16, bool FP8>
 __global__ __launch_bounds__(256) void quantize_fragments_kernel(const void* __restrict__ in, uint32_t rows,
                                                                  uint32_t cols, uint8_t* __restrict__ codes,
@@ -240,8 +240,10 @@ __global__ __launch_bounds__(256) void quantize_fragments_kernel(const void* __r
         }
         *reinterpret_cast<u32x4*>(codes + (((uint64_t)g * nk + kk) * 64 + lane) * 16) = out;
     }
-    // block 8q + 2u + h: byte u of lane 32h + r32 of quad q
-    sbytes[u][lane] = s;
+    // block 8q + 2u + h: byte u of lane 32h + r32 of quad q. A block holding
+    // inf or NaN gets the E8M0 NaN byte, so its products -- and the row's
+    // outputs -- are NaN instead of finite values of a meaningless scale.
+    sbytes[u][lane] = finite ? s : 0xffu;
     __syncthreads();
     if (u == 0) {
         const uint32_t word = sbytes[0][lane] | (sbytes[1][lane] << 8) | (sbytes[2][lane] << 16) | (sbytes[3][lane] << 24);

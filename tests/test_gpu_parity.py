@@ -763,6 +763,24 @@ def test_prefill_quantize_fragments_bit_exact(mx4, ctx, oracle, act, xtype):
 
 
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+def test_prefill_non_finite_activations_give_nan_rows(mx4, ctx, oracle, act):
+    """A token row holding inf or NaN: the reference's sums over it are inf or
+    NaN (engine/src/lib.rs:240-266); requantized here, its blocks carry the E8M0
+    NaN scale, so every output of that row is NaN. The other rows are unaffected."""
+    m, n, k = 40, 96, 512
+    w = ctx.synth_weight(33, n, k, 0.02)
+    packed, scales = ctx.download_weight(w)
+    x = oracle.bf16_to_f32(oracle.synth_bf16(34, 1.0, m * k)).reshape(m, k)
+    x[3, 100] = np.inf
+    x[17, 5] = np.nan
+    y = _run_prefill(mx4, ctx, x, w, act, mx4.F32)
+    assert np.all(np.isnan(y[3])) and np.all(np.isnan(y[17]))
+    ok = np.setdiff1d(np.arange(m), [3, 17])
+    ref, _ = _prefill_ref(oracle, x[ok], packed, scales, act)
+    assert_close(y[ok], ref, f"prefill {act} finite rows")
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
 def test_prefill_quantize_once_matmul_many(mx4, ctx, oracle, act):
     """Requantize x once in the matrix-core layout and reuse it for two weights
     (q|k|v style): each product equals the fused mx4_matmul_prefill bit for bit."""
