@@ -53,7 +53,7 @@ typedef enum mx4_dtype { MX4_F32 = 0, MX4_BF16 = 1 } mx4_dtype;
  * engine/src/gpu.rs:469-515 re-tuned for gfx950. */
 typedef enum mx4_path {
     MX4_PATH_AUTO = 0,
-    MX4_PATH_GEMV = 1,     /* M == 1 decode GEMV (no MFMA) */
+    MX4_PATH_GEMV = 1,     /* decode GEMV (no MFMA): M == 1, or 2 <= M <= 4 with bf16 x */
     MX4_PATH_SKINNY = 2,   /* exact skinny kernel on bf16 MFMA, M <= 32, K in {2,4,6,8,12}*1024 */
     MX4_PATH_GENERIC = 3,  /* exact fallback for any M and K % 32 == 0 */
     MX4_PATH_PREFILL = 4   /* block-scaled MFMA on requantized activations */
@@ -171,6 +171,13 @@ mx4_status mx4_matmul_group(mx4_context *ctx, const void *x_dev, mx4_dtype x_typ
 mx4_status mx4_gemv_config(mx4_context *ctx, const void *x_dev, mx4_dtype x_type,
                            const mx4_weight *const *w, float *const *y_dev, uint32_t count,
                            int team_waves, int rows_per_team, int teams_per_workgroup, uint32_t teams);
+
+/* Tuning hook for the few-token GEMV (2 <= m <= 4 bf16 token rows, the
+ * MX4_PATH_GEMV kernel for m > 1): the number of teams walking the row-sets
+ * and of teams per workgroup sharing one LDS copy of the token rows. Zero
+ * keeps the default; a shape that cannot be launched gives MX4_ERR_UNSUPPORTED. */
+mx4_status mx4_gemv_tokens_config(mx4_context *ctx, const void *x_dev, uint32_t m, const mx4_weight *w,
+                                  float *y_dev, uint32_t teams, uint32_t teams_per_workgroup);
 
 /* Prefill on CDNA4 block-scaled MFMA (V_MFMA_SCALE_F32_*_F8F6F4): x is
  * requantized per 32 along K (MXFP4 by python/quantize_mxfp4.py:18-39, or MX

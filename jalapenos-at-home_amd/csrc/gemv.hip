@@ -464,6 +464,144 @@ __global__ __launch_bounds__(512) void gemv_m1_one_kernel(const uint8_t* __restr
     gemv_m1_body<XBF16, WG, BPL, R, AM>(sg, x, k);
 }
 
+// A few tokens (speculative verify, 2 <= m <= MT, bf16 activations): the
+// M = 1 weight stream -- each lane's 16-byte blocks of R rows, 1 KiB contiguous
+// per wave load instruction, the next row-set in flight while the current one
+// is reduced -- with every converted weight pair multiplied into all MT token
+// rows, so the weights are read once for all of them. A team (one workgroup)
+// of WG waves splits each row's K; each lane keeps the x blocks of every token
+// in registers (token slots >= m hold zeros and write nothing). The R * MT
+// per-lane sums go through the same butterfly as the M = 1 kernel, then (for
+// WG > 1) through LDS.
+template <int BPL, int MT>
+__device__ __forceinline__ void rows_dot_mt(const LaneX<true, BPL> (&xr)[MT], const u32x4 (&w)[BPL],
+                                            const uint32_t (&s)[BPL], float* acc) {
+#pragma unroll
+    for (int tok = 0; tok < MT; ++tok) acc[tok] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+        const float sc = __uint_as_float(s[j] << 23);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const bf16x2 w0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j][d], sc, 0);
+            const bf16x2 w1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j][d], sc, 1);
+            const bf16x2 w2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j][d], sc, 2);
+            const bf16x2 w3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j][d], sc, 3);
+#pragma unroll
+            for (int tok = 0; tok < MT; ++tok) {
+                float a = acc[tok];
+                a = __builtin_amdgcn_fdot2_f32_bf16(w0, as_bf16x2(xr[tok].p[j][4 * d + 0]), a, false);
+                a = __builtin_amdgcn_fdot2_f32_bf16(w1, as_bf16x2(xr[tok].p[j][4 * d + 1]), a, false);
+                a = __builtin_amdgcn_fdot2_f32_bf16(w2, as_bf16x2(xr[tok].p[j][4 * d + 2]), a, false);
+                a = __builtin_amdgcn_fdot2_f32_bf16(w3, as_bf16x2(xr[tok].p[j][4 * d + 3]), a, false);
+                acc[tok] = a;
+            }
+        }
+    }
+}
+
+template <int WG, int BPL, int R, int MT>
+__global__ __launch_bounds__(512) void gemv_mt_kernel(const uint8_t* __restrict__ packed,
+                                                      const uint8_t* __restrict__ scales,
+                                                      const void* __restrict__ x, float* __restrict__ y, uint32_t m,
+                                                      uint32_t n, uint32_t rowsets) {
+    constexpr int RM = R * MT;
+    static_assert(RM == 2 || RM == 4 || RM == 8, "rows x tokens per team");
+    constexpr uint32_t T = 64 * WG;
+    constexpr uint32_t nblk = 64 * WG * BPL, k = 32 * nblk, row_bytes = k / 2, xbytes = MT * k * 2;
+    const uint32_t tpw = blockDim.x / T;
+    const uint32_t team = __builtin_amdgcn_readfirstlane(threadIdx.x / T);
+    const uint32_t t = threadIdx.x % T, lane = t % 64;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t / 64);
+    Segs sg;
+#pragma unroll
+    for (int q = 0; q < kMaxSegs; ++q) {
+        sg.packed[q] = packed;
+        sg.scales[q] = scales;
+        sg.y[q] = y;
+        sg.n[q] = n;
+        sg.first[q + 1] = rowsets;
+    }
+    sg.first[0] = 0;
+    sg.count = 1;
+    sg.rowsets = rowsets;
+    sg.am_partial = nullptr;
+
+    const uint32_t stride = gridDim.x * tpw;
+    const uint32_t first = blockIdx.x * tpw;  // the workgroup's first team visits the most row-sets
+    uint32_t rs = first + team;
+    RowSet<true, BPL, R> a, b;
+    load_rowset<true, WG, BPL, R>(sg, rs, rowsets, t, row_bytes, nblk, a);
+    // Dynamic LDS: the MT token rows of x when several teams share the
+    // workgroup (loaded once, then each lane copies its blocks to registers),
+    // then the cross-wave partial sums [tpw][2][WG][RM].
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    float(*red)[WG][RM] = reinterpret_cast<float(*)[WG][RM]>(smem + (tpw > 1 ? xbytes : 0)) + 2 * team;
+    LaneX<true, BPL> xr[MT];
+    const uint8_t* xb = static_cast<const uint8_t*>(x);
+    if (tpw > 1) {
+        const uint32_t live = (m < (uint32_t)MT ? m : (uint32_t)MT) * k * 2;
+        for (uint32_t c = threadIdx.x; c < xbytes / 16; c += blockDim.x)
+            *reinterpret_cast<u32x4*>(smem + 16 * c) = 16 * c < live ? load_u32x4(xb + 16 * c) : u32x4{0u, 0u, 0u, 0u};
+        __syncthreads();
+#pragma unroll
+        for (int tok = 0; tok < MT; ++tok) xr[tok].load_lds(smem + (size_t)tok * k * 2, t, T);
+    } else {
+#pragma unroll
+        for (int tok = 0; tok < MT; ++tok) {
+            if ((uint32_t)tok < m) {
+                xr[tok].load(xb + (size_t)tok * k * 2, t, T);
+            } else {
+#pragma unroll
+                for (int j = 0; j < BPL; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) xr[tok].p[j][e] = 0u;
+            }
+        }
+    }
+    uint32_t parity = 0;
+    auto finish = [&](uint32_t set, const RowSet<true, BPL, R>& cur) {
+        float acc[RM];
+#pragma unroll
+        for (int i = 0; i < R; ++i) rows_dot_mt<BPL, MT>(xr, cur.w[i], cur.s[i], acc + i * MT);
+        const uint32_t row0 = set * R;  // past n for a team beyond the last row-set: nothing is written
+        const float total = wave_reduce_rows<RM>(acc, lane);
+        const uint32_t idx = reduced_row_of_lane<RM>(lane);
+        if constexpr (WG == 1) {
+            const uint32_t row = row0 + idx / MT, tok = idx % MT;
+            if (row_writer<RM>(lane) && row < n && tok < m) y[(size_t)tok * n + row] = total;
+        } else {
+            if (row_writer<RM>(lane)) red[parity][wave][idx] = total;
+            __syncthreads();
+            if (t < (uint32_t)RM) {
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < WG; ++w) v += red[parity][w][t];
+                const uint32_t row = row0 + t / MT, tok = t % MT;
+                if (row < n && tok < m) y[(size_t)tok * n + row] = v;
+            }
+            parity ^= 1;
+        }
+    };
+    // Every team of the workgroup runs as many turns as the first one (the
+    // cross-wave reduction has a workgroup barrier); a team past the end loads
+    // zeros and writes nothing.
+    for (uint32_t rf = first;;) {
+        uint32_t nxt = rs + stride;
+        load_rowset<true, WG, BPL, R>(sg, nxt, rowsets, t, row_bytes, nblk, b);
+        finish(rs, a);
+        rf += stride;
+        if (rf >= rowsets) break;
+        rs = nxt;
+        nxt = rs + stride;
+        load_rowset<true, WG, BPL, R>(sg, nxt, rowsets, t, row_bytes, nblk, a);
+        finish(rs, b);
+        rf += stride;
+        if (rf >= rowsets) break;
+        rs = nxt;
+    }
+}
+
 // Generic exact kernel: any M (tokens processed MT at a time), any K % 32 == 0,
 // any scale byte. Every element is decoded exactly as engine/src/mxfp4.rs:27-33
 // does (level * 2^(s-127): subnormal for small bytes, inf for large levels at
@@ -708,6 +846,58 @@ hipError_t launch_gemv_m1(const GemvArgs& a, int cus) {
     g.x_bf16 = a.x_bf16;
     g.stream = a.stream;
     return launch_gemv_m1_group(g, cus, nullptr);
+}
+
+// Default shape of the few-token launch, from a sweep on MI355X (Qwen3
+// shapes, 2..4 tokens): wide weights (4096 row-sets or more) use one
+// workgroup per CU whose 8 / WG teams share one LDS copy of the token rows
+// (when it fits); narrower ones use independent teams, 1024 of one wave or 512
+// of several.
+static void mt_default(uint32_t rowsets, int wg, int cus, bool x_fits, uint32_t& teams, uint32_t& tpw) {
+    if (rowsets >= 4096 && x_fits) {
+        tpw = 8u / (uint32_t)wg;
+        teams = (uint32_t)cus * tpw;
+    } else {
+        tpw = 1;
+        teams = (uint32_t)cus * (wg == 1 ? 4u : 2u);
+    }
+    if (teams > rowsets) teams = rowsets;
+}
+
+// teams: row-set walkers (0: the default); tpw: teams per workgroup sharing one
+// LDS copy of the token rows (0: the default; more than one needs the copy and
+// the partial sums within 64 KiB).
+template <int WG, int BPL, int R, int MT>
+static hipError_t go_mt(const GemvArgs& a, int cus, uint32_t teams, uint32_t tpw) {
+    const uint32_t rowsets = (a.n + R - 1) / R;
+    constexpr uint32_t xbytes = MT * 2048u * WG * BPL * 2;
+    if (teams == 0 || tpw == 0)
+        mt_default(rowsets, WG, cus, xbytes + (8 / WG) * 2 * WG * R * MT * 4 <= 65536, teams, tpw);
+    if (tpw < 1 || 64 * WG * tpw > 512) return hipErrorNotSupported;
+    if (tpw > 1 && xbytes + tpw * 2 * WG * R * MT * 4 > 65536) return hipErrorNotSupported;
+    if (teams > rowsets) teams = rowsets;
+    const uint32_t grid = (teams + tpw - 1) / tpw;
+    const size_t lds = (tpw > 1 ? xbytes : 0) + (size_t)tpw * 2 * WG * R * MT * sizeof(float);
+    hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT>), dim3(grid), dim3(64 * WG * tpw), lds, a.stream, a.packed,
+                       a.scales, a.x, a.y, a.m, a.n, rowsets);
+    return hipGetLastError();
+}
+
+bool gemv_mt_supported(uint32_t m, uint32_t k, bool x_bf16) {
+    return x_bf16 && m >= 2 && m <= 4 && (k == 2048 || k == 4096 || k == 6144 || k == 8192 || k == 12288);
+}
+
+hipError_t launch_gemv_mt(const GemvArgs& a, int cus, uint32_t teams, uint32_t tpw) {
+    if (!gemv_mt_supported(a.m, a.k, a.x_bf16) || a.n == 0) return hipErrorNotSupported;
+#define MX4_MT(K, W, B)                                                                                  \
+    if (a.k == K) return a.m <= 2 ? go_mt<W, B, 2, 2>(a, cus, teams, tpw) : go_mt<W, B, 2, 4>(a, cus, teams, tpw);
+    MX4_MT(2048, 1, 1)
+    MX4_MT(4096, 1, 2)
+    MX4_MT(6144, 3, 1)
+    MX4_MT(8192, 2, 2)
+    MX4_MT(12288, 3, 2)
+#undef MX4_MT
+    return hipErrorNotSupported;
 }
 
 template <bool XBF16, int MT>

@@ -39,6 +39,11 @@ struct M1Config {
     uint32_t grid = 0;      // teams in the launch (0: one row-set each)
 };
 hipError_t launch_gemv_m1_group(const GemvGroup& g, int cus, const M1Config* forced);
+// 2 <= m <= 4 tokens with bf16 activations: the M == 1 weight stream with
+// every decoded weight multiplied into all token rows (exact, like skinny).
+bool gemv_mt_supported(uint32_t m, uint32_t k, bool x_bf16);
+// teams / tpw (teams per workgroup): 0 = the default launch shape.
+hipError_t launch_gemv_mt(const GemvArgs& a, int cus, uint32_t teams = 0, uint32_t tpw = 0);
 hipError_t launch_gemv_generic(const GemvArgs& a);
 // M = 1 projection + greedy argmax epilogue (a.y may be null); hipErrorNotSupported
 // for configurations without the epilogue instance. partial: max_partials keys.

@@ -227,7 +227,11 @@ mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
     }
     mx4::GemvArgs a{w->packed, w->scales, x, y, m, w->rows, w->cols, xt == MX4_BF16, ctx->stream};
     if (path == MX4_PATH_AUTO) {
-        if (m == 1 && mx4::gemv_m1_supported(w->cols) && scales_foldable(w))
+        // 2..4 bf16 token rows: the few-token GEMV, except where the skinny
+        // kernel measured faster (3-4 tokens on 4096-row weights, Qwen3-8B q/o/down)
+        const bool tokens = mx4::gemv_mt_supported(m, w->cols, xt == MX4_BF16) &&
+                            (m == 2 || w->rows <= 2048 || w->rows >= 8192);
+        if ((m == 1 && mx4::gemv_m1_supported(w->cols) || tokens) && scales_foldable(w))
             path = MX4_PATH_GEMV;
         else if (m >= 2 && mx4::skinny_supported(m, w->cols) && scales_foldable(w))
             path = MX4_PATH_SKINNY;
@@ -237,11 +241,13 @@ mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
     hipError_t e;
     switch (path) {
         case MX4_PATH_GEMV:
-            if (m != 1 || !mx4::gemv_m1_supported(w->cols))
-                return fail(MX4_ERR_UNSUPPORTED, "GEMV path needs m == 1 and K/32 in {64,128,192,256,384}");
+            if (!(m == 1 && mx4::gemv_m1_supported(w->cols)) && !mx4::gemv_mt_supported(m, w->cols, xt == MX4_BF16))
+                return fail(MX4_ERR_UNSUPPORTED,
+                            "GEMV path needs m == 1 and K/32 in {64,128,192,256,384}, or 2 <= m <= 4 with bf16 x "
+                            "and K in {2048, 4096, 6144, 8192, 12288}");
             if (!scales_foldable(w))
                 return fail(MX4_ERR_UNSUPPORTED, "GEMV path folds scales into the converter; scale bytes outside 2..252 need GENERIC");
-            e = mx4::launch_gemv_m1(a, ctx->cus);
+            e = m == 1 ? mx4::launch_gemv_m1(a, ctx->cus) : mx4::launch_gemv_mt(a, ctx->cus);
             break;
         case MX4_PATH_SKINNY:
             if (!mx4::skinny_supported(m, w->cols))
@@ -622,6 +628,22 @@ mx4_status mx4_gemv_config(mx4_context* ctx, const void* x, mx4_dtype xt, const 
     c.grid = teams;
     hipError_t e = mx4::launch_gemv_m1_group(gg, ctx->cus, &c);
     if (e == hipErrorNotSupported) return fail(MX4_ERR_UNSUPPORTED, "configuration not instantiated");
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status mx4_gemv_tokens_config(mx4_context* ctx, const void* x, uint32_t m, const mx4_weight* w, float* y,
+                                  uint32_t teams, uint32_t teams_per_workgroup) {
+    mx4_status st = check_matmul_args(ctx, x, MX4_BF16, m, w, y);
+    if (st != MX4_OK) return st;
+    if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the GEMV configurations are for MXFP4 weights");
+    if (!scales_foldable(w)) return fail(MX4_ERR_UNSUPPORTED, "scale bytes outside 2..252 need the generic kernel");
+    if (!mx4::gemv_mt_supported(m, w->cols, true))
+        return fail(MX4_ERR_UNSUPPORTED, "few-token GEMV needs 2 <= m <= 4 and K in {2048, 4096, 6144, 8192, 12288}");
+    DeviceGuard g(ctx->device);
+    mx4::GemvArgs a{w->packed, w->scales, x, y, m, w->rows, w->cols, true, ctx->stream};
+    hipError_t e = mx4::launch_gemv_mt(a, ctx->cus, teams, teams_per_workgroup);
+    if (e == hipErrorNotSupported) return fail(MX4_ERR_UNSUPPORTED, "configuration not possible");
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
     return MX4_OK;
 }

@@ -64,6 +64,7 @@ SIGNATURES = {
     "mx4_matmul_prefill": (_int, [_vp, _vp, _int, _u32, _vp, _int, _vp]),
     "mx4_matmul_group": (_int, [_vp, _vp, _int, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32]),
     "mx4_gemv_config": (_int, [_vp, _vp, _int, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32, _int, _int, _int, _u32]),
+    "mx4_gemv_tokens_config": (_int, [_vp, _vp, _u32, _vp, _vp, _u32, _u32]),
     "mx4_matmul_batch": (_int, [_vp, _vp, _u32]),
     "mx4_matmul_mx": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
     "mx4_reserve_prefill": (_int, [_vp, _u32, _u32]),
@@ -367,6 +368,10 @@ class Context:
     def prefill_matmul(self, codes: DeviceBuffer, scales: DeviceBuffer, act: int, m: int, w: Weight,
                        y: DeviceBuffer) -> None:
         check(lib().mx4_prefill_matmul(self.handle, codes.ptr, scales.ptr, act, m, w.handle, y.ptr))
+
+    def gemv_tokens_config(self, x: DeviceBuffer, m: int, w: Weight, y: DeviceBuffer, teams: int, tpw: int) -> int:
+        """Few-token GEMV (bf16 x) with an explicit launch shape; returns the status."""
+        return lib().mx4_gemv_tokens_config(self.handle, x.ptr, m, w.handle, y.ptr, teams, tpw)
 
     def prefill_config(self, codes: DeviceBuffer, scales: DeviceBuffer, act: int, m: int, w: Weight,
                        y: DeviceBuffer, tile_m: int, tile_n: int, split_k: int) -> int:

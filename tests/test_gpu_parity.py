@@ -616,6 +616,31 @@ def test_skinny_8b_shapes(mx4, ctx, oracle, name):
             assert_close(y[:, rows], refx, f"skinny {name} m={m} xtype={xtype}")
 
 
+@pytest.mark.parametrize("k", [2048, 4096, 6144, 8192, 12288])
+def test_gemv_few_tokens(mx4, ctx, oracle, k):
+    """2 <= M <= 4 bf16 token rows on the decode GEMV path (the weights read once
+    for all of them): ragged N against the oracle, and one-hot activations
+    return the decoded weights bit for bit."""
+    say(f"few-token GEMV k={k}")
+    rng = np.random.default_rng(k)
+    n = 333
+    w = ctx.synth_weight(700 + k // 1024, n, k, 0.02)
+    packed, scales = ctx.download_weight(w)
+    for m in (2, 3, 4):
+        x = oracle.bf16_to_f32(oracle.synth_bf16(800 + m, 1.0, m * k)).reshape(m, k)
+        ref = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
+        assert_close(run_matmul(mx4, ctx, x, w, mx4.PATH_GEMV, mx4.BF16), ref, f"few-token m={m} k={k}")
+    p2 = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    s2 = rng.integers(110, 140, (n, k // 32), dtype=np.uint8)
+    w2 = ctx.upload_weight(p2, s2, n, k)
+    for m in (2, 3, 4):
+        cols = rng.choice(k, m, replace=False)
+        x = np.zeros((m, k), np.float32)
+        x[np.arange(m), cols] = 1.0
+        y = run_matmul(mx4, ctx, x, w2, mx4.PATH_GEMV, mx4.BF16)
+        assert np.array_equal(y, oracle.dequantize(p2, s2)[:, cols].T), m
+
+
 def test_skinny_ragged_rows_and_identity(mx4, ctx, oracle):
     """Weight rows not a multiple of the 16-row tile, and an exact identity KAT:
     one-hot activations return the decoded weights bit for bit."""
