@@ -11,6 +11,29 @@ namespace mx4 {
 // python/quantize_mxfp4.py:18-39 for one 32-element block. The scale byte is
 // s = max(E - 2, 0) with E the biased exponent of amax (0 for zero or
 // subnormal amax): frexp(amax).exp - 3 = E - 129, clipped at -127.
+// Largest |v| of a block and whether every value is finite, as a tree over
+// the magnitude bits (for non-negative floats the bit patterns order like the
+// values, so the maximum is exact in any order; a tree keeps the dependency
+// chain at 5 steps instead of 32). `finite` is false for inf and NaN.
+__device__ __forceinline__ float block_amax(const float (&v)[32], bool& finite) {
+    uint32_t m[16], e[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t a = __float_as_uint(v[i]) & 0x7fffffffu, b = __float_as_uint(v[i + 16]) & 0x7fffffffu;
+        m[i] = a > b ? a : b;
+        e[i] = ((a & 0x7f800000u) == 0x7f800000u) | ((b & 0x7f800000u) == 0x7f800000u);
+    }
+#pragma unroll
+    for (int w = 8; w >= 1; w /= 2)
+#pragma unroll
+        for (int i = 0; i < w; ++i) {
+            m[i] = m[i] > m[i + w] ? m[i] : m[i + w];
+            e[i] |= e[i + w];
+        }
+    finite = e[0] == 0;
+    return __uint_as_float(m[0]);
+}
+
 __device__ __forceinline__ uint32_t mxfp4_scale_byte(float amax) {
     int e_biased = (int)((__float_as_uint(amax) >> 23) & 0xffu);
     int s = e_biased - 2;
@@ -67,14 +90,8 @@ __global__ __launch_bounds__(256) void quantize_mxfp4_kernel(const void* __restr
     if (b >= blocks) return;
     float v[32];
     load_block32<BF16>(in, b, v);
-    float amax = 0.0f;
-    bool finite = true;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        float a = __builtin_fabsf(v[i]);
-        finite &= a <= 3.40282347e38f;  // false for inf and NaN
-        amax = a > amax ? a : amax;
-    }
+    bool finite;
+    const float amax = block_amax(v, finite);
     if (!finite) atomicOr(bad, 1u);
     const uint32_t s = mxfp4_scale_byte(amax);
     u32x4 out;
@@ -137,14 +154,8 @@ __global__ __launch_bounds__(256) void quantize_fp8_kernel(const void* __restric
     if (b >= blocks) return;
     float v[32];
     load_block32<BF16>(in, b, v);
-    float amax = 0.0f;
-    bool finite = true;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        float a = __builtin_fabsf(v[i]);
-        finite &= a <= 3.40282347e38f;
-        amax = a > amax ? a : amax;
-    }
+    bool finite;
+    const float amax = block_amax(v, finite);
     if (!finite) atomicOr(bad, 1u);
     const uint32_t s = fp8_scale_byte(amax);
 #pragma unroll
@@ -201,14 +212,8 @@ __global__ __launch_bounds__(256) void quantize_fragments_kernel(const void* __r
 #pragma unroll
         for (int i = 0; i < 32; ++i) v[i] = 0.0f;
     }
-    float amax = 0.0f;
-    bool finite = true;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        float a = __builtin_fabsf(v[i]);
-        finite &= a <= 3.40282347e38f;
-        amax = a > amax ? a : amax;
-    }
+    bool finite;
+    const float amax = block_amax(v, finite);
     if (!finite) atomicOr(bad, 1u);
     uint32_t s;
     if constexpr (FP8) {
