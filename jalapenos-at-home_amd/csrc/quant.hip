@@ -1,6 +1,7 @@
 // quant.hip -- MXFP4 format kernels: quantize (the weight recipe and the
 // activation requantizer of the MFMA path), MX-FP8 requantize, dequantize,
 // first-max argmax, scale range scan and the synthetic-input generator.
+#include "mx_encode.h"
 #include "mx4_device.h"
 #include "mx4_kernels.h"
 
@@ -42,15 +43,7 @@ __device__ __forceinline__ uint32_t mxfp4_scale_byte(float amax) {
 
 __device__ __forceinline__ uint32_t mxfp4_code(float v, uint32_t s) {
     const float scaled = __builtin_amdgcn_ldexpf(__builtin_fabsf(v), 127 - (int)s);
-    // searchsorted(MIDPOINTS, scaled, side="left") = #midpoints < scaled
-    uint32_t code = (scaled > 0.25f) + (scaled > 0.75f) + (scaled > 1.25f) + (scaled > 1.75f) +
-                    (scaled > 2.5f) + (scaled > 3.5f) + (scaled > 5.0f);
-    // ties to even: scaled equal to the midpoint just above an odd code
-    const float mid_tab[7] = {0.25f, 0.75f, 1.25f, 1.75f, 2.5f, 3.5f, 5.0f};
-    float mid = mid_tab[code < 6 ? code : 6];
-    code += ((code & 1u) != 0u) & (scaled == mid);
-    code |= (__float_as_uint(v) >> 31) << 3;  // signbit, so -0.0 -> code 8
-    return code;
+    return e2m1_magnitude_code(scaled) | ((__float_as_uint(v) >> 31) << 3);  // signbit, so -0.0 -> code 8
 }
 
 template <bool BF16>
@@ -129,20 +122,7 @@ __device__ __forceinline__ uint32_t fp8_scale_byte(float amax) {
 
 __device__ __forceinline__ uint32_t e4m3_code(float v, uint32_t s) {
     const float scaled = __builtin_amdgcn_ldexpf(__builtin_fabsf(v), 127 - (int)s);
-    uint32_t code;
-    if (scaled < 0.015625f) {  // 2^-6: subnormal step 2^-9
-        code = (uint32_t)__builtin_rintf(scaled * 512.0f);
-    } else {
-        int E = (int)((__float_as_uint(scaled) >> 23) & 0xffu) - 127;
-        float q = __builtin_rintf(__builtin_amdgcn_ldexpf(scaled, 3 - E));
-        if (q >= 16.0f) {
-            q = 8.0f;
-            E += 1;
-        }
-        int c = ((E + 7) << 3) | ((int)q - 8);
-        code = (E > 8 || c > 0x7e) ? 0x7eu : (uint32_t)c;
-    }
-    return code | ((__float_as_uint(v) >> 31) << 7);
+    return e4m3_magnitude_code(scaled) | ((__float_as_uint(v) >> 31) << 7);
 }
 
 template <bool BF16>
