@@ -364,6 +364,40 @@ def test_lm_head_greedy_argmax_identical(mx4, ctx, oracle):
         assert np.array_equal(y2.download(np.float32).reshape(1, n), y)
 
 
+def test_recorded_decode_tail_replays(mx4, ctx, oracle):
+    """A recorded pass (HIP graph) holding the fused lm_head argmax, a separate
+    argmax over rows and a few-token GEMV: every replay, with new activations
+    uploaded between replays, equals the eager calls on the same inputs (the
+    kernels clear nothing with memsets; their key buffers are plain stores)."""
+    n, k = 5000, 2048
+    w = ctx.synth_weight(61, n, k, 0.02)
+    x = ctx.buffer(4 * k * 2)
+    y1, idx1, idx2 = ctx.buffer(n * 4), ctx.buffer(4), ctx.buffer(4)
+    y4 = ctx.buffer(3 * n * 4)
+
+    def enqueue():
+        ctx.matmul_argmax(x, mx4.BF16, w, y1, idx1)
+        ctx.argmax_rows(y1, 1, n, idx2)
+        ctx.matmul_ptr(x.ptr, mx4.BF16, 3, w, y4.ptr)
+
+    p = ctx.record(enqueue)
+    for rep in range(4):
+        bits = oracle.synth_bf16(900 + rep, 1.0, 3 * k)
+        x.upload(bits)
+        p.launch()
+        ctx.synchronize()
+        got = (y1.download(np.float32), idx1.download(np.uint32)[0], idx2.download(np.uint32)[0],
+               y4.download(np.float32))
+        enqueue()
+        ctx.synchronize()
+        want = (y1.download(np.float32), idx1.download(np.uint32)[0], idx2.download(np.uint32)[0],
+                y4.download(np.float32))
+        assert np.array_equal(got[0], want[0]) and got[1] == want[1] == got[2] == want[2], rep
+        assert np.array_equal(got[3], want[3]), rep
+        assert got[1] == oracle.argmax(want[0]), rep
+    p.release()
+
+
 @pytest.mark.parametrize("k", [2048, 4096])
 def test_matmul_argmax_first_max_rule(mx4, ctx, oracle, k):
     """The fused argmax keeps engine/src/model.rs:288-296 exactly: ties go to the
