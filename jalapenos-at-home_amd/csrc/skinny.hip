@@ -79,7 +79,7 @@ __device__ __forceinline__ void split3(const f32x4 a, const f32x4 b, bf16x8& hi,
 // lane group), scales and activation fragments are loaded one unit ahead of the
 // MFMAs. After a tile's last unit the TW partial 16x16 tiles are summed
 // through LDS (double-buffered: one barrier per tile).
-template <bool XBF16, int MT, int U, int NU, int TW>
+template <bool XBF16, int MT, int U, int NU, int TW, bool RESX>
 __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restrict__ packed,
                                                          const uint8_t* __restrict__ scales,
                                                          const void* __restrict__ x, float* __restrict__ y,
@@ -99,8 +99,26 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     struct Unit {
         u32x4 w[U];
         uint32_t s[U];
-        u32x4 xa[MT][U][XQ];
+        u32x4 xa[RESX ? 1 : MT][RESX ? 1 : U][RESX ? 1 : XQ];
     };
+    // RESX: a wave's K chunks are the same for every tile, so its activation
+    // fragments for all of them are loaded once, here, instead of with every
+    // tile's weights (for the lm_head that halves the bytes the kernel reads).
+    u32x4 xres[RESX ? NU : 1][RESX ? U : 1][RESX ? MT : 1][RESX ? XQ : 1];
+    if constexpr (RESX) {
+#pragma unroll
+        for (int p = 0; p < NU; ++p)
+#pragma unroll
+            for (int q = 0; q < U; ++q) {
+                const uint32_t blk = 4 * (wave + (p * U + q) * TW) + g;
+#pragma unroll
+                for (int j = 0; j < MT; ++j) {
+                    const uint32_t off = ((16 * j + col) * k + 32 * blk) * (XBF16 ? 2u : 4u);
+#pragma unroll
+                    for (int c = 0; c < XQ; ++c) xres[p][q][j][c] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16 * c, 0, 0);
+                }
+            }
+    }
     auto load = [&](uint32_t tile, uint32_t part, Unit& out) {
         const bool valid = tile < tiles;
         const uint32_t row0 = valid ? tile * 16 : 0;
@@ -113,6 +131,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
             const uint32_t blk = 4 * (wave + (part * U + q) * TW) + g;
             out.w[q] = __builtin_amdgcn_raw_buffer_load_b128(wr, col * row_bytes + 16 * blk, 0, kNT);
             out.s[q] = __builtin_amdgcn_raw_buffer_load_b8(sr, col * nblk + blk, 0, 0);
+            if constexpr (RESX) continue;
 #pragma unroll
             for (int j = 0; j < MT; ++j) {
                 const uint32_t off = ((16 * j + col) * k + 32 * blk) * (XBF16 ? 2u : 4u);
@@ -128,7 +147,12 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
 #pragma unroll
         for (int j = 0; j < MT; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     };
-    auto compute = [&](const Unit& cur) {
+    // unit `p` (compile-time) of the current tile
+    auto compute = [&](const Unit& cur, int p) {
+        auto xa = [&](int j, int q, int c) -> u32x4 {
+            if constexpr (RESX) return xres[p][q][j][c];
+            else return cur.xa[j][q][c];
+        };
 #pragma unroll
         for (int q = 0; q < U; ++q) {
             const float sc = __uint_as_float(cur.s[q] << 23);
@@ -138,11 +162,11 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
 #pragma unroll
                 for (int j = 0; j < MT; ++j) {
                     if constexpr (XBF16) {
-                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.xa[j][q][t]), b, acc[j], 0, 0, 0);
+                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa(j, q, t)), b, acc[j], 0, 0, 0);
                     } else {
                         bf16x8 hi, mid, lo;
-                        split3(__builtin_bit_cast(f32x4, cur.xa[j][q][2 * t]),
-                               __builtin_bit_cast(f32x4, cur.xa[j][q][2 * t + 1]), hi, mid, lo);
+                        split3(__builtin_bit_cast(f32x4, xa(j, q, 2 * t)), __builtin_bit_cast(f32x4, xa(j, q, 2 * t + 1)),
+                               hi, mid, lo);
                         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, acc[j], 0, 0, 0);
                         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b, acc[j], 0, 0, 0);
                         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, acc[j], 0, 0, 0);
@@ -177,40 +201,39 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
         zero();
     };
 
-    uint32_t tile = blockIdx.x, part = 0;
+    // The units of a tile are unrolled (their index, and so their activation
+    // fragments, known at compile time); each unit's weights are loaded while
+    // the previous one computes, the next tile's first unit during the last.
+    uint32_t tile = blockIdx.x;
     if (tile >= tiles) return;
     zero();
-    Unit ua, ub;
-    load(tile, part, ua);
+    Unit u[2];
+    load(tile, 0, u[0]);
     for (;;) {
-        uint32_t nt = tile, np = part + 1;
-        if (np == (uint32_t)NU) { np = 0; nt = tile + gridDim.x; }
-        load(nt, np, ub);
-        compute(ua);
-        if (part == (uint32_t)NU - 1) reduce_write(tile);
-        if (nt >= tiles) break;
-        tile = nt;
-        part = np;
-        nt = tile;
-        np = part + 1;
-        if (np == (uint32_t)NU) { np = 0; nt = tile + gridDim.x; }
-        load(nt, np, ua);
-        compute(ub);
-        if (part == (uint32_t)NU - 1) reduce_write(tile);
-        if (nt >= tiles) break;
-        tile = nt;
-        part = np;
+        const uint32_t next = tile + gridDim.x;  // past the end: loads read zeros, nothing is used
+#pragma unroll
+        for (int p = 0; p < NU; ++p) {
+            if (p + 1 < NU)
+                load(tile, (uint32_t)(p + 1), u[(p + 1) % 2]);
+            else
+                load(next, 0, u[(p + 1) % 2]);
+            compute(u[p % 2], p);
+        }
+        reduce_write(tile);
+        if (next >= tiles) break;
+        tile = next;
+        if constexpr (NU % 2 == 1) u[0] = u[1];
     }
 }
 
-template <bool XBF16, int MT, int U, int NU, int TW>
+template <bool XBF16, int MT, int U, int NU, int TW, bool RESX>
 hipError_t go(const GemvArgs& a, int cus) {
     const uint32_t tiles = (a.n + 15) / 16;
     uint32_t grid = (uint32_t)cus * 2u;  // two workgroups of TW waves per CU
     if (grid > tiles) grid = tiles;
     const uint32_t per = (tiles + grid - 1) / grid;
     grid = (tiles + per - 1) / per;
-    hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW>), dim3(grid), dim3(64 * TW), 0, a.stream, a.packed,
+    hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX>), dim3(grid), dim3(64 * TW), 0, a.stream, a.packed,
                        a.scales, a.x, a.y, a.m, a.n);
     return hipGetLastError();
 }
@@ -221,12 +244,17 @@ template <bool XBF16, int MT>
 hipError_t go_k(const GemvArgs& a, int cus) {
     constexpr int U = (XBF16 && MT == 1) ? 2 : 1;
     constexpr int TW = 8;
+    // bf16 activations of up to 16 tokens stay resident in registers for K up
+    // to 6144 (at most 6 chunks per wave: 96 VGPRs)
+    constexpr bool R = XBF16 && MT == 1;
     switch (a.k) {
-        case 2048: return go<XBF16, MT, U, 16 / (U * 4), 4>(a, cus);
-        case 4096: return go<XBF16, MT, U, 4 / U, TW>(a, cus);
-        case 6144: return go<XBF16, MT, U, 6 / U, TW>(a, cus);
-        case 8192: return go<XBF16, MT, U, 8 / U, TW>(a, cus);
-        case 12288: return go<XBF16, MT, U, 12 / U, TW>(a, cus);
+        case 2048: return go<XBF16, MT, U, 16 / (U * 4), 4, R>(a, cus);
+        case 4096: return go<XBF16, MT, U, 4 / U, TW, R>(a, cus);
+        case 6144: return go<XBF16, MT, U, 6 / U, TW, R>(a, cus);
+        // wider rows keep the per-tile activation loads: resident in registers
+        // they need 16 or 12 waves per workgroup and measured slower (down)
+        case 8192: return go<XBF16, MT, U, 8 / U, TW, false>(a, cus);
+        case 12288: return go<XBF16, MT, U, 12 / U, TW, false>(a, cus);
         default: return hipErrorNotSupported;
     }
 }

@@ -650,6 +650,26 @@ def test_skinny_8b_shapes(mx4, ctx, oracle, name):
             assert_close(y[:, rows], refx, f"skinny {name} m={m} xtype={xtype}")
 
 
+@pytest.mark.parametrize("n,k", [(2048, 2048), (2048, 6144), (1000, 6144), (333, 2048)])
+def test_skinny_resident_activations(mx4, ctx, oracle, n, k):
+    """The skinny kernel with bf16 activations held in registers for the whole
+    kernel (K up to 6144: the 1.7B q/o/gate/up and down widths; an odd number of
+    units per tile at 6144), including ragged N, against the oracle; f32
+    activations (the per-tile loading form) on the same weights."""
+    say(f"skinny resident x {k}->{n}")
+    rng = np.random.default_rng(n + k)
+    w = ctx.synth_weight(1100 + k // 1024, n, k, 0.02)
+    packed, scales = ctx.download_weight(w)
+    rows = _sample_rows(n, 96, rng) if n > 96 else np.arange(n)
+    for m in (5, 8, 16, 17):
+        x = oracle.bf16_to_f32(oracle.synth_bf16(1200 + m, 1.0, m * k)).reshape(m, k)
+        ref = np.concatenate([oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), int(r), int(r) + 1)
+                              for r in rows], axis=1)
+        for xtype in (mx4.BF16, mx4.F32):
+            y = run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, xtype)
+            assert_close(y[:, rows], ref, f"skinny {k}->{n} m={m} xtype={xtype}")
+
+
 @pytest.mark.parametrize("k", [2048, 4096, 6144, 8192, 12288])
 def test_gemv_few_tokens(mx4, ctx, oracle, k):
     """2 <= M <= 4 bf16 token rows on the decode GEMV path (the weights read once
