@@ -414,7 +414,7 @@ def main() -> int:
                    "bytes_per_step": step_bytes, "x_dtype": "bf16", "y_dtype": "f32",
                    "distinct_weights_bytes": sum(w.nbytes for (_, _, _, w) in weights),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "gemv_m1_kernel (all launches of the step)",
+        "roofline": {"bound": "hbm", "kernel": "M=1 GEMV (gemv_m1_head_kernel, gemv_m1_one_kernel: all launches of the step)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "basis": "algorithmic bytes of one decode step / GPU event time of one step"},

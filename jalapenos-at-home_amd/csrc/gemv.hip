@@ -243,10 +243,9 @@ __device__ __forceinline__ Seg pick_seg(const Segs& sg, uint32_t rs) {
 // makes the compiler's wait-count merge fall back to waiting for every load,
 // the prefetch included, which serialises streaming and compute.)
 template <bool XBF16, int WG, int BPL, int R>
-__device__ __forceinline__ void load_rowset(const Segs& sg, uint32_t rs, uint32_t rowsets, uint32_t t,
-                                            uint32_t row_bytes, uint32_t nblk, RowSet<XBF16, BPL, R>& out) {
+__device__ __forceinline__ void load_rowset_in(const Seg& sgm, uint32_t rs, uint32_t rowsets, uint32_t t,
+                                               uint32_t row_bytes, uint32_t nblk, RowSet<XBF16, BPL, R>& out) {
     const bool valid = rs < rowsets;
-    const Seg sgm = pick_seg(sg, rs);
     const uint32_t row0 = valid ? (rs - sgm.first) * R : 0;
     uint32_t rows = sgm.n - row0 < (uint32_t)R ? sgm.n - row0 : (uint32_t)R;
     rows = valid ? rows : 0;
@@ -263,6 +262,12 @@ __device__ __forceinline__ void load_rowset(const Segs& sg, uint32_t rs, uint32_
     }
     // keep the stream ahead of the arithmetic that follows
     __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool XBF16, int WG, int BPL, int R>
+__device__ __forceinline__ void load_rowset(const Segs& sg, uint32_t rs, uint32_t rowsets, uint32_t t,
+                                            uint32_t row_bytes, uint32_t nblk, RowSet<XBF16, BPL, R>& out) {
+    load_rowset_in<XBF16, WG, BPL, R>(pick_seg(sg, rs), rs, rowsets, t, row_bytes, nblk, out);
 }
 
 // Sum over one row's blocks owned by this lane. The E8M0 scale is folded into
@@ -349,22 +354,31 @@ __device__ __forceinline__ void finish_rowset(const Segs& sg, uint32_t rs, const
     }
 }
 
-// A workgroup holds `tpw` = blockDim.x / (64 WG) independent teams. With more
+// A workgroup holds `tpw` independent teams of 64 WG threads. With more
 // than one, x is staged once per workgroup in LDS and every team reads its
 // blocks from there: each workgroup loads the whole activation row, so fewer,
 // larger workgroups cut that L2 traffic (for o at K = 4096 it matched the
 // weight bytes with one team per workgroup). Dynamic LDS: x (k elements), then
 // the cross-wave partial sums [tpw][2][WG][R].
-template <bool XBF16, int WG, int BPL, int R, bool AM>
-__device__ __forceinline__ void gemv_m1_body(const Segs& sg, const void* __restrict__ x, uint32_t k) {
+//
+// HEAD0: the launcher guarantees every team's first row-set lies in segment 0
+// (grid * tpw <= first[1]), so the first load needs only segment 0's weight
+// and scale pointers and row count, taken from `early`; `late(early)` then
+// supplies the whole table, fetched while that load is in flight.
+struct AllEarly {
+    __device__ const Segs& operator()(const Segs& early) const { return early; }
+};
+
+template <bool XBF16, int WG, int BPL, int R, bool AM, bool HEAD0 = false, class Late = AllEarly>
+__device__ __forceinline__ void gemv_m1_body(const Segs& early, const void* __restrict__ x, uint32_t k, uint32_t tpw,
+                                             uint32_t grid, Late late = {}) {
     constexpr uint32_t T = 64 * WG;  // threads per team
-    const uint32_t tpw = blockDim.x / T;
     const uint32_t team = __builtin_amdgcn_readfirstlane(threadIdx.x / T);
     const uint32_t t = threadIdx.x % T;
     const uint32_t row_bytes = k / 2;
     const uint32_t nblk = k / 32;
-    const uint32_t rowsets = sg.rowsets;
-    const uint32_t stride = gridDim.x * tpw;
+    const uint32_t rowsets = early.rowsets;
+    const uint32_t stride = grid * tpw;
     const uint32_t first = blockIdx.x * tpw;  // the workgroup's first team visits the most row-sets
     uint32_t rs = first + team;               // the host launches at most `rowsets` teams per row-set turn
 
@@ -372,13 +386,23 @@ __device__ __forceinline__ void gemv_m1_body(const Segs& sg, const void* __restr
     // SGPRs here makes the compiler fetch them in one scalar round trip
     // (otherwise it splits the fetch and waits twice before the first weight
     // load); the weight stream is issued first, the activations right behind.
-#pragma unroll
-    for (int q = 0; q < kMaxSegs; ++q)
-        asm volatile("" ::"s"(sg.packed[q]), "s"(sg.scales[q]), "s"(sg.y[q]), "s"(sg.n[q]), "s"(sg.first[q]));
-    asm volatile("" ::"s"(x), "s"(sg.count), "s"(k));
-    __builtin_amdgcn_sched_barrier(0);
     RowSet<XBF16, BPL, R> a, b;
-    load_rowset<XBF16, WG, BPL, R>(sg, rs, rowsets, t, row_bytes, nblk, a);
+    if constexpr (HEAD0) {
+        asm volatile("" ::"s"(early.packed[0]), "s"(early.scales[0]), "s"(early.n[0]), "s"(x), "s"(k), "s"(rowsets),
+                     "s"(tpw));
+        __builtin_amdgcn_sched_barrier(0);
+        load_rowset_in<XBF16, WG, BPL, R>(Seg{early.packed[0], early.scales[0], nullptr, early.n[0], 0u}, rs, rowsets,
+                                          t, row_bytes, nblk, a);
+    } else {
+#pragma unroll
+        for (int q = 0; q < kMaxSegs; ++q)
+            asm volatile("" ::"s"(early.packed[q]), "s"(early.scales[q]), "s"(early.y[q]), "s"(early.n[q]),
+                         "s"(early.first[q]));
+        asm volatile("" ::"s"(x), "s"(early.count), "s"(k), "s"(tpw));
+        __builtin_amdgcn_sched_barrier(0);
+        load_rowset<XBF16, WG, BPL, R>(early, rs, rowsets, t, row_bytes, nblk, a);
+    }
+    const Segs sg = late(early);
     LaneX<XBF16, BPL> xr;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t xbytes = k * (XBF16 ? 2 : 4);
@@ -388,7 +412,7 @@ __device__ __forceinline__ void gemv_m1_body(const Segs& sg, const void* __restr
         xr.load(x, t, T);
     } else {
         const uint8_t* xg = static_cast<const uint8_t*>(x);
-        for (uint32_t c = threadIdx.x; c < xbytes / 16; c += blockDim.x)
+        for (uint32_t c = threadIdx.x; c < xbytes / 16; c += tpw * T)
             *reinterpret_cast<u32x4*>(smem + 16 * c) = load_u32x4(xg + 16 * c);
         __syncthreads();
         xr.load_lds(smem, t, T);
@@ -426,28 +450,97 @@ __device__ __forceinline__ void gemv_m1_body(const Segs& sg, const void* __restr
         __syncthreads();
         if (threadIdx.x == 0) {
             uint64_t m = 0;
-            for (uint32_t w = 0; w < blockDim.x / 64; ++w) m = max_u64(m, wbest[w]);
+            for (uint32_t w = 0; w < tpw * WG; ++w) m = max_u64(m, wbest[w]);
             sg.am_partial[blockIdx.x] = m;
         }
     }
 }
 
+// The launchers pass the teams per workgroup (`tpw`) and the grid size as
+// arguments: blockDim.x and gridDim.x are read from the dispatch's hidden
+// arguments, the workgroup size by a vector load whose address depends on a
+// scalar load, two memory round trips that would otherwise stand before the
+// first weight load.
+//
 // A group of up to four weights (their table passed by value).
 template <bool XBF16, int WG, int BPL, int R, bool AM>
-__global__ __launch_bounds__(512) void gemv_m1_kernel(Segs sg, const void* __restrict__ x, uint32_t k) {
-    gemv_m1_body<XBF16, WG, BPL, R, AM>(sg, x, k);
+__global__ __launch_bounds__(512) void gemv_m1_kernel(Segs sg, const void* __restrict__ x, uint32_t k, uint32_t tpw,
+                                                      uint32_t grid) {
+    gemv_m1_body<XBF16, WG, BPL, R, AM>(sg, x, k, tpw, grid);
+}
+
+// A group whose teams all start in segment 0: what the first load needs --
+// segment 0's weight and scale pointers and row count, x, k, the row-set
+// count and the launch shape -- comes first, as scalars that kernel argument
+// preloading places in SGPRs; the by-value table behind them is read from the
+// argument segment only for later row-sets and the stores.
+//
+// The table is read through the kernel argument segment pointer, laundered
+// after the first load is issued: a by-value argument's loads are placed at
+// kernel entry, where the compiler would wait for them (the register it
+// reuses from an 8-dword fetch) before the first weight load. Explicit
+// arguments are laid out in order at their natural alignment, as the members
+// of HeadArgs are.
+struct HeadArgs {
+    const uint8_t* packed0;
+    const uint8_t* scales0;
+    const void* x;
+    uint32_t n0, k, rowsets, tpw, grid;
+    Segs tail;
+};
+
+using KernargSegs = const __attribute__((address_space(4))) Segs;
+
+struct HeadTail {
+    __device__ Segs operator()(const Segs& early) const {
+        uint64_t kp = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
+        asm volatile("" : "+s"(kp));
+        KernargSegs* tail = reinterpret_cast<KernargSegs*>(kp + offsetof(HeadArgs, tail));
+        Segs sg;
+#pragma unroll
+        for (int q = 0; q < kMaxSegs; ++q) {
+            sg.packed[q] = tail->packed[q];
+            sg.scales[q] = tail->scales[q];
+            sg.y[q] = tail->y[q];
+            sg.n[q] = tail->n[q];
+            sg.first[q] = tail->first[q];
+        }
+        sg.first[kMaxSegs] = tail->first[kMaxSegs];
+        sg.count = tail->count;
+        sg.am_partial = nullptr;
+        sg.packed[0] = early.packed[0];
+        sg.scales[0] = early.scales[0];
+        sg.n[0] = early.n[0];
+        sg.rowsets = early.rowsets;
+        return sg;
+    }
+};
+
+template <bool XBF16, int WG, int BPL, int R>
+__global__ __launch_bounds__(512) void gemv_m1_head_kernel(const uint8_t* __restrict__ packed0,
+                                                           const uint8_t* __restrict__ scales0,
+                                                           const void* __restrict__ x, uint32_t n0, uint32_t k,
+                                                           uint32_t rowsets, uint32_t tpw, uint32_t grid, Segs tail) {
+    (void)tail;  // read through the argument segment by HeadTail
+    Segs early{};
+    early.packed[0] = packed0;
+    early.scales[0] = scales0;
+    early.n[0] = n0;
+    early.rowsets = rowsets;
+    gemv_m1_body<XBF16, WG, BPL, R, false, true>(early, x, k, tpw, grid, HeadTail{});
 }
 
 // One weight, every argument a plain scalar: this file is built with kernel
-// argument preloading, so on entry they already sit in SGPRs and the first
-// weight load issues without a scalar memory round trip (a by-value table
-// cannot be preloaded).
+// argument preloading, so on entry the ones the first loads need already sit
+// in SGPRs and the first weight load issues without a memory round trip (a
+// by-value table cannot be preloaded; y and am_partial, needed only at the
+// first store, come last and may be fetched).
 template <bool XBF16, int WG, int BPL, int R, bool AM>
 __global__ __launch_bounds__(512) void gemv_m1_one_kernel(const uint8_t* __restrict__ packed,
                                                           const uint8_t* __restrict__ scales,
-                                                          const void* __restrict__ x, float* __restrict__ y,
-                                                          uint32_t n, uint32_t k, uint32_t rowsets,
-                                                          uint64_t* __restrict__ am_partial) {
+                                                          const void* __restrict__ x, uint32_t n, uint32_t k,
+                                                          uint32_t rowsets, uint32_t tpw, uint32_t grid,
+                                                          float* __restrict__ y, uint64_t* __restrict__ am_partial) {
     Segs sg;
 #pragma unroll
     for (int q = 0; q < kMaxSegs; ++q) {
@@ -461,7 +554,7 @@ __global__ __launch_bounds__(512) void gemv_m1_one_kernel(const uint8_t* __restr
     sg.count = 1;
     sg.rowsets = rowsets;
     sg.am_partial = am_partial;
-    gemv_m1_body<XBF16, WG, BPL, R, AM>(sg, x, k);
+    gemv_m1_body<XBF16, WG, BPL, R, AM>(sg, x, k, tpw, grid);
 }
 
 // A few tokens (speculative verify, 2 <= m <= MT, bf16 activations): the
@@ -503,13 +596,13 @@ __device__ __forceinline__ void rows_dot_mt(const LaneX<true, BPL> (&xr)[MT], co
 template <int WG, int BPL, int R, int MT>
 __global__ __launch_bounds__(512) void gemv_mt_kernel(const uint8_t* __restrict__ packed,
                                                       const uint8_t* __restrict__ scales,
-                                                      const void* __restrict__ x, float* __restrict__ y, uint32_t m,
-                                                      uint32_t n, uint32_t rowsets) {
+                                                      const void* __restrict__ x, uint32_t m, uint32_t n,
+                                                      uint32_t rowsets, uint32_t tpw, uint32_t grid,
+                                                      float* __restrict__ y) {
     constexpr int RM = R * MT;
     static_assert(RM == 2 || RM == 4 || RM == 8, "rows x tokens per team");
     constexpr uint32_t T = 64 * WG;
     constexpr uint32_t nblk = 64 * WG * BPL, k = 32 * nblk, row_bytes = k / 2, xbytes = MT * k * 2;
-    const uint32_t tpw = blockDim.x / T;
     const uint32_t team = __builtin_amdgcn_readfirstlane(threadIdx.x / T);
     const uint32_t t = threadIdx.x % T, lane = t % 64;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t / 64);
@@ -527,7 +620,7 @@ __global__ __launch_bounds__(512) void gemv_mt_kernel(const uint8_t* __restrict_
     sg.rowsets = rowsets;
     sg.am_partial = nullptr;
 
-    const uint32_t stride = gridDim.x * tpw;
+    const uint32_t stride = grid * tpw;
     const uint32_t first = blockIdx.x * tpw;  // the workgroup's first team visits the most row-sets
     uint32_t rs = first + team;
     RowSet<true, BPL, R> a, b;
@@ -541,7 +634,7 @@ __global__ __launch_bounds__(512) void gemv_mt_kernel(const uint8_t* __restrict_
     const uint8_t* xb = static_cast<const uint8_t*>(x);
     if (tpw > 1) {
         const uint32_t live = (m < (uint32_t)MT ? m : (uint32_t)MT) * k * 2;
-        for (uint32_t c = threadIdx.x; c < xbytes / 16; c += blockDim.x)
+        for (uint32_t c = threadIdx.x; c < xbytes / 16; c += tpw * T)
             *reinterpret_cast<u32x4*>(smem + 16 * c) = 16 * c < live ? load_u32x4(xb + 16 * c) : u32x4{0u, 0u, 0u, 0u};
         __syncthreads();
 #pragma unroll
@@ -671,10 +764,14 @@ static hipError_t go_m1(const Segs& sg, const void* x, uint32_t k, uint32_t grid
     const size_t lds = (tpw > 1 ? (size_t)k * (XBF16 ? 2 : 4) : 0) + (size_t)tpw * 2 * WG * R * sizeof(float);
     if (sg.count == 1)
         hipLaunchKernelGGL((gemv_m1_one_kernel<XBF16, WG, BPL, R, false>), dim3(grid), dim3(64 * WG * tpw), lds, st,
-                           sg.packed[0], sg.scales[0], x, sg.y[0], sg.n[0], k, sg.rowsets, (uint64_t*)nullptr);
+                           sg.packed[0], sg.scales[0], x, sg.n[0], k, sg.rowsets, (uint32_t)tpw, grid, sg.y[0],
+                           (uint64_t*)nullptr);
+    else if ((uint64_t)grid * tpw <= sg.first[1])
+        hipLaunchKernelGGL((gemv_m1_head_kernel<XBF16, WG, BPL, R>), dim3(grid), dim3(64 * WG * tpw), lds, st,
+                           sg.packed[0], sg.scales[0], x, sg.n[0], k, sg.rowsets, (uint32_t)tpw, grid, sg);
     else
         hipLaunchKernelGGL((gemv_m1_kernel<XBF16, WG, BPL, R, false>), dim3(grid), dim3(64 * WG * tpw), lds, st, sg,
-                           x, k);
+                           x, k, (uint32_t)tpw, grid);
     return hipGetLastError();
 }
 
@@ -791,7 +888,7 @@ template <bool XBF16, int BPL, int R>
 static hipError_t go_am(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int tpw, uint32_t* idx, hipStream_t st) {
     const size_t lds = (tpw > 1 ? (size_t)k * (XBF16 ? 2 : 4) : 0) + (size_t)tpw * 2 * R * sizeof(float);
     hipLaunchKernelGGL((gemv_m1_one_kernel<XBF16, 1, BPL, R, true>), dim3(grid), dim3(64 * tpw), lds, st, sg.packed[0],
-                       sg.scales[0], x, sg.y[0], sg.n[0], k, sg.rowsets, sg.am_partial);
+                       sg.scales[0], x, sg.n[0], k, sg.rowsets, (uint32_t)tpw, grid, sg.y[0], sg.am_partial);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_argmax_reduce(sg.am_partial, 1, grid, idx, st);
@@ -879,7 +976,7 @@ static hipError_t go_mt(const GemvArgs& a, int cus, uint32_t teams, uint32_t tpw
     const uint32_t grid = (teams + tpw - 1) / tpw;
     const size_t lds = (tpw > 1 ? xbytes : 0) + (size_t)tpw * 2 * WG * R * MT * sizeof(float);
     hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT>), dim3(grid), dim3(64 * WG * tpw), lds, a.stream, a.packed,
-                       a.scales, a.x, a.y, a.m, a.n, rowsets);
+                       a.scales, a.x, a.m, a.n, rowsets, tpw, grid, a.y);
     return hipGetLastError();
 }
 

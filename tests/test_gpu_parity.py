@@ -589,6 +589,42 @@ def test_group_equals_individual(mx4, ctx, oracle):
         ctx.matmul_group(xb.ptr, mx4.BF16, 1, [ws[0], other], [ys[0].ptr, ys[1].ptr])
 
 
+@pytest.mark.parametrize("k,shapes", [
+    (4096, [4096, 1024, 1024]),    # 8B q|k|v: every team starts in q (preloaded head), later turns reach k and v
+    (4096, [12288, 12288]),        # 8B gate|up: preloaded head, 8 teams per workgroup
+    (4096, [3001, 999, 7]),        # preloaded head, ragged row-sets at every segment end
+    (2048, [2048, 1024, 1024]),    # 1.7B q|k|v: more teams than q's row-sets, the table kernel
+    (2048, [6144, 6144]),          # 1.7B gate|up: the table kernel
+    (4096, [40, 8, 24, 100]),      # four tiny segments: one row-set per team, the table kernel
+    (12288, [2050, 30]),           # wide K, 3-wave teams
+])
+def test_group_segments_against_oracle(mx4, ctx, oracle, k, shapes):
+    """A grouped launch equals the separate launches bit for bit and the oracle to
+    the float bar, for bf16 and f32 activations. The launcher passes segment 0's
+    fields as preloaded scalars when every team's first row-set lies in segment 0
+    (teams <= segment 0's row-sets) and the whole table otherwise; the cases above
+    take both kernels."""
+    say(f"grouped gemv k={k} shapes={shapes}")
+    ws = [ctx.synth_weight(300 + i, n, k, 0.02) for i, n in enumerate(shapes)]
+    xb16 = oracle.synth_bf16(11, 1.0, k)
+    x = oracle.bf16_to_f32(xb16).reshape(1, k)
+    xdev = {mx4.BF16: ctx.to_device(xb16), mx4.F32: ctx.to_device(x)}
+    refs = []
+    for w in ws:
+        packed, scales = ctx.download_weight(w)
+        refs.append(oracle.matmul(x, packed.reshape(-1), scales.reshape(-1)))
+    ys = [ctx.buffer(n * 4) for n in shapes]
+    for xt in (mx4.BF16, mx4.F32):
+        for y, n in zip(ys, shapes):
+            y.upload(np.full(n, np.nan, np.float32))
+        ctx.matmul_group(xdev[xt].ptr, xt, 1, ws, [y.ptr for y in ys])
+        grouped = [y.download(np.float32) for y in ys]
+        for i, (w, y, g, ref) in enumerate(zip(ws, ys, grouped, refs)):
+            assert_close(g.reshape(1, -1), ref, f"segment {i} xt={xt}")
+            ctx.matmul_ptr(xdev[xt].ptr, xt, 1, w, y.ptr)
+            assert np.array_equal(f32_bits(y.download(np.float32)), f32_bits(g)), f"segment {i} xt={xt}"
+
+
 def test_extreme_scales_take_the_exact_path(mx4, ctx, oracle):
     """Scale bytes 0, 1 (subnormal weights) and 253, 254 (inf weights) are outside
     the converter-folding range; AUTO routes them to the exact generic kernel."""
