@@ -15,12 +15,15 @@
 //    the contraction is over K, so any K order shared by A and B is exact;
 //  * bf16 activations are exact operands. f32 activations are split into
 //    three bf16 terms hi + mid + lo (24 significant bits), three MFMAs each;
-//  * a persistent workgroup of TW waves splits K (wave w takes chunks w,
-//    w + TW, ...; its activation fragments stay in registers for the whole
-//    kernel), walks 16-row weight tiles with the next tile prefetched, and
-//    reduces its TW partial tiles through LDS;
+//  * a persistent workgroup of TW waves splits K (unit p of wave w is the U
+//    adjacent chunks from (p TW + w) U on, so a wave reads whole 128-byte
+//    lines of each row; its activation fragments stay in registers for the
+//    whole kernel), walks 16-row weight tiles with the next ones prefetched,
+//    and reduces its TW partial tiles through LDS;
 //  * loads go through buffer resources: token rows >= M and weight rows >= N
 //    read as zeros without touching memory.
+#include <type_traits>
+
 #include "mx4_device.h"
 #include "mx4_kernels.h"
 
@@ -72,13 +75,14 @@ __device__ __forceinline__ void split3(const f32x4 a, const f32x4 b, bf16x8& hi,
     }
 }
 
-// Persistent kernel, K = 128 * U * NU * TW exactly. Wave w of a workgroup
-// owns the K chunks w, w + TW, w + 2 TW, ... of every weight row. The
-// workgroup walks 16-row weight tiles (tile, tile + grid, ...); each tile is
-// NU work units of U chunks per wave. A unit's weights (16 rows x U blocks per
-// lane group), scales and activation fragments are loaded one unit ahead of the
-// MFMAs. After a tile's last unit the TW partial 16x16 tiles are summed
-// through LDS (double-buffered: one barrier per tile).
+// Persistent kernel, K = 128 * U * NU * TW exactly. Unit p of wave w of a
+// workgroup is the U adjacent 128-element chunks from (p TW + w) U on, in
+// every weight row. The workgroup walks 16-row weight tiles (tile, tile +
+// grid, ...); each tile is NU units per wave. A unit's weights (16 rows x U
+// blocks per lane group), scales and activation fragments are loaded one unit
+// ahead of the MFMAs, or, with one unit per tile, two tiles ahead. After a
+// tile's last unit the TW partial 16x16 tiles are summed through LDS
+// (double-buffered: one barrier per tile).
 template <bool XBF16, int MT, int U, int NU, int TW, bool RESX>
 __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restrict__ packed,
                                                          const uint8_t* __restrict__ scales,
@@ -110,7 +114,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
         for (int p = 0; p < NU; ++p)
 #pragma unroll
             for (int q = 0; q < U; ++q) {
-                const uint32_t blk = 4 * (wave + (p * U + q) * TW) + g;
+                const uint32_t blk = 4 * ((p * TW + wave) * U + q) + g;
 #pragma unroll
                 for (int j = 0; j < MT; ++j) {
                     const uint32_t off = ((16 * j + col) * k + 32 * blk) * (XBF16 ? 2u : 4u);
@@ -128,7 +132,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
         const __amdgpu_buffer_rsrc_t xq = valid ? xr : empty;
 #pragma unroll
         for (int q = 0; q < U; ++q) {
-            const uint32_t blk = 4 * (wave + (part * U + q) * TW) + g;
+            const uint32_t blk = 4 * ((part * TW + wave) * U + q) + g;
             out.w[q] = __builtin_amdgcn_raw_buffer_load_b128(wr, col * row_bytes + 16 * blk, 0, kNT);
             out.s[q] = __builtin_amdgcn_raw_buffer_load_b8(sr, col * nblk + blk, 0, 0);
             if constexpr (RESX) continue;
@@ -207,29 +211,73 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     uint32_t tile = blockIdx.x;
     if (tile >= tiles) return;
     zero();
-    Unit u[2];
-    load(tile, 0, u[0]);
-    for (;;) {
-        const uint32_t next = tile + gridDim.x;  // past the end: loads read zeros, nothing is used
+    const uint32_t stride = gridDim.x;  // tiles past the end load zeros and use nothing
+    if constexpr (RESX && NU == 1) {
+        // A tile is one unit: the next D - 1 tiles' weights are in flight
+        // while one computes (D buffers, rotated by unrolling). The compiler's
+        // wait counts are exact inside the unrolled body but conservative at
+        // the loop head, where it waits for all but the newest tile; two
+        // rounds of D steps per loop turn make that one step in 2 D.
+        constexpr int D = 3;
+        Unit u[D];
 #pragma unroll
-        for (int p = 0; p < NU; ++p) {
-            if (p + 1 < NU)
-                load(tile, (uint32_t)(p + 1), u[(p + 1) % 2]);
-            else
-                load(next, 0, u[(p + 1) % 2]);
-            compute(u[p % 2], p);
+        for (int d = 0; d + 1 < D; ++d) load(tile + d * stride, 0, u[d]);
+        auto step = [&](uint32_t cur, auto slot) {
+            constexpr int S = decltype(slot)::value % D;
+            load(cur + (D - 1) * stride, 0, u[(S + D - 1) % D]);
+            compute(u[S], 0);
+            reduce_write(cur);
+        };
+        auto turn = [&](auto first) -> bool {
+            constexpr int F = decltype(first)::value;
+            step(tile, std::integral_constant<int, F + 0>{});
+            if ((tile += stride) >= tiles) return true;
+            step(tile, std::integral_constant<int, F + 1>{});
+            if ((tile += stride) >= tiles) return true;
+            if constexpr (D >= 3) {
+                step(tile, std::integral_constant<int, F + 2>{});
+                if ((tile += stride) >= tiles) return true;
+            }
+            if constexpr (D >= 4) {
+                step(tile, std::integral_constant<int, F + 3>{});
+                if ((tile += stride) >= tiles) return true;
+            }
+            return false;
+        };
+        for (;;) {
+            if (turn(std::integral_constant<int, 0>{})) break;
+            if (turn(std::integral_constant<int, D>{})) break;
         }
-        reduce_write(tile);
-        if (next >= tiles) break;
-        tile = next;
-        if constexpr (NU % 2 == 1) u[0] = u[1];
+    } else {
+        // Units ping-pong through two buffers, unit p of a tile in u[p % 2]
+        // (NU is even or 1 only with the ring above).
+        static_assert(NU % 2 == 0, "an odd unit count needs the copy-free rotation");
+        Unit u[2];
+        load(tile, 0, u[0]);
+        for (;;) {
+            const uint32_t next = tile + stride;
+#pragma unroll
+            for (int p = 0; p < NU; ++p) {
+                if (p + 1 < NU)
+                    load(tile, (uint32_t)(p + 1), u[(p + 1) % 2]);
+                else
+                    load(next, 0, u[(p + 1) % 2]);
+                compute(u[p % 2], p);
+            }
+            reduce_write(tile);
+            if (next >= tiles) break;
+            tile = next;
+        }
     }
 }
 
 template <bool XBF16, int MT, int U, int NU, int TW, bool RESX>
 hipError_t go(const GemvArgs& a, int cus) {
     const uint32_t tiles = (a.n + 15) / 16;
-    uint32_t grid = (uint32_t)cus * 2u;  // two workgroups of TW waves per CU
+    // two workgroups of TW waves per CU; with one unit per tile, eight waves
+    // per CU (two per SIMD: the three buffers need more than the 128 VGPRs of
+    // four waves per SIMD)
+    uint32_t grid = (uint32_t)cus * ((RESX && NU == 1) ? 8u / TW : 2u);
     if (grid > tiles) grid = tiles;
     const uint32_t per = (tiles + grid - 1) / grid;
     grid = (tiles + per - 1) / per;
@@ -240,6 +288,11 @@ hipError_t go(const GemvArgs& a, int cus) {
 
 // Chunks per unit: two for bf16 activations and one token tile, one otherwise,
 // so that two units (the one computed and the one in flight) fit the registers.
+// With resident activations and at least two tiles per workgroup of the ring
+// launch (8 waves per CU), a tile is one unit and three tiles stream through
+// the ring: gate/up at 8 tokens 14.3 -> 10.4 us, lm_head 91 -> 86 us. Weights
+// with fewer tiles (each workgroup one tile or two) keep two units per tile,
+// which measured 0.3-0.8 us faster there.
 template <bool XBF16, int MT>
 hipError_t go_k(const GemvArgs& a, int cus) {
     constexpr int U = (XBF16 && MT == 1) ? 2 : 1;
@@ -247,10 +300,18 @@ hipError_t go_k(const GemvArgs& a, int cus) {
     // bf16 activations of up to 16 tokens stay resident in registers for K up
     // to 6144 (at most 6 chunks per wave: 96 VGPRs)
     constexpr bool R = XBF16 && MT == 1;
+    const uint32_t tiles = (a.n + 15) / 16;
+    const uint32_t ring_grid = (uint32_t)(cus > 0 ? cus : 256) * 8u;  // waves per CU
+    const bool ring = R && tiles >= 2 * ring_grid / TW;
     switch (a.k) {
-        case 2048: return go<XBF16, MT, U, 16 / (U * 4), 4, R>(a, cus);
-        case 4096: return go<XBF16, MT, U, 4 / U, TW, R>(a, cus);
-        case 6144: return go<XBF16, MT, U, 6 / U, TW, R>(a, cus);
+        case 2048:
+            if constexpr (R) if (ring) return go<XBF16, MT, 4, 1, 4, R>(a, cus);
+            return go<XBF16, MT, U, 16 / (U * 4), 4, R>(a, cus);
+        case 4096:
+            if constexpr (R) if (ring) return go<XBF16, MT, 4, 1, TW, R>(a, cus);
+            return go<XBF16, MT, U, 4 / U, TW, R>(a, cus);
+        case 6144:  // (a one-unit tile of 6 chunks would spill)
+            return go<XBF16, MT, R ? 3 : U, R ? 2 : 6 / U, TW, R>(a, cus);
         // wider rows keep the per-tile activation loads: resident in registers
         // they need 16 or 12 waves per workgroup and measured slower (down)
         case 8192: return go<XBF16, MT, U, 8 / U, TW, false>(a, cus);
