@@ -49,6 +49,26 @@ __device__ __forceinline__ bf16x8 weights8(uint32_t word, float sc) {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// The 4U scale bytes of a unit's U adjacent chunks in one row, one load per
+// lane (the four lanes of a row read the same bytes): byte 4q + g of the run
+// is lane group g's block of chunk q.
+template <int U>
+__device__ __forceinline__ void load_scale_run(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t (&out)[U]) {
+    if constexpr (U == 4) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
+    } else if constexpr (U == 3) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, off, 0, 0);
+        out[0] = v[0]; out[1] = v[1]; out[2] = v[2];
+    } else if constexpr (U == 2) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+        out[0] = v[0]; out[1] = v[1];
+    } else {
+        static_assert(U == 1, "1 to 4 chunks per unit");
+        out[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    }
+}
+
 // Wait states after an MFMA chain whose accumulators are read next. The
 // compiler can place a v_accvgpr_read of an XDL result right after a branch
 // without the wait states the result needs (seen with ROCm 7.2 on gfx950: the
@@ -102,7 +122,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
 
     struct Unit {
         u32x4 w[U];
-        uint32_t s[U];
+        uint32_t s[U];  // scale-byte runs: chunk q's byte for lane group g is byte g of s[q]
         u32x4 xa[RESX ? 1 : MT][RESX ? 1 : U][RESX ? 1 : XQ];
     };
     // RESX: a wave's K chunks are the same for every tile, so its activation
@@ -130,11 +150,11 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
         const __amdgpu_buffer_rsrc_t wr = valid ? rsrc(packed + (size_t)row0 * row_bytes, rows * row_bytes) : empty;
         const __amdgpu_buffer_rsrc_t sr = valid ? rsrc(scales + (size_t)row0 * nblk, rows * nblk) : empty;
         const __amdgpu_buffer_rsrc_t xq = valid ? xr : empty;
+        load_scale_run<U>(sr, col * nblk + 4 * (part * TW + wave) * U, out.s);
 #pragma unroll
         for (int q = 0; q < U; ++q) {
             const uint32_t blk = 4 * ((part * TW + wave) * U + q) + g;
             out.w[q] = __builtin_amdgcn_raw_buffer_load_b128(wr, col * row_bytes + 16 * blk, 0, kNT);
-            out.s[q] = __builtin_amdgcn_raw_buffer_load_b8(sr, col * nblk + blk, 0, 0);
             if constexpr (RESX) continue;
 #pragma unroll
             for (int j = 0; j < MT; ++j) {
@@ -159,7 +179,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
         };
 #pragma unroll
         for (int q = 0; q < U; ++q) {
-            const float sc = __uint_as_float(cur.s[q] << 23);
+            const float sc = __uint_as_float(((cur.s[q] >> (8 * g)) & 0xffu) << 23);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const bf16x8 b = weights8(cur.w[q][t], sc);
