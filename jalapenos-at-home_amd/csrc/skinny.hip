@@ -143,6 +143,22 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
                 }
             }
     }
+    // TRANS (two or four chunks per unit): a unit's 16 rows x 64U bytes are
+    // loaded as 16/U rows per instruction, 64U contiguous bytes each (whole
+    // cache lines instead of one half line per row: half the memory requests),
+    // then passed through the wave's own LDS stage into the MFMA layout. Load i
+    // holds rows (16/U) i + j, block b of the unit at lane (4U) j + b. Its stage
+    // slot is swizzled so that the writes and the reads of any 8 consecutive
+    // lanes fall in 8 different 16-byte bank groups:
+    //   U = 4: 64 i + 16 j + (b + 2 j + (i & 1)) % 16
+    //   U = 2: 64 i + 8 j + (b + (j & ~1)) % 8
+    constexpr bool TRANS = U == 2 || U == 4;
+    constexpr uint32_t RPL = 16 / U, BPR = 4 * U;  // rows per load, blocks per row of a unit
+    __shared__ u32x4 stage[TRANS ? TW : 1][TRANS ? 64 * U : 1];
+    auto swz = [](uint32_t i, uint32_t j, uint32_t b) -> uint32_t {
+        if constexpr (U == 4) return 64 * i + 16 * j + ((b + 2 * j + (i & 1)) & 15);
+        else return 64 * i + 8 * j + ((b + (j & ~1u)) & 7);
+    };
     auto load = [&](uint32_t tile, uint32_t part, Unit& out) {
         const bool valid = tile < tiles;
         const uint32_t row0 = valid ? tile * 16 : 0;
@@ -151,10 +167,15 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
         const __amdgpu_buffer_rsrc_t sr = valid ? rsrc(scales + (size_t)row0 * nblk, rows * nblk) : empty;
         const __amdgpu_buffer_rsrc_t xq = valid ? xr : empty;
         load_scale_run<U>(sr, col * nblk + 4 * (part * TW + wave) * U, out.s);
+        const uint32_t span = 64 * (part * TW + wave) * U;  // the unit's first byte in a row
 #pragma unroll
         for (int q = 0; q < U; ++q) {
             const uint32_t blk = 4 * ((part * TW + wave) * U + q) + g;
-            out.w[q] = __builtin_amdgcn_raw_buffer_load_b128(wr, col * row_bytes + 16 * blk, 0, kNT);
+            if constexpr (TRANS)
+                out.w[q] = __builtin_amdgcn_raw_buffer_load_b128(wr, (RPL * q + lane / BPR) * row_bytes + span + 16 * (lane % BPR),
+                                                                 0, kNT);
+            else
+                out.w[q] = __builtin_amdgcn_raw_buffer_load_b128(wr, col * row_bytes + 16 * blk, 0, kNT);
             if constexpr (RESX) continue;
 #pragma unroll
             for (int j = 0; j < MT; ++j) {
@@ -177,12 +198,22 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
             if constexpr (RESX) return xres[p][q][j][c];
             else return cur.xa[j][q][c];
         };
+        u32x4 wq[U];
+        if constexpr (TRANS) {
+#pragma unroll
+            for (int i = 0; i < U; ++i) stage[wave][swz(i, lane / BPR, lane % BPR)] = cur.w[i];
+#pragma unroll
+            for (int q = 0; q < U; ++q) wq[q] = stage[wave][swz(col / RPL, col % RPL, 4 * q + g)];
+        } else {
+#pragma unroll
+            for (int q = 0; q < U; ++q) wq[q] = cur.w[q];
+        }
 #pragma unroll
         for (int q = 0; q < U; ++q) {
             const float sc = __uint_as_float(((cur.s[q] >> (8 * g)) & 0xffu) << 23);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const bf16x8 b = weights8(cur.w[q][t], sc);
+                const bf16x8 b = weights8(wq[q][t], sc);
 #pragma unroll
                 for (int j = 0; j < MT; ++j) {
                     if constexpr (XBF16) {
@@ -306,6 +337,15 @@ hipError_t go(const GemvArgs& a, int cus) {
     return hipGetLastError();
 }
 
+// The three-tile ring (bf16 activations, K 2048 or 4096) pays from two tiles
+// per workgroup at eight waves per CU (K = 2048 runs 4-wave workgroups).
+bool tile_ring(const GemvArgs& a, int cus) {
+    const uint32_t tiles = (a.n + 15) / 16;
+    const uint32_t waves = (uint32_t)(cus > 0 ? cus : 256) * 8u;
+    const uint32_t tw = a.k == 2048 ? 4u : 8u;
+    return a.x_bf16 && (a.k == 2048 || a.k == 4096) && tiles >= 2 * waves / tw;
+}
+
 // Chunks per unit: two for bf16 activations and one token tile, one otherwise,
 // so that two units (the one computed and the one in flight) fit the registers.
 // With resident activations and at least two tiles per workgroup of the ring
@@ -320,9 +360,7 @@ hipError_t go_k(const GemvArgs& a, int cus) {
     // bf16 activations of up to 16 tokens stay resident in registers for K up
     // to 6144 (at most 6 chunks per wave: 96 VGPRs)
     constexpr bool R = XBF16 && MT == 1;
-    const uint32_t tiles = (a.n + 15) / 16;
-    const uint32_t ring_grid = (uint32_t)(cus > 0 ? cus : 256) * 8u;  // waves per CU
-    const bool ring = R && tiles >= 2 * ring_grid / TW;
+    const bool ring = R && tile_ring(a, cus);
     switch (a.k) {
         case 2048:
             if constexpr (R) if (ring) return go<XBF16, MT, 4, 1, 4, R>(a, cus);
@@ -348,10 +386,24 @@ bool skinny_supported(uint32_t m, uint32_t k) {
     return m >= 1 && m <= 32 && kk;
 }
 
+// More than 16 tokens on weights long enough for the tile ring run as two
+// launches of 16 and m - 16 token rows: the one-token-tile kernel keeps its
+// activations resident and streams through the ring, which two token tiles
+// per launch cannot afford in registers (lm_head at 17-32 tokens: 256-357 us
+// in one launch, 115-125 in two; gate 29-40 -> 18-20 us). Shorter weights
+// measured faster in one launch with two token tiles.
 hipError_t launch_skinny(const GemvArgs& a, int cus) {
     if (!skinny_supported(a.m, a.k)) return hipErrorNotSupported;
-    if (a.m <= 16) return a.x_bf16 ? go_k<true, 1>(a, cus) : go_k<false, 1>(a, cus);
-    return a.x_bf16 ? go_k<true, 2>(a, cus) : go_k<false, 2>(a, cus);
+    auto one = [&](const GemvArgs& b) { return b.x_bf16 ? go_k<true, 1>(b, cus) : go_k<false, 1>(b, cus); };
+    if (a.m <= 16) return one(a);
+    if (!tile_ring(a, cus)) return a.x_bf16 ? go_k<true, 2>(a, cus) : go_k<false, 2>(a, cus);
+    GemvArgs lo = a, hi = a;
+    lo.m = 16;
+    hi.m = a.m - 16;
+    hi.x = static_cast<const uint8_t*>(a.x) + (size_t)16 * a.k * (a.x_bf16 ? 2 : 4);
+    hi.y = a.y + (size_t)16 * a.n;
+    const hipError_t e = one(lo);
+    return e != hipSuccess ? e : one(hi);
 }
 
 }  // namespace mx4

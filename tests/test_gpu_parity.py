@@ -731,6 +731,34 @@ def test_gemv_few_tokens(mx4, ctx, oracle, k):
         assert np.array_equal(y, oracle.dequantize(p2, s2)[:, cols].T), m
 
 
+@pytest.mark.parametrize("n,k", [(8192 + 5, 4096), (16384 + 37, 2048)])
+def test_skinny_tile_ring(mx4, ctx, oracle, n, k):
+    """Weights long enough for the skinny kernel's three-tile ring (at least two
+    16-row tiles per workgroup at eight waves per CU), ragged N, up to 16 tokens
+    in one launch and more as two: one-hot bf16 activations return the decoded
+    weights bit for bit in every row, and random activations match the oracle on
+    sampled rows."""
+    say(f"skinny tile ring {k}->{n}")
+    rng = np.random.default_rng(n)
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(112, 136, (n, k // 32), dtype=np.uint8)
+    w = ctx.upload_weight(packed, scales, n, k)
+    dec = oracle.dequantize(packed, scales)
+    for m in (5, 16, 17, 32):
+        cols = rng.choice(k, m, replace=False)
+        x = np.zeros((m, k), np.float32)
+        x[np.arange(m), cols] = 1.0
+        y = run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.BF16)
+        assert np.array_equal(y, dec[:, cols].T), f"identity m={m}"
+    rows = _sample_rows(n, 128, rng)
+    for m in (8, 13, 29):
+        x = oracle.bf16_to_f32(oracle.synth_bf16(1500 + m, 1.0, m * k)).reshape(m, k)
+        ref = np.concatenate([oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), int(r), int(r) + 1)
+                              for r in rows], axis=1)
+        y = run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.BF16)
+        assert_close(y[:, rows], ref, f"ring {k}->{n} m={m}")
+
+
 def test_skinny_ragged_rows_and_identity(mx4, ctx, oracle):
     """Weight rows not a multiple of the 16-row tile, and an exact identity KAT:
     one-hot activations return the decoded weights bit for bit."""
