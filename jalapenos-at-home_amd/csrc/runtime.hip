@@ -227,11 +227,13 @@ mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
     }
     mx4::GemvArgs a{w->packed, w->scales, x, y, m, w->rows, w->cols, xt == MX4_BF16, ctx->stream};
     if (path == MX4_PATH_AUTO) {
-        // 2..4 bf16 token rows: the few-token GEMV, except where the skinny
-        // kernel measured faster (3-4 tokens on 4096-row weights, Qwen3-8B q/o/down)
+        // 2..4 bf16 token rows: the few-token GEMV where it measured faster
+        // than the skinny kernel on the Qwen3 1.7B/8B shapes: 2 tokens below
+        // vocabulary-sized weights, and 3-4 tokens on 1024-row weights at
+        // K >= 4096 (8B k/v)
         const bool tokens = mx4::gemv_mt_supported(m, w->cols, xt == MX4_BF16) &&
-                            (m == 2 || w->rows <= 2048 || w->rows >= 8192);
-        if ((m == 1 && mx4::gemv_m1_supported(w->cols) || tokens) && scales_foldable(w))
+                            ((m == 2 && w->rows < 65536) || (w->rows <= 1024 && w->cols >= 4096));
+        if (((m == 1 && mx4::gemv_m1_supported(w->cols)) || tokens) && scales_foldable(w))
             path = MX4_PATH_GEMV;
         else if (m >= 2 && mx4::skinny_supported(m, w->cols) && scales_foldable(w))
             path = MX4_PATH_SKINNY;
