@@ -809,9 +809,11 @@ bool gemv_m1_supported(uint32_t k) {
 // Default configuration, from sweeps on MI355X over the launches of the Qwen3
 // 1.7B and 8B decode steps (q|k|v and gate|up grouped, cold weights, recorded
 // passes). One wave per team for K <= 4096 (1-2 blocks per lane), several
-// teams per workgroup for the wide matrices; for long K a 3-wave team and few
-// workgroups, because every workgroup loads the whole activation row (24 KiB
-// at K = 12288). Grids are in teams per CU.
+// teams per workgroup for the wide matrices (two-wave teams for the
+// vocabulary-sized lm_head); for long K multi-wave teams and few workgroups,
+// because every workgroup loads the whole activation row (24 KiB at K =
+// 12288): at 12288 four 2-wave teams share one LDS copy of it. Grids are in
+// teams per CU.
 static void default_m1_config(uint32_t k, uint32_t rows, int cus, M1Config& c) {
     const uint32_t nblk = k / 32;
     const uint32_t scale = (uint32_t)(cus > 0 ? cus : 256);  // the table is for 256 CUs
@@ -822,8 +824,9 @@ static void default_m1_config(uint32_t k, uint32_t rows, int cus, M1Config& c) {
             if (rows > 8192) { c.r = 2; c.tpw = rows > 65536 ? 8 : 4; c.grid = 16 * scale; }
             break;
         case 128:  // K = 4096
-            c.wg = 1; c.r = rows > 65536 ? 4 : 2; c.grid = (rows > 65536 || rows <= 8192 ? 4 : 16) * scale;
-            if (rows > 8192) c.tpw = rows > 65536 ? 4 : 8;
+            c.wg = 1; c.r = 2; c.grid = (rows <= 8192 ? 4 : 16) * scale;
+            if (rows > 8192) c.tpw = 8;
+            if (rows > 65536) { c.wg = 2; c.grid = 8 * scale; c.tpw = 4; }  // vocabulary-sized
             break;
         case 192:  // K = 6144
             c.wg = 3; c.r = 2; c.grid = 2 * scale;
@@ -832,7 +835,7 @@ static void default_m1_config(uint32_t k, uint32_t rows, int cus, M1Config& c) {
             c.wg = 2; c.r = 4; c.grid = 8 * scale;
             break;
         default:  // K = 12288
-            c.wg = 3; c.r = 2; c.grid = 2 * scale;
+            c.wg = 2; c.r = 1; c.grid = 4 * scale; c.tpw = 4;
             break;
     }
 }
@@ -899,6 +902,11 @@ hipError_t launch_gemv_m1_argmax(const GemvArgs& a, uint64_t* partial, uint32_t 
     if (!gemv_m1_supported(a.k) || a.n == 0) return hipErrorNotSupported;
     M1Config c;
     default_m1_config(a.k, a.n, cus, c);
+    if (c.wg != 1) {
+        // the argmax instances are one-wave teams: the vocabulary-sized
+        // one-wave configuration (4 rows, 4 teams per CU, 4 per workgroup)
+        c.wg = 1; c.r = 4; c.grid = 4 * (uint32_t)(cus > 0 ? cus : 256); c.tpw = 4;
+    }
     const uint32_t nblk = a.k / 32;
     const int bpl = (int)(nblk / 64);
     if ((bpl != 1 && bpl != 2) || (c.r != 2 && c.r != 4)) return hipErrorNotSupported;
