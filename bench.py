@@ -110,7 +110,7 @@ def time_shapes(ctx, weights, xs, ys, reps: int = 3):
     return table
 
 
-def time_skinny(ctx, weights, ms=(1, 2, 4, 8, 16), reps: int = 3):
+def time_skinny(ctx, weights, ms=(1, 2, 4, 8, 16, 32), reps: int = 3):
     """Speculative-verify shapes: each 8B projection at M token rows (exact path:
     GEMV for M = 1, skinny bf16-MFMA kernel above), 36 cold copies in a recorded
     pass, per-call latency and effective GB/s (bytes with M*K*2 + M*N*4)."""
