@@ -247,9 +247,10 @@ mx4_status mx4_prefill_matmul(mx4_context *ctx, const uint8_t *codes_dev, const 
 /* Tuning hook for the prefill GEMM (arguments as mx4_prefill_matmul): the
  * workgroup tile (tile_m rows x tile_n columns) and the number of K parts
  * inside the workgroup (split_k, summed through LDS) of one compiled
- * instance: 128 x 192 x 1 (K % 512 == 0), 128 x 128 x 1, 64 x 128 x 2
- * (K % 512 == 0); MX4_ERR_UNSUPPORTED when none matches. tile_m == 0 keeps the
- * default choice. */
+ * instance: 128 x 192 x 1 (K % 512 == 0), 128 x 128 x 1, 64 x 128 x 2 and
+ * 128 x 192 x 2 (K % 512 == 0), 128 x 64 x 4, 64 x 128 x 4, 128 x 96 x 4 and
+ * 128 x 128 x 4 (K % 1024 == 0); MX4_ERR_UNSUPPORTED when none matches.
+ * tile_m == 0 keeps the default choice. */
 mx4_status mx4_prefill_config(mx4_context *ctx, const uint8_t *codes_dev, const uint8_t *scales_dev,
                               mx4_act_format act, uint32_t m, const mx4_weight *w, float *y_dev,
                               uint32_t tile_m, uint32_t tile_n, uint32_t split_k);

@@ -36,9 +36,10 @@
 //
 // Kernel: a wave owns a (32 TM) x (32 TN) output tile over its K range and
 // keeps a ring of Q slots of U k-steps of fragments in flight (the register
-// file is the prefetch buffer). Four waves per workgroup: 2 x 2 tiles, or (for
-// KSPLIT = 2) two tiles x two K halves whose partial tiles meet in LDS at the
-// end. Each fragment row-group gets its own buffer resource bounded to the
+// file is the prefetch buffer). Four waves per workgroup: 2 x 2 tiles, two
+// tiles x two K halves (KSPLIT = 2) or one tile x four K quarters (KSPLIT =
+// 4); partial tiles of one output tile meet in LDS at the end and are summed
+// in K order. Each fragment row-group gets its own buffer resource bounded to the
 // wave's K range, so the prefetch beyond it reads zeros without touching memory.
 #include "mx4_device.h"
 #include "mx4_kernels.h"
@@ -93,22 +94,32 @@ __device__ __forceinline__ uint32_t clamp_bytes(uint64_t want, uint64_t base, ui
     return (uint32_t)(base >= total ? 0 : (total - base < want ? total - base : want));
 }
 
+// Wave grid of a workgroup for a K split: 2 x 2 tiles (1), 1 x 2 tiles x two
+// K halves (2), one tile x four K quarters (4).
+constexpr int wave_rows(int ksplit) { return ksplit == 1 ? 2 : 1; }
+constexpr int wave_cols(int ksplit) { return ksplit == 4 ? 1 : 2; }
+
 // TM x TN tiles of 32 x 32 per wave; U k-steps per slot; Q slots in flight;
-// KSPLIT K halves per workgroup; RS scale quads in flight; NKC = k-steps per
-// wave when fixed at compile time (fully unrolled), 0 for a loop.
+// KSPLIT K parts per workgroup; RS scale quads in flight; NKC = k-steps per
+// wave when fixed at compile time (fully unrolled), 0 for a loop. One loop
+// body is ROT turns of the slot ring, enough to cover whole rounds of the
+// scale ring.
 template <bool A_FP8, int TM, int TN, int U, int Q, int KSPLIT, int RS, int NKC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_kernel(
     const uint8_t* __restrict__ wf, const uint8_t* __restrict__ wsf, const uint8_t* __restrict__ xf,
     const uint8_t* __restrict__ xsf, float* __restrict__ y, uint32_t m, uint32_t n, uint32_t k) {
-    static_assert((Q * U) % 4 == 0 && ((Q * U) / 4) % RS == 0, "slots must cover whole scale quads");
-    constexpr int WM = KSPLIT == 1 ? 2 : 1;
-    constexpr uint32_t BM = WM * 32 * TM, BN = 2 * 32 * TN;
+    static_assert((Q * U) % 4 == 0, "slots must cover whole scale quads");
+    constexpr int ROT = ((Q * U) / 4) % RS == 0 ? 1 : RS;
+    static_assert(((ROT * Q * U) / 4) % RS == 0, "a loop body must cover whole rounds of the scale ring");
+    static_assert(KSPLIT == 1 || KSPLIT == 2 || KSPLIT == 4, "K split of 1, 2 or 4 waves");
+    constexpr int WM = wave_rows(KSPLIT), WN = wave_cols(KSPLIT);
+    constexpr uint32_t BM = WM * 32 * TM, BN = WN * 32 * TN;
     constexpr uint32_t AF = A_FP8 ? 2048 : 1024;  // bytes of one A fragment
     const uint32_t t = threadIdx.x, lane = t % 64;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t / 64);
-    const uint32_t wn = wave % 2;
+    const uint32_t wn = wave % WN;
     const uint32_t wm = KSPLIT == 1 ? wave / 2 : 0;
-    const uint32_t kh = KSPLIT == 1 ? 0 : wave / 2;
+    const uint32_t kh = wave / (WM * WN);
     const uint32_t m0 = blockIdx.y * BM + wm * 32 * TM;
     const uint32_t n0 = blockIdx.x * BN + wn * 32 * TN;
     const uint32_t nk_all = k / 64, nq_all = k / 256;
@@ -176,57 +187,69 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int r = 0; r < RS - 1; ++r) issue_scales(r, sa[r], sb[r]);
 #pragma unroll
     for (int j = 0; j < Q; ++j) issue(j, sl[j]);
-    // one turn of the ring: Q slots of U k-steps starting at k-step `base`
-    auto turn = [&](uint32_t base) {
+    // ROT turns of the ring: Q slots of U k-steps each, from k-step `base`
+    auto body = [&](uint32_t base) {
 #pragma unroll
-        for (int j = 0; j < Q; ++j) {
+        for (int rot = 0; rot < ROT; ++rot)
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int kl = j * U + u;
-                const int g = kl / 4, o = kl % 4;
-                if (o == 0) issue_scales(base / 4 + g + RS - 1, sa[(g + RS - 1) % RS], sb[(g + RS - 1) % RS]);
-                switch (o) {
-                    case 0: kstep<0, A_FP8, TM, TN>(sl[j].a[u], sl[j].b[u], sa[g % RS], sb[g % RS], acc); break;
-                    case 1: kstep<1, A_FP8, TM, TN>(sl[j].a[u], sl[j].b[u], sa[g % RS], sb[g % RS], acc); break;
-                    case 2: kstep<2, A_FP8, TM, TN>(sl[j].a[u], sl[j].b[u], sa[g % RS], sb[g % RS], acc); break;
-                    default: kstep<3, A_FP8, TM, TN>(sl[j].a[u], sl[j].b[u], sa[g % RS], sb[g % RS], acc); break;
+            for (int j = 0; j < Q; ++j) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int kl = (rot * Q + j) * U + u;
+                    const int g = kl / 4, o = kl % 4;
+                    if (o == 0) issue_scales(base / 4 + g + RS - 1, sa[(g + RS - 1) % RS], sb[(g + RS - 1) % RS]);
+                    switch (o) {
+                        case 0: kstep<0, A_FP8, TM, TN>(sl[j].a[u], sl[j].b[u], sa[g % RS], sb[g % RS], acc); break;
+                        case 1: kstep<1, A_FP8, TM, TN>(sl[j].a[u], sl[j].b[u], sa[g % RS], sb[g % RS], acc); break;
+                        case 2: kstep<2, A_FP8, TM, TN>(sl[j].a[u], sl[j].b[u], sa[g % RS], sb[g % RS], acc); break;
+                        default: kstep<3, A_FP8, TM, TN>(sl[j].a[u], sl[j].b[u], sa[g % RS], sb[g % RS], acc); break;
+                    }
                 }
+                // refill this slot only after its MFMAs were issued: otherwise the
+                // scheduler hoists every refill to the end of the ring turn
+                __builtin_amdgcn_sched_barrier(0);
+                issue(base / U + rot * Q + j + Q, sl[j]);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            // refill this slot only after its MFMAs were issued: otherwise the
-            // scheduler hoists every refill to the end of the ring turn
-            __builtin_amdgcn_sched_barrier(0);
-            issue(base / U + j + Q, sl[j]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
     };
     if constexpr (NKC != 0) {
         // straight-line code: the wait counts stay exact (in a loop the compiler
         // waits for every outstanding load at the loop head)
+        static_assert(NKC % (ROT * Q * U) == 0, "the unrolled form covers whole loop bodies");
 #pragma unroll
-        for (uint32_t base = 0; base < (uint32_t)NKC; base += Q * U) turn(base);
+        for (uint32_t base = 0; base < (uint32_t)NKC; base += ROT * Q * U) body(base);
     } else {
-        for (uint32_t base = 0; base < nk; base += Q * U) turn(base);
+        // a partial last body reads zeros past the resources' K range
+        for (uint32_t base = 0; base < nk; base += ROT * Q * U) body(base);
     }
     mfma_drain();
 
-    if constexpr (KSPLIT == 2) {
-        __shared__ float red[2][TM * TN * 16][64];
-        if (kh == 1) {
+    if constexpr (KSPLIT > 1) {
+        // K parts meet as a tree: part p + KSPLIT/2 into p, then part 1 into 0
+        // (a fixed order, so repeated calls agree bit for bit). Waves that are
+        // done return; a barrier waits only for the waves still running.
+        constexpr int HALF = KSPLIT / 2;
+        __shared__ float red[WN][HALF][TM * TN * 16][64];
+#pragma unroll
+        for (int width = HALF; width >= 1; width /= 2) {
+            if (kh >= (uint32_t)width) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) red[wn][kh - width][(i * TN + j) * 16 + v][lane] = acc[i][j][v];
+            }
+            __syncthreads();
+            if (kh >= (uint32_t)width) return;
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) red[wn][(i * TN + j) * 16 + v][lane] = acc[i][j][v];
+                    for (int v = 0; v < 16; ++v) acc[i][j][v] += red[wn][kh][(i * TN + j) * 16 + v][lane];
+            if (width > 1) __syncthreads();
         }
-        __syncthreads();
-        if (kh == 1) return;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) acc[i][j][v] += red[wn][(i * TN + j) * 16 + v][lane];
     }
     // Branch-free stores through a resource over y (prefill_supported keeps
     // row n 4 + 4 col below 2^31 over the whole grid): rows past m fall
@@ -295,18 +318,39 @@ __global__ __launch_bounds__(256) void scales_to_fragments_kernel(const uint8_t*
 
 template <bool A_FP8, int TM, int TN, int U, int Q, int KSPLIT, int RS, int NKC>
 hipError_t go(const PrefillArgs& a) {
-    constexpr uint32_t BM = (KSPLIT == 1 ? 2 : 1) * 32 * TM, BN = 64 * TN;
+    constexpr uint32_t BM = wave_rows(KSPLIT) * 32 * TM, BN = wave_cols(KSPLIT) * 32 * TN;
     dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM);
     hipLaunchKernelGGL((prefill_kernel<A_FP8, TM, TN, U, Q, KSPLIT, RS, NKC>), grid, dim3(256), 0, a.stream, a.wf,
                        a.wsf, a.xf, a.xsf, a.y, a.m, a.n, a.k);
     return hipGetLastError();
 }
 
+// Wave tiles of TM x TN fragments with K in KS parts inside the workgroup,
+// four k-steps in flight per wave; unrolled for the model's K sizes. Each
+// part must start on a whole scale quad (four k-steps).
+template <bool A_FP8, int TM, int TN, int KS>
+hipError_t go_parts(const PrefillArgs& a) {
+    if (a.k % (256 * KS) != 0) return hipErrorNotSupported;
+    if (a.k == 4096) return go<A_FP8, TM, TN, 1, 4, KS, 2, 4096 / 64 / KS>(a);
+    if (a.k == 12288) return go<A_FP8, TM, TN, 1, 4, KS, 2, 12288 / 64 / KS>(a);
+    return go<A_FP8, TM, TN, 1, 4, KS, 2, 0>(a);
+}
+
 template <bool A_FP8>
 hipError_t dispatch(const PrefillArgs& a) {
     if (a.tile_m != 0) {
         // tuning: one explicit instance. Workgroup tiles: 128 x 192 and
-        // 128 x 128 over the full K; 64 x 128 with K halves inside it.
+        // 128 x 128 over the full K; 64 x 128 with K halves inside it; wave
+        // tiles of 128 x 96 in K halves (128 x 192) or of 128 x 64, 64 x 128,
+        // 128 x 96 and 128 x 128 in K quarters.
+        if (a.split_k == 2 && a.tile_m == 128 && a.tile_n == 192) return go_parts<A_FP8, 4, 3, 2>(a);
+        if (a.split_k == 4) {
+            if (a.tile_m == 128 && a.tile_n == 64) return go_parts<A_FP8, 4, 2, 4>(a);
+            if (a.tile_m == 64 && a.tile_n == 128) return go_parts<A_FP8, 2, 4, 4>(a);
+            if (a.tile_m == 128 && a.tile_n == 96) return go_parts<A_FP8, 4, 3, 4>(a);
+            if (a.tile_m == 128 && a.tile_n == 128) return go_parts<A_FP8, 4, 4, 4>(a);
+            return hipErrorNotSupported;
+        }
         if (a.tile_m == 128 && a.tile_n == 192 && a.split_k == 1 && a.k % 512 == 0)
             return go<A_FP8, 2, 3, 2, 4, 1, 2, 0>(a);
         if (a.tile_m == 128 && a.tile_n == 128 && a.split_k == 1)
@@ -318,12 +362,12 @@ hipError_t dispatch(const PrefillArgs& a) {
         }
         return hipErrorNotSupported;
     }
-    // measured on MI355X at M = 512 (Qwen3-8B shapes): wide N keeps 2 x 3 tiles
-    // per wave over the full K; otherwise 2 x 2 tiles with K split in two
-    // inside the workgroup, fully unrolled for the model's K sizes
-    if constexpr (!A_FP8) {
-        if (a.n >= 8192 && a.n % 192 == 0 && a.k % 512 == 0) return go<false, 2, 3, 2, 4, 1, 2, 0>(a);
-    }
+    // measured on MI355X at M = 512 (Qwen3-8B shapes): wide N takes 4 x 3 tiles
+    // per wave with K in halves (gate/up: MXFP4 23.0 -> 21.9 us, MX-FP8 36.8
+    // -> 27.6 us against 2 x 3 tiles over the full K); otherwise 2 x 2 tiles
+    // with K split in two inside the workgroup, fully unrolled for the model's
+    // K sizes (larger tiles and K quarters measured slower there)
+    if (a.n >= 8192 && a.k % 512 == 0) return go_parts<A_FP8, 4, 3, 2>(a);
     if (a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 2, 2, 32>(a);
     if (a.k == 12288) return go<A_FP8, 2, 2, 2, 4, 2, 2, 96>(a);
     if (a.k % 512 == 0) return go<A_FP8, 2, 2, 2, 4, 2, 2, 0>(a);

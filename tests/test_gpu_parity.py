@@ -940,9 +940,12 @@ def test_prefill_quantize_once_matmul_many(mx4, ctx, oracle, act):
         assert np.array_equal(yb.download(np.float32).reshape(m, n), _run_prefill(mx4, ctx, x, w, act, mx4.BF16))
 
 
-PREFILL_INSTANCES = ([(4096, t) for t in ((128, 192, 1), (128, 128, 1), (64, 128, 2))] +
-                     [(12288, t) for t in ((128, 128, 1), (64, 128, 2))] +
-                     [(1536, t) for t in ((128, 192, 1), (128, 128, 1), (64, 128, 2))] +
+PREFILL_INSTANCES = ([(4096, t) for t in ((128, 192, 1), (128, 128, 1), (64, 128, 2), (128, 192, 2), (128, 64, 4),
+                                            (64, 128, 4), (128, 96, 4), (128, 128, 4))] +
+                     [(12288, t) for t in ((128, 128, 1), (64, 128, 2), (128, 192, 2), (128, 64, 4), (64, 128, 4),
+                                           (128, 96, 4), (128, 128, 4))] +
+                     [(1536, t) for t in ((128, 192, 1), (128, 128, 1), (64, 128, 2), (128, 192, 2))] +
+                     [(2048, t) for t in ((128, 64, 4), (64, 128, 4), (128, 96, 4), (128, 128, 4))] +
                      [(1280, (128, 128, 1)), (768, (128, 128, 1))])
 
 
@@ -978,7 +981,11 @@ def test_prefill_config_rejects_unknown_instance(mx4, ctx):
     codes, sc = ctx.prefill_act_buffers(m, k, mx4.ACT_MXFP4)
     yb = ctx.buffer(m * n * 4)
     assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 96, 256, 1) == mx4.ERR_UNSUPPORTED
-    assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 64, 128, 4) == mx4.ERR_UNSUPPORTED
+    assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 64, 64, 4) == mx4.ERR_UNSUPPORTED
+    # K quarters must start on whole scale quads (K % 1024 == 0)
+    w2 = ctx.synth_weight(8, n, 1536, 0.02)
+    codes2, sc2 = ctx.prefill_act_buffers(m, 1536, mx4.ACT_MXFP4)
+    assert ctx.prefill_config(codes2, sc2, mx4.ACT_MXFP4, m, w2, yb, 128, 64, 4) == mx4.ERR_UNSUPPORTED
 
 
 def test_prefill_recorded_pass_after_prepare(mx4, ctx, oracle):
