@@ -19,7 +19,15 @@ x) + M*N*4 (f32 y). value = bytes per step / wall time per step.
 
 cpu_baseline: the CPU oracle (a restatement of engine/src/lib.rs:240-266) on
 the box's host, one thread, over a bounded sample with the step's shape mix:
-all 7 projections of the first 3 layers plus the matching 3/36 of lm_head's rows.
+all 7 projections of the first 9 layers plus the matching 9/36 of lm_head's
+rows. extra.cpu_all_cores runs the same sample on every host thread (the
+oracle parallelises over output elements; each element keeps its order).
+
+extra also carries the other M = 1 workloads: the Qwen3-1.7B decode step (28
+layers x {q 2048->2048, k/v 2048->1024, o 2048->2048, gate/up 2048->6144,
+down 6144->2048} + lm_head 2048->151936, tensor j from seed 2000 + j, grouped
+and recorded like the 8B step) with its per-shape figures, and the single
+6144 x 2048 GEMV of the weight from seed 0 and x from seed 1.
 """
 from __future__ import annotations
 
@@ -42,6 +50,10 @@ LAYER = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 40
 LM_HEAD = ("lm_head", 151936, 4096)
 LAYERS = 36
 HBM_PEAK_GBS = 8000.0
+LAYER_1P7B = [("q", 2048, 2048), ("k", 1024, 2048), ("v", 1024, 2048), ("o", 2048, 2048),
+              ("gate", 6144, 2048), ("up", 6144, 2048), ("down", 2048, 6144)]
+LM_HEAD_1P7B = ("lm_head", 151936, 2048)
+LAYERS_1P7B = 28
 
 
 def gemv_bytes(m: int, n: int, k: int, x_bytes: int = 2) -> int:
@@ -52,28 +64,45 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def build_step(ctx: mx4hip.Context):
+def build_step(ctx: mx4hip.Context, layer=LAYER, lm_head=LM_HEAD, layers=LAYERS, seed0=1000):
     """Distinct resident weights for every projection of the step."""
     weights = []
-    seed = 1000
-    for layer in range(LAYERS):
-        for name, n, k in LAYER:
+    seed = seed0
+    for _ in range(layers):
+        for name, n, k in layer:
             weights.append((name, n, k, ctx.synth_weight(seed, n, k, 0.02)))
             seed += 1
-    name, n, k = LM_HEAD
+    name, n, k = lm_head
     weights.append((name, n, k, ctx.synth_weight(seed, n, k, 0.02)))
     ctx.synchronize()
     return weights
 
 
-def time_shapes(ctx, weights, xs, ys, reps: int = 3):
+def enqueue_grouped_step(ctx, weights, xs, yq, layer=LAYER, layers=LAYERS):
+    """One decode step as the model issues it: per layer q|k|v (one grouped
+    launch on the shared x), o, gate|up (grouped), down; then lm_head."""
+    hidden = layer[0][2]
+    inter = layer[-1][2]
+    per = len(layer)
+    for li in range(layers):
+        lw = {name: w for (name, _, _, w) in weights[li * per:(li + 1) * per]}
+        ctx.matmul_group(xs[hidden].ptr, mx4hip.BF16, 1, [lw["q"], lw["k"], lw["v"]],
+                         [yq["q"].ptr, yq["k"].ptr, yq["v"].ptr])
+        ctx.matmul_ptr(xs[hidden].ptr, mx4hip.BF16, 1, lw["o"], yq["o"].ptr)
+        ctx.matmul_group(xs[hidden].ptr, mx4hip.BF16, 1, [lw["gate"], lw["up"]], [yq["gate"].ptr, yq["up"].ptr])
+        ctx.matmul_ptr(xs[inter].ptr, mx4hip.BF16, 1, lw["down"], yq["down"].ptr)
+    _, n, k, w = weights[-1]
+    ctx.matmul_ptr(xs[k].ptr, mx4hip.BF16, 1, w, yq["lm_head"].ptr)
+
+
+def time_shapes(ctx, weights, xs, ys, reps: int = 3, layer=LAYER):
     """Per-launch GPU time of each projection shape and of the grouped launches:
-    the 36 distinct copies back to back (cold weights) in a recorded pass, timed
-    with events on the context stream."""
+    the distinct copies of each (one per layer) back to back, cold, in a
+    recorded pass, timed with events on the context stream."""
     by = {}
     for (nm, n, k, w) in weights:
         by.setdefault(nm, []).append((n, k, w))
-    plans = [(name, [name]) for name, _, _ in LAYER] + [("qkv", ["q", "k", "v"]), ("gate_up", ["gate", "up"]),
+    plans = [(name, [name]) for name, _, _ in layer] + [("qkv", ["q", "k", "v"]), ("gate_up", ["gate", "up"]),
                                                          ("lm_head", ["lm_head"])]
     table = {}
     for label, members in plans:
@@ -219,8 +248,70 @@ def time_prefill(ctx, weights, m: int = 512, reps: int = 5):
     return out
 
 
-def cpu_baseline(ctx, weights, x_host: dict, layers: int = 9) -> dict:
-    """The oracle on the host: one thread, `layers` layers + the matching share of lm_head."""
+def time_model_1p7b(ctx, steps: int, warmup: int, reps: int = 3) -> dict:
+    """The Qwen3-1.7B decode step at M = 1 (28 layers, 0.92 GB of distinct
+    resident weights), grouped and recorded like the 8B step, plus its
+    per-shape figures. The weights are released afterwards."""
+    weights = build_step(ctx, LAYER_1P7B, LM_HEAD_1P7B, LAYERS_1P7B, seed0=2000)
+    xs = {}
+    for k in sorted({k for (_, _, k, _) in weights}):
+        xs[k] = ctx.buffer(k * 2)
+        ctx.synth_bf16(1, 1.0, k, xs[k])
+    ys = {n: ctx.buffer(n * 4) for n in sorted({n for (_, n, _, _) in weights})}
+    yq = {name: ctx.buffer(n * 4) for name, n, _ in LAYER_1P7B + [LM_HEAD_1P7B]}
+    step_bytes = sum(gemv_bytes(1, n, k) for (_, n, k, _) in weights)
+    p = ctx.record(lambda: enqueue_grouped_step(ctx, weights, xs, yq, LAYER_1P7B, LAYERS_1P7B))
+    for _ in range(warmup):
+        p.launch()
+    ctx.synchronize()
+    best = None
+    for _ in range(reps):
+        ctx.synchronize()
+        ctx.timer_begin()
+        for _ in range(steps):
+            p.launch()
+        ms = ctx.timer_end() / steps
+        best = ms if best is None else min(best, ms)
+    p.release()
+    gbps = step_bytes / (best * 1e-3) / 1e9
+    out = {"workload": "qwen3-1.7b decode step, M=1: 28 layers x 7 projections + lm_head (197 GEMVs, "
+                       f"{LAYERS_1P7B * 4 + 1} launches)",
+           "bytes_per_step": step_bytes, "ms_per_step": round(best, 4), "GBps": round(gbps, 1),
+           "frac": round(gbps / HBM_PEAK_GBS, 4),
+           "shapes": time_shapes(ctx, weights, xs, ys, layer=LAYER_1P7B)}
+    ctx.synchronize()
+    for (_, _, _, w) in weights:
+        w.release()
+    return out
+
+
+def time_config1(ctx, reps: int = 5) -> dict:
+    """The single GEMV of the CPU reference case: W 6144 x 2048 from seed 0,
+    x bf16 [1, 2048] from seed 1, y f32 [1, 6144]; 8 calls per recorded pass
+    on the same (warm) weight."""
+    n, k = 6144, 2048
+    w = ctx.synth_weight(0, n, k, 0.02)
+    x = ctx.buffer(k * 2)
+    ctx.synth_bf16(1, 1.0, k, x)
+    y = ctx.buffer(n * 4)
+    p = ctx.record(lambda: [ctx.matmul_ptr(x.ptr, mx4hip.BF16, 1, w, y.ptr) for _ in range(8)])
+    p.launch()
+    best = None
+    for _ in range(reps):
+        ctx.synchronize()
+        ctx.timer_begin()
+        p.launch()
+        t = ctx.timer_end() / 8
+        best = t if best is None else min(best, t)
+    p.release()
+    ctx.synchronize()
+    w.release()
+    b = gemv_bytes(1, n, k)
+    return {"n": n, "k": k, "bytes": b, "us": round(best * 1e3, 3), "GBps": round(b / (best * 1e-3) / 1e9, 1)}
+
+
+def cpu_baseline(ctx, weights, x_host: dict, layers: int = 9, threads: int = 1) -> dict:
+    """The oracle on the host: `threads` threads, `layers` layers + the matching share of lm_head."""
     from oracle import mx4_oracle as oracle
 
     if not oracle.LIB_PATH.exists():
@@ -235,13 +326,21 @@ def cpu_baseline(ctx, weights, x_host: dict, layers: int = 9) -> dict:
         packed, scales = ctx.download_weight(w)
         x = x_host[k]
         t0 = time.perf_counter()
-        oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), 0, rows, threads=1)
+        oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), 0, rows, threads=threads)
         total_s += time.perf_counter() - t0
         total_bytes += gemv_bytes(1, rows, k)
-    return {"value": round(total_bytes / total_s / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+    how = "single-threaded" if threads == 1 else f"{threads}-thread"
+    return {"value": round(total_bytes / total_s / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"first {layers} of 36 layers (all 7 projections) + {layers}/36 of lm_head rows, "
-                      f"{total_bytes} B in {total_s:.1f} s, single-threaded C restatement of "
+                      f"{total_bytes} B in {total_s:.1f} s, {how} C restatement of "
                       "engine/src/lib.rs:240-266"}
+
+
+def host_threads() -> int:
+    """Threads this process may use: the scheduler's CPU set, capped by OMP_NUM_THREADS when set."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(env))) if env.isdigit() else n
 
 
 def main() -> int:
@@ -255,6 +354,7 @@ def main() -> int:
     ap.add_argument("--no-shapes", action="store_true")
     ap.add_argument("--no-skinny", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-1p7b", action="store_true", help="skip the Qwen3-1.7B step and the single config-1 GEMV")
     ap.add_argument("--profile-traffic", action="store_true",
                     help="for counter runs: 2 eager grouped steps, then a 1 GiB device copy as the byte calibration")
     ap.add_argument("--profile-prefill", action="store_true",
@@ -289,18 +389,10 @@ def main() -> int:
     ops = ctx.make_ops([(xs[k].ptr, mx4hip.BF16, 1, w, ys[n].ptr) for (_, n, k, w) in weights])
     step_bytes = sum(gemv_bytes(1, n, k) for (_, n, k, _) in weights)
     # per layer: q|k|v share x, gate|up share x (distinct y buffers for each)
-    yq = {name: ctx.buffer(n * 4) for name, n, _ in LAYER}
+    yq = {name: ctx.buffer(n * 4) for name, n, _ in LAYER + [LM_HEAD]}
 
     def enqueue_grouped():
-        for layer in range(LAYERS):
-            lw = {name: w for (name, _, _, w) in weights[layer * len(LAYER):(layer + 1) * len(LAYER)]}
-            ctx.matmul_group(xs[4096].ptr, mx4hip.BF16, 1, [lw["q"], lw["k"], lw["v"]],
-                             [yq["q"].ptr, yq["k"].ptr, yq["v"].ptr])
-            ctx.matmul_ptr(xs[4096].ptr, mx4hip.BF16, 1, lw["o"], yq["o"].ptr)
-            ctx.matmul_group(xs[4096].ptr, mx4hip.BF16, 1, [lw["gate"], lw["up"]], [yq["gate"].ptr, yq["up"].ptr])
-            ctx.matmul_ptr(xs[12288].ptr, mx4hip.BF16, 1, lw["down"], yq["down"].ptr)
-        _, n, k, w = weights[-1]
-        ctx.matmul_ptr(xs[k].ptr, mx4hip.BF16, 1, w, ys[n].ptr)
+        enqueue_grouped_step(ctx, weights, xs, yq)
 
     if args.separate:
         enqueue = lambda: ctx.matmul_batch(ops)  # noqa: E731
@@ -384,10 +476,19 @@ def main() -> int:
         log("prefill (M=512, block-scaled MFMA) timing")
         extra["prefill"] = time_prefill(ctx, weights)
 
+    if not args.no_1p7b:
+        log("qwen3-1.7b decode step and the config-1 GEMV")
+        extra["qwen3_1p7b"] = time_model_1p7b(ctx, max(5, args.steps // 2), max(1, args.warmup))
+        extra["single_gemv_6144x2048"] = time_config1(ctx)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, 1 thread)")
         cpu = cpu_baseline(ctx, weights, x_host)
+        nt = host_threads()
+        if nt > 1:
+            log(f"cpu baseline (oracle, {nt} threads)")
+            extra["cpu_all_cores"] = cpu_baseline(ctx, weights, x_host, threads=nt)
 
     # HBM bytes per step from the committed FETCH_SIZE + WRITE_SIZE counter runs
     traffic = None
