@@ -95,13 +95,39 @@ def enqueue_grouped_step(ctx, weights, xs, yq, layer=LAYER, layers=LAYERS):
     ctx.matmul_ptr(xs[k].ptr, mx4hip.BF16, 1, w, yq["lm_head"].ptr)
 
 
-def time_shapes(ctx, weights, xs, ys, reps: int = 3, layer=LAYER):
-    """Per-launch GPU time of each projection shape and of the grouped launches:
-    the distinct copies of each (one per layer) back to back, cold, in a
-    recorded pass, timed with events on the context stream."""
-    by = {}
+MIN_COPIES = 4
+
+
+def copies_by_name(ctx, weights, seed0: int = 9000):
+    """The weights grouped by projection name, each with at least MIN_COPIES
+    distinct copies: a shape with a single weight (lm_head) gets extra copies
+    from the same recipe, so that its per-launch time is taken over several
+    cold launches in one recorded pass, as for the per-layer shapes. Returns
+    the groups and the extra weights (to release afterwards)."""
+    by, extra = {}, []
     for (nm, n, k, w) in weights:
         by.setdefault(nm, []).append((n, k, w))
+    for nm, lst in by.items():
+        n, k, _ = lst[0]
+        while len(lst) < MIN_COPIES:
+            w = ctx.synth_weight(seed0 + len(extra), n, k, 0.02)
+            extra.append(w)
+            lst.append((n, k, w))
+    ctx.synchronize()
+    return by, extra
+
+
+def release(ctx, extra) -> None:
+    ctx.synchronize()
+    for w in extra:
+        w.release()
+
+
+def time_shapes(ctx, weights, xs, ys, reps: int = 3, layer=LAYER):
+    """Per-launch GPU time of each projection shape and of the grouped launches:
+    the distinct copies of each (one per layer; lm_head in four copies) back to
+    back, cold, in a recorded pass, timed with events on the context stream."""
+    by, extra = copies_by_name(ctx, weights)
     plans = [(name, [name]) for name, _, _ in layer] + [("qkv", ["q", "k", "v"]), ("gate_up", ["gate", "up"]),
                                                          ("lm_head", ["lm_head"])]
     table = {}
@@ -136,16 +162,16 @@ def time_shapes(ctx, weights, xs, ys, reps: int = 3, layer=LAYER):
         table[label] = {"k": k, "n": n, "bytes": b, "us": round(best * 1e3, 3),
                         "GBps": round(b / (best * 1e-3) / 1e9, 1),
                         "frac": round(b / (best * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    release(ctx, extra)
     return table
 
 
 def time_skinny(ctx, weights, ms=(1, 2, 4, 8, 16, 32), reps: int = 3):
     """Speculative-verify shapes: each 8B projection at M token rows (exact path:
-    GEMV for M = 1, skinny bf16-MFMA kernel above), 36 cold copies in a recorded
-    pass, per-call latency and effective GB/s (bytes with M*K*2 + M*N*4)."""
-    by = {}
-    for (nm, n, k, w) in weights:
-        by.setdefault(nm, []).append((n, k, w))
+    GEMV for M = 1, skinny bf16-MFMA kernel above), 36 cold copies (lm_head: 4)
+    in a recorded pass, per-call latency and effective GB/s (bytes with
+    M*K*2 + M*N*4)."""
+    by, extra = copies_by_name(ctx, weights)
     out = {}
     for name, n, k in LAYER + [LM_HEAD]:
         ws = [w for (_, _, w) in by[name]]
@@ -172,6 +198,7 @@ def time_skinny(ctx, weights, ms=(1, 2, 4, 8, 16, 32), reps: int = 3):
             b = gemv_bytes(m, n, k)
             row[f"M{m}"] = {"us": round(best * 1e3, 3), "GBps": round(b / (best * 1e-3) / 1e9, 1)}
         out[name] = row
+    release(ctx, extra)
     return out
 
 
