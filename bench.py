@@ -337,6 +337,53 @@ def time_config1(ctx, reps: int = 5) -> dict:
     return {"n": n, "k": k, "bytes": b, "us": round(best * 1e3, 3), "GBps": round(b / (best * 1e-3) / 1e9, 1)}
 
 
+def time_prefill_layer(ctx, weights, m: int = 512, reps: int = 5) -> dict:
+    """All seven projections of one 8B layer at M = 512 as a model issues them:
+    q|k|v as one grouped launch on one requantization, o, gate|up grouped, and
+    down (4 requantizations + 4 GEMMs), against the seven projections launched
+    one by one (7 + 7). Layer 0's weights; 8 layers per recorded pass."""
+    lw = {name: w for (name, _, _, w) in weights[:len(LAYER)]}
+    for w in lw.values():
+        w.prepare_prefill()
+    dims = {name: (n, k) for name, n, k in LAYER}
+    ctx.reserve_prefill(m, max(k for (_, k) in dims.values()))
+    xb = {k: ctx.buffer(m * k * 2) for k in {k for (_, k) in dims.values()}}
+    for k, b in xb.items():
+        ctx.synth_bf16(3, 1.0, m * k, b)
+    ys = {name: ctx.buffer(m * n * 4) for name, (n, _) in dims.items()}
+    flops = sum(2.0 * m * n * k for (n, k) in dims.values())
+    peaks = {"mxfp4": 10.1e15, "mxfp8": 5.0e15}
+    out = {"m": m, "flops": flops}
+    for act, code in (("mxfp4", mx4hip.ACT_MXFP4), ("mxfp8", mx4hip.ACT_MXFP8)):
+        def grouped():
+            ctx.matmul_prefill_group(xb[4096], mx4hip.BF16, m, [lw["q"], lw["k"], lw["v"]], code,
+                                     [ys["q"], ys["k"], ys["v"]])
+            ctx.matmul_prefill(xb[4096], mx4hip.BF16, m, lw["o"], code, ys["o"])
+            ctx.matmul_prefill_group(xb[4096], mx4hip.BF16, m, [lw["gate"], lw["up"]], code, [ys["gate"], ys["up"]])
+            ctx.matmul_prefill(xb[12288], mx4hip.BF16, m, lw["down"], code, ys["down"])
+
+        def separate():
+            for name, (_, k) in dims.items():
+                ctx.matmul_prefill(xb[k], mx4hip.BF16, m, lw[name], code, ys[name])
+
+        res = {}
+        for label, fn in (("grouped", grouped), ("separate", separate)):
+            p = ctx.record(lambda: [fn() for _ in range(8)])
+            p.launch()
+            best = None
+            for _ in range(reps):
+                ctx.synchronize()
+                ctx.timer_begin()
+                p.launch()
+                t = ctx.timer_end() / 8
+                best = t if best is None else min(best, t)
+            p.release()
+            tf = flops / (best * 1e-3)
+            res[label] = {"us": round(best * 1e3, 2), "TFLOPs": round(tf / 1e12, 1), "frac": round(tf / peaks[act], 4)}
+        out[act] = res
+    return out
+
+
 def cpu_baseline(ctx, weights, x_host: dict, layers: int = 9, threads: int = 1) -> dict:
     """The oracle on the host: `threads` threads, `layers` layers + the matching share of lm_head."""
     from oracle import mx4_oracle as oracle
@@ -502,6 +549,7 @@ def main() -> int:
     if not args.no_prefill:
         log("prefill (M=512, block-scaled MFMA) timing")
         extra["prefill"] = time_prefill(ctx, weights)
+        extra["prefill_layer"] = time_prefill_layer(ctx, weights)
 
     if not args.no_1p7b:
         log("qwen3-1.7b decode step and the config-1 GEMV")

@@ -186,6 +186,16 @@ mx4_status mx4_gemv_tokens_config(mx4_context *ctx, const void *x_dev, uint32_t 
 mx4_status mx4_matmul_prefill(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m,
                               const mx4_weight *w, mx4_act_format act, float *y_dev);
 
+/* mx4_matmul_prefill for up to 4 weights of the same width that read the
+ * same activations (q|k|v at engine/src/lib.rs:353-355, gate|up at
+ * :459-467): one requantization and one block-scaled MFMA launch, the
+ * weights' output columns side by side in its grid. y_dev[i][m][w[i].rows];
+ * each output equals mx4_matmul_prefill's for its weight within f32 rounding
+ * (the same, bit for bit, when the group's default instance is the weight's). */
+mx4_status mx4_matmul_prefill_group(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m,
+                                    const mx4_weight *const *w, mx4_act_format act, float *const *y_dev,
+                                    uint32_t count);
+
 /* One projection of a batch or recorded pass: y[m][w.rows] = x[m][w.cols] . W^T. */
 typedef struct mx4_op {
     const void *x;
@@ -243,6 +253,11 @@ mx4_status mx4_prefill_quantize(mx4_context *ctx, const void *x_dev, mx4_dtype x
                                 mx4_act_format act, uint8_t *codes_dev, uint8_t *scales_dev);
 mx4_status mx4_prefill_matmul(mx4_context *ctx, const uint8_t *codes_dev, const uint8_t *scales_dev,
                               mx4_act_format act, uint32_t m, const mx4_weight *w, float *y_dev);
+/* mx4_prefill_matmul over 1 to 4 weights of the same width in one launch
+ * (as mx4_matmul_prefill_group, on activations already requantized). */
+mx4_status mx4_prefill_matmul_group(mx4_context *ctx, const uint8_t *codes_dev, const uint8_t *scales_dev,
+                                    mx4_act_format act, uint32_t m, const mx4_weight *const *w,
+                                    float *const *y_dev, uint32_t count);
 
 /* Tuning hook for the prefill GEMM (arguments as mx4_prefill_matmul): the
  * workgroup tile (tile_m rows x tile_n columns) and the number of K parts
@@ -254,6 +269,11 @@ mx4_status mx4_prefill_matmul(mx4_context *ctx, const uint8_t *codes_dev, const 
 mx4_status mx4_prefill_config(mx4_context *ctx, const uint8_t *codes_dev, const uint8_t *scales_dev,
                               mx4_act_format act, uint32_t m, const mx4_weight *w, float *y_dev,
                               uint32_t tile_m, uint32_t tile_n, uint32_t split_k);
+/* The same hook for a group of 1 to 4 weights (as mx4_prefill_matmul_group). */
+mx4_status mx4_prefill_group_config(mx4_context *ctx, const uint8_t *codes_dev, const uint8_t *scales_dev,
+                                    mx4_act_format act, uint32_t m, const mx4_weight *const *w,
+                                    float *const *y_dev, uint32_t count, uint32_t tile_m, uint32_t tile_n,
+                                    uint32_t split_k);
 
 /* engine/src/mxfp4.rs:35-49 on device: out_dev[rows*cols] f32, bit-exact. */
 mx4_status mx4_dequantize(mx4_context *ctx, const mx4_weight *w, float *out_dev);

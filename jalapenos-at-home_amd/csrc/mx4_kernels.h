@@ -66,14 +66,20 @@ hipError_t launch_bf16_matmul(const uint16_t* w, const void* x, bool x_bf16, flo
 // Block-scaled MFMA prefill on requantized activations. Both operands are in
 // the fragment-native layout of prefill.hip (launch_to_fragments, or the
 // quantizers' fragment output).
+// Up to kMaxPrefillGroup weights of the same K that share the activations
+// (q|k|v, gate|up) run as one launch: segment s owns the workgroup columns
+// from its own first tile on, each with its own weight and output.
+constexpr uint32_t kMaxPrefillGroup = 4;
 struct PrefillArgs {
-    const uint8_t* wf;        // weight codes, fragment-native, rows padded to 32
-    const uint8_t* wsf;       // weight scales, fragment-native
-    const uint8_t* xf;        // requantized activations: fp4 or fp8 fragments
-    const uint8_t* xsf;       // activation scales, fragment-native
-    float* y;                 // [m][n]
-    uint32_t m, n, k;
-    bool fp8;                 // activations are MX-FP8 (E4M3) instead of MXFP4
+    const uint8_t* wf[kMaxPrefillGroup];   // weight codes, fragment-native, rows padded to 32
+    const uint8_t* wsf[kMaxPrefillGroup];  // weight scales, fragment-native
+    float* y[kMaxPrefillGroup];            // [m][n[s]]
+    uint32_t n[kMaxPrefillGroup];          // rows of each weight
+    uint32_t count;                        // weights in the group, 1..kMaxPrefillGroup
+    const uint8_t* xf;                     // requantized activations: fp4 or fp8 fragments
+    const uint8_t* xsf;                    // activation scales, fragment-native
+    uint32_t m, k;
+    bool fp8;                              // activations are MX-FP8 (E4M3) instead of MXFP4
     hipStream_t stream;
     // 0: the default for the shape; else the workgroup tile (rows, columns)
     // and K split inside it of a compiled instance (hipErrorNotSupported if none)

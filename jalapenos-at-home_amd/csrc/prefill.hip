@@ -104,10 +104,19 @@ constexpr int wave_cols(int ksplit) { return ksplit == 4 ? 1 : 2; }
 // wave when fixed at compile time (fully unrolled), 0 for a loop. One loop
 // body is ROT turns of the slot ring, enough to cover whole rounds of the
 // scale ring.
+// The weights of one launch: segment s takes workgroup columns [tile0[s],
+// tile0[s + 1]); unused segments start at 0xffffffff.
+struct Segs {
+    const uint8_t* wf[kMaxPrefillGroup];
+    const uint8_t* wsf[kMaxPrefillGroup];
+    float* y[kMaxPrefillGroup];
+    uint32_t n[kMaxPrefillGroup];
+    uint32_t tile0[kMaxPrefillGroup];
+};
+
 template <bool A_FP8, int TM, int TN, int U, int Q, int KSPLIT, int RS, int NKC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_kernel(
-    const uint8_t* __restrict__ wf, const uint8_t* __restrict__ wsf, const uint8_t* __restrict__ xf,
-    const uint8_t* __restrict__ xsf, float* __restrict__ y, uint32_t m, uint32_t n, uint32_t k) {
+    const Segs segs, const uint8_t* __restrict__ xf, const uint8_t* __restrict__ xsf, uint32_t m, uint32_t k) {
     static_assert((Q * U) % 4 == 0, "slots must cover whole scale quads");
     constexpr int ROT = ((Q * U) / 4) % RS == 0 ? 1 : RS;
     static_assert(((ROT * Q * U) / 4) % RS == 0, "a loop body must cover whole rounds of the scale ring");
@@ -120,8 +129,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const uint32_t wn = wave % WN;
     const uint32_t wm = KSPLIT == 1 ? wave / 2 : 0;
     const uint32_t kh = wave / (WM * WN);
+    // this workgroup's weight: uniform selects over the segment table (an
+    // index into the argument struct would be a memory load)
+    const uint32_t bx = blockIdx.x;
+    const uint8_t* __restrict__ wf = segs.wf[0];
+    const uint8_t* __restrict__ wsf = segs.wsf[0];
+    float* __restrict__ y = segs.y[0];
+    uint32_t n = segs.n[0], t0 = 0;
+#pragma unroll
+    for (int s = 1; s < (int)kMaxPrefillGroup; ++s) {
+        const bool in = bx >= segs.tile0[s];
+        wf = in ? segs.wf[s] : wf;
+        wsf = in ? segs.wsf[s] : wsf;
+        y = in ? segs.y[s] : y;
+        n = in ? segs.n[s] : n;
+        t0 = in ? segs.tile0[s] : t0;
+    }
     const uint32_t m0 = blockIdx.y * BM + wm * 32 * TM;
-    const uint32_t n0 = blockIdx.x * BN + wn * 32 * TN;
+    const uint32_t n0 = (bx - t0) * BN + wn * 32 * TN;
     const uint32_t nk_all = k / 64, nq_all = k / 256;
     const uint32_t nk = NKC ? (uint32_t)NKC : nk_all / KSPLIT;  // k-steps of this wave
     const uint32_t k0 = kh * nk;
@@ -319,9 +344,23 @@ __global__ __launch_bounds__(256) void scales_to_fragments_kernel(const uint8_t*
 template <bool A_FP8, int TM, int TN, int U, int Q, int KSPLIT, int RS, int NKC>
 hipError_t go(const PrefillArgs& a) {
     constexpr uint32_t BM = wave_rows(KSPLIT) * 32 * TM, BN = wave_cols(KSPLIT) * 32 * TN;
-    dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM);
-    hipLaunchKernelGGL((prefill_kernel<A_FP8, TM, TN, U, Q, KSPLIT, RS, NKC>), grid, dim3(256), 0, a.stream, a.wf,
-                       a.wsf, a.xf, a.xsf, a.y, a.m, a.n, a.k);
+    Segs sg{};
+    uint32_t cols = 0;
+    for (uint32_t s = 0; s < kMaxPrefillGroup; ++s) {
+        if (s < a.count) {
+            sg.wf[s] = a.wf[s];
+            sg.wsf[s] = a.wsf[s];
+            sg.y[s] = a.y[s];
+            sg.n[s] = a.n[s];
+            sg.tile0[s] = cols;
+            cols += (a.n[s] + BN - 1) / BN;
+        } else {
+            sg.tile0[s] = 0xffffffffu;
+        }
+    }
+    dim3 grid(cols, (a.m + BM - 1) / BM);
+    hipLaunchKernelGGL((prefill_kernel<A_FP8, TM, TN, U, Q, KSPLIT, RS, NKC>), grid, dim3(256), 0, a.stream, sg,
+                       a.xf, a.xsf, a.m, a.k);
     return hipGetLastError();
 }
 
@@ -362,12 +401,18 @@ hipError_t dispatch(const PrefillArgs& a) {
         }
         return hipErrorNotSupported;
     }
+    uint32_t ntot = 0;
+    for (uint32_t s = 0; s < a.count; ++s) ntot += a.n[s];
     // measured on MI355X at M = 512 (Qwen3-8B shapes): wide N takes 4 x 3 tiles
     // per wave with K in halves (gate/up: MXFP4 23.0 -> 21.9 us, MX-FP8 36.8
     // -> 27.6 us against 2 x 3 tiles over the full K); otherwise 2 x 2 tiles
     // with K split in two inside the workgroup, fully unrolled for the model's
     // K sizes (larger tiles and K quarters measured slower there)
-    if (a.n >= 8192 && a.k % 512 == 0) return go_parts<A_FP8, 4, 3, 2>(a);
+    if (ntot >= 8192 && a.k % 512 == 0) return go_parts<A_FP8, 4, 3, 2>(a);
+    // q|k|v in one launch (4096 + 1024 + 1024 rows, K = 4096): 128 x 128
+    // workgroup tiles over the full K, 192 workgroups (MXFP4 17.3 -> 15.9 us,
+    // MX-FP8 22.4 -> 20.6 us against 2 x 2 tiles in K halves)
+    if (ntot > 4096 && a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 1, 2, 0>(a);
     if (a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 2, 2, 32>(a);
     if (a.k == 12288) return go<A_FP8, 2, 2, 2, 4, 2, 2, 96>(a);
     if (a.k % 512 == 0) return go<A_FP8, 2, 2, 2, 4, 2, 2, 0>(a);
@@ -407,7 +452,9 @@ hipError_t launch_to_fragments(const uint8_t* codes, const uint8_t* scales, uint
 }
 
 hipError_t launch_prefill(const PrefillArgs& a, int) {
-    if (!prefill_supported(a.m, a.n, a.k)) return hipErrorNotSupported;
+    if (a.count < 1 || a.count > kMaxPrefillGroup) return hipErrorNotSupported;
+    for (uint32_t s = 0; s < a.count; ++s)
+        if (!prefill_supported(a.m, a.n[s], a.k)) return hipErrorNotSupported;
     return a.fp8 ? dispatch<true>(a) : dispatch<false>(a);
 }
 

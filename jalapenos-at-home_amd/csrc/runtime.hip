@@ -169,7 +169,19 @@ uint64_t prefill_workspace_bytes(uint64_t m, uint64_t cols, bool fp8) {
 
 mx4::PrefillArgs prefill_args(mx4_context* ctx, const mx4_weight* w, const uint8_t* xf, const uint8_t* xsf,
                               float* y, uint32_t m, bool fp8) {
-    return mx4::PrefillArgs{w->frag, w->frag_scales, xf, xsf, y, m, w->rows, w->cols, fp8, ctx->stream};
+    mx4::PrefillArgs a{};
+    a.wf[0] = w->frag;
+    a.wsf[0] = w->frag_scales;
+    a.y[0] = y;
+    a.n[0] = w->rows;
+    a.count = 1;
+    a.xf = xf;
+    a.xsf = xsf;
+    a.m = m;
+    a.k = w->cols;
+    a.fp8 = fp8;
+    a.stream = ctx->stream;
+    return a;
 }
 
 // The weight's fragment-native copy: built once, outside any recorded pass.
@@ -792,46 +804,113 @@ mx4_status mx4_prefill_quantize(mx4_context* ctx, const void* x, mx4_dtype xt, u
     return MX4_OK;
 }
 
-mx4_status mx4_prefill_matmul(mx4_context* ctx, const uint8_t* codes, const uint8_t* scales, mx4_act_format act,
-                              uint32_t m, const mx4_weight* w, float* y) {
-    if (!ctx || !codes || !scales || !w || !y) return fail(MX4_ERR_ARGUMENT, "null argument");
+namespace {
+
+// One block-scaled MFMA launch over requantized activations for `count`
+// weights of the same K (a group shares the activations), with the default
+// instance (tile_m == 0) or an explicit one.
+mx4_status prefill_group(mx4_context* ctx, const uint8_t* codes, const uint8_t* scales, mx4_act_format act,
+                         uint32_t m, const mx4_weight* const* ws, float* const* ys, uint32_t count, uint32_t tile_m,
+                         uint32_t tile_n, uint32_t split_k) {
+    if (!ctx || !codes || !scales || !ws || !ys) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (count < 1 || count > mx4::kMaxPrefillGroup)
+        return fail(MX4_ERR_ARGUMENT, "a prefill group holds 1 to %u weights", mx4::kMaxPrefillGroup);
     if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
     if (m == 0) return fail(MX4_ERR_ARGUMENT, "m must be at least 1");
-    if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
-    if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
-    if (!mx4::prefill_supported(m, w->rows, w->cols))
-        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0 and operands under 2 GiB");
+    for (uint32_t i = 0; i < count; ++i) {
+        const mx4_weight* w = ws[i];
+        if (!w || !ys[i]) return fail(MX4_ERR_ARGUMENT, "null argument");
+        if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
+        if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
+        if (w->cols != ws[0]->cols) return fail(MX4_ERR_SHAPE, "the weights of a group share K");
+        if (!mx4::prefill_supported(m, w->rows, w->cols))
+            return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0 and operands under 2 GiB");
+    }
     DeviceGuard g(ctx->device);
-    mx4_weight* wm = const_cast<mx4_weight*>(w);
-    mx4_status st = prepare_fragments(ctx, wm);
-    if (st != MX4_OK) return st;
-    hipError_t e = mx4::launch_prefill(prefill_args(ctx, wm, codes, scales, y, m, act == MX4_ACT_MXFP8), ctx->cus);
+    mx4::PrefillArgs a{};
+    for (uint32_t i = 0; i < count; ++i) {
+        mx4_weight* wm = const_cast<mx4_weight*>(ws[i]);  // the fragment copy is a cache of the weight
+        mx4_status st = prepare_fragments(ctx, wm);
+        if (st != MX4_OK) return st;
+        a.wf[i] = wm->frag;
+        a.wsf[i] = wm->frag_scales;
+        a.y[i] = ys[i];
+        a.n[i] = wm->rows;
+    }
+    a.count = count;
+    a.xf = codes;
+    a.xsf = scales;
+    a.m = m;
+    a.k = ws[0]->cols;
+    a.fp8 = act == MX4_ACT_MXFP8;
+    a.stream = ctx->stream;
+    a.tile_m = tile_m;
+    a.tile_n = tile_n;
+    a.split_k = split_k;
+    hipError_t e = mx4::launch_prefill(a, ctx->cus);
+    if (e == hipErrorNotSupported && tile_m != 0) return fail(MX4_ERR_UNSUPPORTED, "no such prefill instance for this shape");
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
     return MX4_OK;
+}
+
+}  // namespace
+
+mx4_status mx4_prefill_matmul(mx4_context* ctx, const uint8_t* codes, const uint8_t* scales, mx4_act_format act,
+                              uint32_t m, const mx4_weight* w, float* y) {
+    return prefill_group(ctx, codes, scales, act, m, &w, &y, 1, 0, 0, 0);
+}
+
+mx4_status mx4_prefill_matmul_group(mx4_context* ctx, const uint8_t* codes, const uint8_t* scales,
+                                    mx4_act_format act, uint32_t m, const mx4_weight* const* ws, float* const* ys,
+                                    uint32_t count) {
+    return prefill_group(ctx, codes, scales, act, m, ws, ys, count, 0, 0, 0);
 }
 
 mx4_status mx4_prefill_config(mx4_context* ctx, const uint8_t* codes, const uint8_t* scales, mx4_act_format act,
                               uint32_t m, const mx4_weight* w, float* y, uint32_t tile_m, uint32_t tile_n,
                               uint32_t split_k) {
-    if (!ctx || !codes || !scales || !w || !y) return fail(MX4_ERR_ARGUMENT, "null argument");
+    return prefill_group(ctx, codes, scales, act, m, &w, &y, 1, tile_m, tile_n, split_k);
+}
+
+mx4_status mx4_prefill_group_config(mx4_context* ctx, const uint8_t* codes, const uint8_t* scales,
+                                    mx4_act_format act, uint32_t m, const mx4_weight* const* ws, float* const* ys,
+                                    uint32_t count, uint32_t tile_m, uint32_t tile_n, uint32_t split_k) {
+    return prefill_group(ctx, codes, scales, act, m, ws, ys, count, tile_m, tile_n, split_k);
+}
+
+mx4_status mx4_matmul_prefill_group(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
+                                    const mx4_weight* const* ws, mx4_act_format act, float* const* ys,
+                                    uint32_t count) {
+    if (!ctx || !ws || !ys) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (count < 1 || count > mx4::kMaxPrefillGroup)
+        return fail(MX4_ERR_ARGUMENT, "a prefill group holds 1 to %u weights", mx4::kMaxPrefillGroup);
+    for (uint32_t i = 0; i < count; ++i) {
+        mx4_status st = check_matmul_args(ctx, x, xt, m, ws[i], ys[i]);
+        if (st != MX4_OK) return st;
+        if (ws[i]->cols != ws[0]->cols) return fail(MX4_ERR_SHAPE, "the weights of a group share K");
+    }
     if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
-    if (m == 0) return fail(MX4_ERR_ARGUMENT, "m must be at least 1");
-    if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
-    if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
-    if (!mx4::prefill_supported(m, w->rows, w->cols))
-        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0 and operands under 2 GiB");
+    for (uint32_t i = 0; i < count; ++i) {
+        if (ws[i]->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
+        if (!mx4::prefill_supported(m, ws[i]->rows, ws[i]->cols))
+            return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0 and operands under 2 GiB");
+    }
     DeviceGuard g(ctx->device);
-    mx4_weight* wm = const_cast<mx4_weight*>(w);
-    mx4_status st = prepare_fragments(ctx, wm);
+    const bool fp8 = act == MX4_ACT_MXFP8;
+    const uint32_t cols = ws[0]->cols;
+    // build every fragment copy before anything is enqueued
+    for (uint32_t i = 0; i < count; ++i) {
+        mx4_status st = prepare_fragments(ctx, const_cast<mx4_weight*>(ws[i]));
+        if (st != MX4_OK) return st;
+    }
+    const uint64_t qoff = (mx4::fragment_bytes(m, cols, fp8) + 255) & ~255ull;
+    mx4_status st = ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(m, cols, fp8));
     if (st != MX4_OK) return st;
-    mx4::PrefillArgs a = prefill_args(ctx, wm, codes, scales, y, m, act == MX4_ACT_MXFP8);
-    a.tile_m = tile_m;
-    a.tile_n = tile_n;
-    a.split_k = split_k;
-    hipError_t e = mx4::launch_prefill(a, ctx->cus);
-    if (e == hipErrorNotSupported) return fail(MX4_ERR_UNSUPPORTED, "no such prefill instance for this shape");
-    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
-    return MX4_OK;
+    uint8_t* xf = static_cast<uint8_t*>(ctx->work);
+    uint8_t* xsf = xf + qoff;
+    hipError_t e = mx4::launch_quantize_fragments(x, xt == MX4_BF16, m, cols, fp8, xf, xsf, ctx->flags, ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "requantize launch failed: %s", hipGetErrorString(e));
+    return prefill_group(ctx, xf, xsf, act, m, ws, ys, count, 0, 0, 0);
 }
 
 mx4_status mx4_matmul_argmax(mx4_context* ctx, const void* x, mx4_dtype xt, const mx4_weight* w, float* y,

@@ -76,6 +76,10 @@ SIGNATURES = {
     "mx4_prefill_quantize": (_int, [_vp, _vp, _int, _u32, _u32, _int, _vp, _vp]),
     "mx4_prefill_matmul": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
     "mx4_prefill_config": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp, _u32, _u32, _u32]),
+    "mx4_prefill_matmul_group": (_int, [_vp, _vp, _vp, _int, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32]),
+    "mx4_prefill_group_config": (_int, [_vp, _vp, _vp, _int, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32,
+                                        _u32, _u32, _u32]),
+    "mx4_matmul_prefill_group": (_int, [_vp, _vp, _int, _u32, ctypes.POINTER(_vp), _int, ctypes.POINTER(_vp), _u32]),
     "mx4_pass_begin": (_int, [_vp]),
     "mx4_pass_end": (_int, [_vp, ctypes.POINTER(_vp)]),
     "mx4_pass_launch": (_int, [_vp, _vp]),
@@ -90,6 +94,14 @@ SIGNATURES = {
     "mx4_timer_end": (_int, [_vp, ctypes.POINTER(ctypes.c_double)]),
     "mx4_decode_table": (_int, [_vp, _int, _vp]),
 }
+
+
+def _handles(ws) -> "ctypes.Array":
+    return (_vp * len(ws))(*[w.handle for w in ws])
+
+
+def _ptrs(bufs) -> "ctypes.Array":
+    return (_vp * len(bufs))(*[b.ptr for b in bufs])
 
 
 def header_symbols() -> list[str]:
@@ -323,6 +335,11 @@ class Context:
     def matmul_prefill(self, x: DeviceBuffer, xtype: int, m: int, w: Weight, act: int, y: DeviceBuffer) -> None:
         check(lib().mx4_matmul_prefill(self.handle, x.ptr, xtype, m, w.handle, act, y.ptr))
 
+    def matmul_prefill_group(self, x: DeviceBuffer, xtype: int, m: int, ws, act: int, ys) -> None:
+        """Requantize x once, then one block-scaled MFMA launch for 1..4 weights (ys: DeviceBuffers)."""
+        wa, ya = _handles(ws), _ptrs(ys)
+        check(lib().mx4_matmul_prefill_group(self.handle, x.ptr, xtype, m, wa, act, ya, len(ws)))
+
     def make_ops(self, ops) -> "ctypes.Array[Op]":
         """ops: iterable of (x_ptr, x_type, m, Weight, y_ptr)."""
         ops = list(ops)
@@ -368,6 +385,18 @@ class Context:
     def prefill_matmul(self, codes: DeviceBuffer, scales: DeviceBuffer, act: int, m: int, w: Weight,
                        y: DeviceBuffer) -> None:
         check(lib().mx4_prefill_matmul(self.handle, codes.ptr, scales.ptr, act, m, w.handle, y.ptr))
+
+    def prefill_matmul_group(self, codes: DeviceBuffer, scales: DeviceBuffer, act: int, m: int, ws, ys) -> None:
+        """mx4_prefill_matmul over 1..4 weights of the same K in one launch (ys: DeviceBuffers)."""
+        wa, ya = _handles(ws), _ptrs(ys)
+        check(lib().mx4_prefill_matmul_group(self.handle, codes.ptr, scales.ptr, act, m, wa, ya, len(ws)))
+
+    def prefill_group_config(self, codes: DeviceBuffer, scales: DeviceBuffer, act: int, m: int, ws, ys,
+                             tile_m: int, tile_n: int, split_k: int) -> int:
+        """Grouped prefill GEMM with an explicit instance; returns the status."""
+        wa, ya = _handles(ws), _ptrs(ys)
+        return lib().mx4_prefill_group_config(self.handle, codes.ptr, scales.ptr, act, m, wa, ya, len(ws),
+                                              tile_m, tile_n, split_k)
 
     def gemv_tokens_config(self, x: DeviceBuffer, m: int, w: Weight, y: DeviceBuffer, teams: int, tpw: int) -> int:
         """Few-token GEMV (bf16 x) with an explicit launch shape; returns the status."""

@@ -975,6 +975,80 @@ def test_prefill_instances_match_oracle(mx4, ctx, oracle, act, k, tile):
     assert np.array_equal(outs[0], outs[1])
 
 
+GROUP_TILES = [(0, 0, 0), (128, 192, 1), (128, 128, 1), (64, 128, 2), (128, 192, 2), (128, 64, 4), (64, 128, 4)]
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+def test_prefill_group_equals_individual(mx4, ctx, oracle, act):
+    """One grouped launch over three weights of the same K (ragged rows, as
+    q|k|v) gives each weight's output bit for bit as the same instance run on
+    that weight alone, for every instance and the default; the default group
+    also matches the oracle on dequant(requant(x))."""
+    m, k = 70, 2048
+    ns = (300, 96, 160)
+    code = mx4.ACT_MXFP4 if act == "mxfp4" else mx4.ACT_MXFP8
+    ws = [ctx.synth_weight(700 + i, n, k, 0.02) for i, n in enumerate(ns)]
+    x = oracle.bf16_to_f32(oracle.synth_bf16(710, 1.0, m * k)).reshape(m, k)
+    xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+    codes, sc = ctx.prefill_act_buffers(m, k, code)
+    ctx.prefill_quantize(xb, mx4.BF16, m, k, code, codes, sc)
+    ys = [ctx.buffer(m * n * 4) for n in ns]
+    y1 = ctx.buffer(max(ns) * m * 4)
+    for tile in GROUP_TILES:
+        say(f"prefill group {act} tile {tile}")
+        for y, n in zip(ys, ns):
+            y.upload(np.full(m * n, np.nan, np.float32))
+        assert ctx.prefill_group_config(codes, sc, code, m, ws, ys, *tile) == 0, mx4.last_error()
+        for w, y, n in zip(ws, ys, ns):
+            y1.upload(np.full(m * max(ns), np.nan, np.float32))
+            assert ctx.prefill_config(codes, sc, code, m, w, y1, *tile) == 0, mx4.last_error()
+            alone = y1.download(np.float32)[: m * n].reshape(m, n)
+            assert np.array_equal(y.download(np.float32).reshape(m, n), alone), (tile, n)
+    for y, n in zip(ys, ns):
+        y.upload(np.full(m * n, np.nan, np.float32))
+    ctx.prefill_matmul_group(codes, sc, code, m, ws, ys)
+    for w, y, n in zip(ws, ys, ns):
+        packed, scales = ctx.download_weight(w)
+        ref, _ = _prefill_ref(oracle, x, packed, scales, act)
+        assert_close(y.download(np.float32).reshape(m, n), ref, f"prefill group {act} n={n}")
+
+
+def test_matmul_prefill_group_requantizes_once(mx4, ctx, oracle):
+    """mx4_matmul_prefill_group (requantize + one grouped launch) at 8B widths
+    (q|k|v rows 4096 + 1024 + 1024, K = 4096; ragged m) against the oracle, and
+    equal to the grouped launch on activations requantized beforehand."""
+    m, k = 40, 4096
+    ns = (4096, 1024, 1024)
+    ws = [ctx.synth_weight(720 + i, n, k, 0.02) for i, n in enumerate(ns)]
+    x = oracle.bf16_to_f32(oracle.synth_bf16(730, 1.0, m * k)).reshape(m, k)
+    xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+    ys = [ctx.buffer(m * n * 4) for n in ns]
+    ctx.matmul_prefill_group(xb, mx4.BF16, m, ws, mx4.ACT_MXFP4, ys)
+    got = [y.download(np.float32).reshape(m, n) for y, n in zip(ys, ns)]
+    codes, sc = ctx.prefill_act_buffers(m, k, mx4.ACT_MXFP4)
+    ctx.prefill_quantize(xb, mx4.BF16, m, k, mx4.ACT_MXFP4, codes, sc)
+    ctx.prefill_matmul_group(codes, sc, mx4.ACT_MXFP4, m, ws, ys)
+    for i, (w, y, n) in enumerate(zip(ws, ys, ns)):
+        assert np.array_equal(y.download(np.float32).reshape(m, n), got[i])
+        packed, scales = ctx.download_weight(w)
+        rows = np.arange(0, n, 7)
+        ref, _ = _prefill_ref(oracle, x, packed.reshape(n, -1)[rows], scales.reshape(n, -1)[rows], "mxfp4")
+        assert_close(got[i][:, rows], ref, f"grouped requant + prefill n={n}")
+
+
+def test_prefill_group_rejects_bad_groups(mx4, ctx):
+    m, k = 32, 1024
+    w1, w2 = ctx.synth_weight(740, 64, k, 0.02), ctx.synth_weight(741, 64, 2048, 0.02)
+    codes, sc = ctx.prefill_act_buffers(m, k, mx4.ACT_MXFP4)
+    y = ctx.buffer(m * 64 * 4)
+    with pytest.raises(mx4.Mx4Error, match="share K"):
+        ctx.prefill_matmul_group(codes, sc, mx4.ACT_MXFP4, m, [w1, w2], [y, y])
+    with pytest.raises(mx4.Mx4Error, match="1 to 4"):
+        ctx.prefill_matmul_group(codes, sc, mx4.ACT_MXFP4, m, [w1] * 5, [y] * 5)
+    with pytest.raises(mx4.Mx4Error, match="1 to 4"):
+        ctx.prefill_matmul_group(codes, sc, mx4.ACT_MXFP4, m, [], [])
+
+
 def test_prefill_config_rejects_unknown_instance(mx4, ctx):
     m, n, k = 64, 256, 4096
     w = ctx.synth_weight(7, n, k, 0.02)
