@@ -280,6 +280,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // row n 4 + 4 col below 2^31 over the whole grid): rows past m fall
     // outside it, and a column past n is biased by 2^31, past its end, so the
     // hardware drops both. (Guarded stores cost a branch per element.)
+    // The stores carry device scope (SC1): at M = 512 the f32 output is as
+    // large as the weights (25 MB for gate), and with the default scope most of
+    // it waited in the L2 for the write-back at the end of the kernel. Measured
+    // per call: q 10.8 -> 10.1 us, gate 21.5 -> 20.2 us, down 22.4 -> 21.9 us.
+    constexpr int kStoreDeviceScope = 0x10;
     const uint32_t r32 = lane % 32, h = lane / 32;
     const __amdgpu_buffer_rsrc_t yr = rsrc(y, m * n * 4);
 #pragma unroll
@@ -291,7 +296,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const uint32_t row = m0 + 32 * i + 8 * (v / 4) + 4 * h + (v % 4);
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][v]), yr, row * n * 4 + cb, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][v]), yr, row * n * 4 + cb, 0,
+                                                      kStoreDeviceScope);
             }
     }
 }
