@@ -249,12 +249,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     mfma_drain();
 
+    // K parts meet as a tree: part p + KSPLIT/2 into p, then part 1 into 0 (a
+    // fixed order, so repeated calls agree bit for bit). Waves that are done
+    // return; a barrier waits only for the waves still running. Partial tiles
+    // cross LDS as 16-byte vectors (lane l's values 4q..4q+3 of a tile at
+    // [tile][q][l]), and the last addition happens tile by tile in the store
+    // loop: summing all tiles first kept every accumulator live in VGPRs, and
+    // the LDS reads then went out two at a time.
+    constexpr int T = TM * TN, HALF = KSPLIT / 2;
+    __shared__ f32x4 red[KSPLIT > 1 ? WN * HALF * T * 4 * 64 : 1];
+    auto red_at = [&](uint32_t part, int tile, int q) -> f32x4& {
+        return red[(((wn * HALF + part) * T + tile) * 4 + q) * 64 + lane];
+    };
     if constexpr (KSPLIT > 1) {
-        // K parts meet as a tree: part p + KSPLIT/2 into p, then part 1 into 0
-        // (a fixed order, so repeated calls agree bit for bit). Waves that are
-        // done return; a barrier waits only for the waves still running.
-        constexpr int HALF = KSPLIT / 2;
-        __shared__ float red[WN][HALF][TM * TN * 16][64];
 #pragma unroll
         for (int width = HALF; width >= 1; width /= 2) {
             if (kh >= (uint32_t)width) {
@@ -263,17 +270,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
 #pragma unroll
-                        for (int v = 0; v < 16; ++v) red[wn][kh - width][(i * TN + j) * 16 + v][lane] = acc[i][j][v];
+                        for (int q = 0; q < 4; ++q)
+                            red_at(kh - width, i * TN + j, q) =
+                                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
             }
             __syncthreads();
             if (kh >= (uint32_t)width) return;
+            if (width > 1) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+                for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
+                    for (int j = 0; j < TN; ++j)
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) acc[i][j][v] += red[wn][kh][(i * TN + j) * 16 + v][lane];
-            if (width > 1) __syncthreads();
+                        for (int q = 0; q < 4; ++q) {
+                            const f32x4 o = red_at(kh, i * TN + j, q);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += o[e];
+                        }
+                __syncthreads();
+            }
         }
     }
     // Branch-free stores through a resource over y (prefill_supported keeps
@@ -292,13 +307,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const uint32_t col = n0 + 32 * j + r32;
         const uint32_t cb = 4 * col + (col < n ? 0u : 0x80000000u);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i) {
+            f32x4 o[4] = {};
+            if constexpr (KSPLIT > 1) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) o[q] = red_at(0, i * TN + j, q);  // part 1's (partial) tile
+            }
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const uint32_t row = m0 + 32 * i + 8 * (v / 4) + 4 * h + (v % 4);
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][v]), yr, row * n * 4 + cb, 0,
+                const float out = KSPLIT > 1 ? acc[i][j][v] + o[v / 4][v % 4] : acc[i][j][v];
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(out), yr, row * n * 4 + cb, 0,
                                                       kStoreDeviceScope);
             }
+        }
     }
 }
 
