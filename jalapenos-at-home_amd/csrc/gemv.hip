@@ -1002,6 +1002,9 @@ hipError_t launch_gemv_mt(const GemvArgs& a, int cus, uint32_t teams, uint32_t t
     MX4_MT(4096, 1, 2)
     MX4_MT(6144, 3, 1)
     MX4_MT(8192, 2, 2)
+    // K = 12288 at 2 tokens: the M = 1 kernel's geometry (2-wave teams, one row
+    // each, four teams per workgroup sharing x through LDS): 8B down 8.77 -> 8.24 us
+    if (a.k == 12288 && a.m <= 2) return go_mt<2, 3, 1, 2>(a, cus, teams, tpw);
     MX4_MT(12288, 3, 2)
 #undef MX4_MT
     return hipErrorNotSupported;
