@@ -17,6 +17,9 @@ one recorded pass (HIP graph) unless --eager is given; --separate launches all
 Algorithmic bytes of one GEMV: N*K/2 (nibbles) + N*K/32 (scales) + M*K*2 (bf16
 x) + M*N*4 (f32 y). value = bytes per step / wall time per step.
 
+extra.dropin_per_call times the per-call drop-in (qwen_hip_matmul: host f32 x
+and y, synchronous) on layer 0 and the lm_head: the PCIe-inclusive rate.
+
 cpu_baseline: the CPU oracle (a restatement of engine/src/lib.rs:240-266) on
 the box's host, one thread, over a bounded sample with the step's shape mix:
 all 7 projections of the first 9 layers plus the matching 9/36 of lm_head's
@@ -273,6 +276,30 @@ def time_prefill(ctx, weights, m: int = 512, reps: int = 5):
             row[act] = res
         out[name] = {"m": m, "n": n, "k": k, **row}
     return out
+
+
+def time_dropin(ctx, weights, x_host: dict, reps: int = 5) -> dict:
+    """The per-call drop-in (qwen_hip_matmul, the qwen_metal_matmul contract):
+    host f32 x in, host f32 y out, synchronous, weights cached by host address
+    after the first call. Layer 0's seven projections and the lm_head, called
+    from Python through ctypes; the PCIe-inclusive rate, never `value`."""
+    sample = weights[:len(LAYER)] + [weights[-1]]
+    host = [(n, k, *ctx.download_weight(w)) for (_, n, k, w) in sample]
+    hip = mx4hip.Hip()
+    for n, k, packed, scales in host:  # uploads and caches the weights
+        hip.matmul(x_host[k], packed, scales)
+    best = None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for n, k, packed, scales in host:
+            hip.matmul(x_host[k], packed, scales)
+        t = time.perf_counter() - t0
+        best = t if best is None else min(best, t)
+    hip.close()
+    b = sum(gemv_bytes(1, n, k, 4) for (n, k, _, _) in host)
+    return {"calls": len(host), "us_per_call": round(best / len(host) * 1e6, 2),
+            "GBps": round(b / best / 1e9, 1), "bytes": b,
+            "sample": "layer 0 (q, k, v, o, gate, up, down) + lm_head, f32 x, host buffers, one call each"}
 
 
 def time_model_1p7b(ctx, steps: int, warmup: int, reps: int = 3) -> dict:
@@ -555,6 +582,8 @@ def main() -> int:
         log("qwen3-1.7b decode step and the config-1 GEMV")
         extra["qwen3_1p7b"] = time_model_1p7b(ctx, max(5, args.steps // 2), max(1, args.warmup))
         extra["single_gemv_6144x2048"] = time_config1(ctx)
+        log("per-call drop-in (host buffers)")
+        extra["dropin_per_call"] = time_dropin(ctx, weights, x_host)
 
     cpu = None
     if not args.no_cpu_baseline:
