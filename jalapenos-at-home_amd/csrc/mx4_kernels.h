@@ -57,7 +57,16 @@ hipError_t launch_embed(const uint8_t* packed, const uint8_t* scales, const uint
 
 // Exact skinny path (2 <= m <= 16) on bf16 MFMA with decoded weights.
 bool skinny_supported(uint32_t m, uint32_t k);
-hipError_t launch_skinny(const GemvArgs& a, int cus);
+// Device scratch of the split-K launches (K = 12288): part_tiles partial tiles
+// of 1 KiB and count_tiles arrival counts, which must be zero before the first
+// launch and are left at zero by every launch. Launches that share it must be
+// ordered (one stream). With no scratch, or too little, the kernel runs unsplit.
+struct SkinnyScratch {
+    float* part = nullptr;
+    uint32_t* count = nullptr;
+    uint32_t part_tiles = 0, count_tiles = 0;
+};
+hipError_t launch_skinny(const GemvArgs& a, int cus, const SkinnyScratch& sc);
 
 // bf16 weights [n][k] (engine/src/lib.rs:255, None arm), any m, f32 accumulation.
 hipError_t launch_bf16_matmul(const uint16_t* w, const void* x, bool x_bf16, float* y, uint32_t m, uint32_t n,

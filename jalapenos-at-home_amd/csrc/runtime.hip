@@ -110,9 +110,16 @@ struct mx4_context {
     // logits of mx4_matmul_argmax when the caller does not want them
     void* logits = nullptr;
     uint64_t logits_cap = 0;
+    // split-K skinny launches: partial tiles (1 KiB each) and per-tile
+    // arrival counts (zero between launches); calls are ordered on `stream`
+    float* split_part = nullptr;
+    uint32_t* split_count = nullptr;
 };
 
 constexpr uint32_t kArgmaxPartials = 8192;
+// 4 MiB of partial tiles: four K slices of up to 8192 rows at 32 tokens
+constexpr uint32_t kSplitPartTiles = 4096;
+constexpr uint32_t kSplitCounts = 4096;
 
 namespace mx4 {
 hipError_t launch_fill_u32(uint32_t* p, uint32_t count, uint32_t value, hipStream_t s);
@@ -268,7 +275,7 @@ mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
                 return fail(MX4_ERR_UNSUPPORTED, "skinny path needs 1 <= m <= 32 and K in {2048, 4096, 6144, 8192, 12288}");
             if (!scales_foldable(w))
                 return fail(MX4_ERR_UNSUPPORTED, "skinny path folds scales into bf16; scale bytes outside 2..252 need GENERIC");
-            e = mx4::launch_skinny(a, ctx->cus);
+            e = mx4::launch_skinny(a, ctx->cus, {ctx->split_part, ctx->split_count, kSplitPartTiles, kSplitCounts});
             break;
         case MX4_PATH_GENERIC:
             e = mx4::launch_gemv_generic(a);
@@ -348,7 +355,11 @@ mx4_status mx4_create(int device, mx4_context** out) {
     if (hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&ctx->ev0) != hipSuccess || hipEventCreate(&ctx->ev1) != hipSuccess ||
         hipMalloc((void**)&ctx->flags, 256) != hipSuccess ||
-        hipMalloc((void**)&ctx->am_partial, kArgmaxPartials * sizeof(uint64_t)) != hipSuccess) {
+        hipMalloc((void**)&ctx->am_partial, kArgmaxPartials * sizeof(uint64_t)) != hipSuccess ||
+        hipMalloc((void**)&ctx->split_part, (size_t)kSplitPartTiles * 1024) != hipSuccess ||
+        hipMalloc((void**)&ctx->split_count, kSplitCounts * sizeof(uint32_t)) != hipSuccess ||
+        hipMemsetAsync(ctx->split_count, 0, kSplitCounts * sizeof(uint32_t), ctx->own) != hipSuccess ||
+        hipStreamSynchronize(ctx->own) != hipSuccess) {
         mx4_destroy(ctx);
         return fail(MX4_ERR_DEVICE, "could not create stream, events or scratch on device %d", device);
     }
@@ -368,6 +379,8 @@ void mx4_destroy(mx4_context* ctx) {
     if (ctx->work) (void)hipFree(ctx->work);
     if (ctx->flags) (void)hipFree(ctx->flags);
     if (ctx->am_partial) (void)hipFree(ctx->am_partial);
+    if (ctx->split_part) (void)hipFree(ctx->split_part);
+    if (ctx->split_count) (void)hipFree(ctx->split_count);
     if (ctx->logits) (void)hipFree(ctx->logits);
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);

@@ -21,7 +21,11 @@
 //    whole kernel), walks 16-row weight tiles with the next ones prefetched,
 //    and reduces its TW partial tiles through LDS;
 //  * loads go through buffer resources: token rows >= M and weight rows >= N
-//    read as zeros without touching memory.
+//    read as zeros without touching memory;
+//  * split K (KS > 1, rows too wide for a workgroup's activations to stay
+//    resident): KS workgroups share a tile, each over one K slice with its
+//    slice's activations resident, and the last of them to finish adds the KS
+//    partial tiles in slice order.
 #include <type_traits>
 
 #include "mx4_device.h"
@@ -95,20 +99,23 @@ __device__ __forceinline__ void split3(const f32x4 a, const f32x4 b, bf16x8& hi,
     }
 }
 
-// Persistent kernel, K = 128 * U * NU * TW exactly. Unit p of wave w of a
-// workgroup is the U adjacent 128-element chunks from (p TW + w) U on, in
-// every weight row. The workgroup walks 16-row weight tiles (tile, tile +
+// Persistent kernel, K = 128 * U * NU * TW * KS exactly. Workgroup b covers
+// K slice b % KS (128 U NU TW elements); unit p of its wave w is the U
+// adjacent 128-element chunks from (p TW + w) U on within the slice, in every
+// weight row. The workgroup walks 16-row weight tiles (tile, tile +
 // grid, ...); each tile is NU units per wave. A unit's weights (16 rows x U
 // blocks per lane group), scales and activation fragments are loaded one unit
 // ahead of the MFMAs, or, with one unit per tile, two tiles ahead. After a
 // tile's last unit the TW partial 16x16 tiles are summed through LDS
 // (double-buffered: one barrier per tile).
-template <bool XBF16, int MT, int U, int NU, int TW, bool RESX>
+template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS>
 __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restrict__ packed,
                                                          const uint8_t* __restrict__ scales,
                                                          const void* __restrict__ x, float* __restrict__ y,
-                                                         uint32_t m, uint32_t n) {
-    constexpr uint32_t k = 128 * U * NU * TW;
+                                                         uint32_t m, uint32_t n, float* __restrict__ part,
+                                                         uint32_t* __restrict__ count) {
+    constexpr uint32_t ks = 128 * U * NU * TW;  // K of one slice
+    constexpr uint32_t k = ks * KS;
     constexpr uint32_t row_bytes = k / 2, nblk = k / 32;
     constexpr int XQ = XBF16 ? 4 : 8;  // 16-byte activation loads per chunk and token tile
     // the wave index is uniform; saying so keeps chunk indices and buffer
@@ -117,6 +124,9 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t col = lane % 16, g = lane / 16;
     const uint32_t tiles = (n + 15) / 16;
+    // the slice's first MX block in a row (KS divides the grid: uniform)
+    const uint32_t slice = KS > 1 ? blockIdx.x % KS : 0u;
+    const uint32_t kb = slice * (ks / 32);
     const __amdgpu_buffer_rsrc_t empty = rsrc(packed, 0);
     const __amdgpu_buffer_rsrc_t xr = rsrc(x, m * k * (XBF16 ? 2u : 4u));
 
@@ -134,7 +144,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
         for (int p = 0; p < NU; ++p)
 #pragma unroll
             for (int q = 0; q < U; ++q) {
-                const uint32_t blk = 4 * ((p * TW + wave) * U + q) + g;
+                const uint32_t blk = kb + 4 * ((p * TW + wave) * U + q) + g;
 #pragma unroll
                 for (int j = 0; j < MT; ++j) {
                     const uint32_t off = ((16 * j + col) * k + 32 * blk) * (XBF16 ? 2u : 4u);
@@ -159,18 +169,18 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
         if constexpr (U == 4) return 64 * i + 16 * j + ((b + 2 * j + (i & 1)) & 15);
         else return 64 * i + 8 * j + ((b + (j & ~1u)) & 7);
     };
-    auto load = [&](uint32_t tile, uint32_t part, Unit& out) {
+    auto load = [&](uint32_t tile, uint32_t unit, Unit& out) {
         const bool valid = tile < tiles;
         const uint32_t row0 = valid ? tile * 16 : 0;
         const uint32_t rows = valid ? (n - row0 < 16u ? n - row0 : 16u) : 0;
         const __amdgpu_buffer_rsrc_t wr = valid ? rsrc(packed + (size_t)row0 * row_bytes, rows * row_bytes) : empty;
         const __amdgpu_buffer_rsrc_t sr = valid ? rsrc(scales + (size_t)row0 * nblk, rows * nblk) : empty;
         const __amdgpu_buffer_rsrc_t xq = valid ? xr : empty;
-        load_scale_run<U>(sr, col * nblk + 4 * (part * TW + wave) * U, out.s);
-        const uint32_t span = 64 * (part * TW + wave) * U;  // the unit's first byte in a row
+        load_scale_run<U>(sr, col * nblk + kb + 4 * (unit * TW + wave) * U, out.s);
+        const uint32_t span = 16 * kb + 64 * (unit * TW + wave) * U;  // the unit's first byte in a row
 #pragma unroll
         for (int q = 0; q < U; ++q) {
-            const uint32_t blk = 4 * ((part * TW + wave) * U + q) + g;
+            const uint32_t blk = kb + 4 * ((unit * TW + wave) * U + q) + g;
             if constexpr (TRANS)
                 out.w[q] = __builtin_amdgcn_raw_buffer_load_b128(wr, (RPL * q + lane / BPR) * row_bytes + span + 16 * (lane % BPR),
                                                                  0, kNT);
@@ -234,23 +244,47 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
 
     __shared__ f32x4 red[2][TW][MT][64];
     uint32_t parity = 0;
+    // Split K: partials are stored and loaded with device scope, so the
+    // per-XCD L2s keep no stale copy of them.
+    constexpr int kDeviceScope = 0x10;
+    auto write_y = [&](uint32_t tile, uint32_t j, const f32x4& sum) {
+        const uint32_t row = tile * 16 + col;
+        if (row < n) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t tok = 16 * j + 4 * g + r;
+                if (tok < m) y[(size_t)tok * n + row] = sum[r];
+            }
+        }
+    };
     auto reduce_write = [&](uint32_t tile) {
 #pragma unroll
         for (int j = 0; j < MT; ++j) red[parity][wave][j][lane] = acc[j];
         __syncthreads();
+        if constexpr (KS > 1) {
+            // wave 0 stores the slice's partial tile, part[tile][slice][j];
+            // the tiles are counted after the tile loop
+            if (wave == 0) {
+                const __amdgpu_buffer_rsrc_t pr = rsrc(part + (size_t)tile * KS * MT * 256, KS * MT * 1024);
+#pragma unroll
+                for (int j = 0; j < MT; ++j) {
+                    f32x4 sum = red[parity][0][j][lane];
+#pragma unroll
+                    for (int w = 1; w < TW; ++w) sum += red[parity][w][j][lane];
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), pr,
+                                                           ((slice * MT + j) * 64 + lane) * 16, 0, kDeviceScope);
+                }
+            }
+            parity ^= 1;
+            zero();
+            return;
+        }
         if (wave < (uint32_t)MT) {
             const uint32_t j = wave;
             f32x4 sum = red[parity][0][j][lane];
 #pragma unroll
             for (int w = 1; w < TW; ++w) sum += red[parity][w][j][lane];
-            const uint32_t row = tile * 16 + col;
-            if (row < n) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t tok = 16 * j + 4 * g + r;
-                    if (tok < m) y[(size_t)tok * n + row] = sum[r];
-                }
-            }
+            write_y(tile, j, sum);
         }
         parity ^= 1;
         zero();
@@ -259,10 +293,10 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     // The units of a tile are unrolled (their index, and so their activation
     // fragments, known at compile time); each unit's weights are loaded while
     // the previous one computes, the next tile's first unit during the last.
-    uint32_t tile = blockIdx.x;
+    uint32_t tile = blockIdx.x / KS;
     if (tile >= tiles) return;
     zero();
-    const uint32_t stride = gridDim.x;  // tiles past the end load zeros and use nothing
+    const uint32_t stride = gridDim.x / KS;  // tiles past the end load zeros and use nothing
     if constexpr (RESX && NU == 1) {
         // A tile is one unit: the next D - 1 tiles' weights are in flight
         // while one computes (D buffers, rotated by unrolling). The compiler's
@@ -320,21 +354,73 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
             tile = next;
         }
     }
+    if constexpr (KS > 1) {
+        // Wave 0 counts its tiles once all its partial stores are complete
+        // (one drain per workgroup, not per tile: stores and loads share one
+        // in-order counter). Lane i counts the workgroup's i-th tile; the
+        // last of a tile's KS workgroups to count it reads the KS partials
+        // (after the count's return), adds them in slice order, writes y and
+        // re-arms the count for the next launch. No wave waits for another
+        // workgroup.
+        if (wave != 0) return;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const uint32_t first = blockIdx.x / KS;
+        const uint32_t mine = (tiles - first + stride - 1) / stride;  // <= 64, checked at launch
+        uint32_t before = 0;
+        if (lane < mine)
+            before = __hip_atomic_fetch_add(count + first + lane * stride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t last = __ballot(lane < mine && before == KS - 1);
+        asm volatile("" ::: "memory");
+        for (uint32_t i = 0; i < mine; ++i) {
+            if (!((last >> i) & 1)) continue;
+            const uint32_t t = first + i * stride;
+            const __amdgpu_buffer_rsrc_t pr = rsrc(part + (size_t)t * KS * MT * 256, KS * MT * 1024);
+            u32x4 v[KS][MT];
+#pragma unroll
+            for (int s2 = 0; s2 < KS; ++s2)
+#pragma unroll
+                for (int j = 0; j < MT; ++j)
+                    v[s2][j] = __builtin_amdgcn_raw_buffer_load_b128(pr, ((s2 * MT + j) * 64 + lane) * 16, 0, kDeviceScope);
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+                f32x4 sum = __builtin_bit_cast(f32x4, v[0][j]);
+#pragma unroll
+                for (int s2 = 1; s2 < KS; ++s2) sum += __builtin_bit_cast(f32x4, v[s2][j]);
+                write_y(t, j, sum);
+            }
+            if (lane == 0) __hip_atomic_store(count + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
-template <bool XBF16, int MT, int U, int NU, int TW, bool RESX>
-hipError_t go(const GemvArgs& a, int cus) {
+template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS = 1>
+hipError_t go(const GemvArgs& a, int cus, const SkinnyScratch& sc = {}) {
     const uint32_t tiles = (a.n + 15) / 16;
     // two workgroups of TW waves per CU; with one unit per tile, eight waves
     // per CU (two per SIMD: the three buffers need more than the 128 VGPRs of
-    // four waves per SIMD)
-    uint32_t grid = (uint32_t)cus * ((RESX && NU == 1) ? 8u / TW : 2u);
+    // four waves per SIMD). With split K, one workgroup per CU and KS of them
+    // per tile: consecutive workgroups take the KS slices of one tile, so each
+    // XCD (every eighth workgroup) keeps one slice of the activations in its L2.
+    uint32_t grid = KS > 1 ? (uint32_t)cus / KS : (uint32_t)cus * ((RESX && NU == 1) ? 8u / TW : 2u);
     if (grid > tiles) grid = tiles;
+    if (grid == 0) grid = 1;
     const uint32_t per = (tiles + grid - 1) / grid;
     grid = (tiles + per - 1) / per;
-    hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX>), dim3(grid), dim3(64 * TW), 0, a.stream, a.packed,
-                       a.scales, a.x, a.y, a.m, a.n);
+    hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX, KS>), dim3(grid * KS), dim3(64 * TW), 0, a.stream,
+                       a.packed, a.scales, a.x, a.y, a.m, a.n, sc.part, sc.count);
     return hipGetLastError();
+}
+
+// Split K needs KS * MT partial tiles and one count per 16-row tile, and
+// counts a workgroup's tiles with one lane each (at most 64 tiles per
+// workgroup; the launch puts cus / KS workgroups on each slice).
+bool split_fits(const GemvArgs& a, int cus, const SkinnyScratch& sc, uint32_t ks, uint32_t mt) {
+    const uint64_t tiles = (a.n + 15) / 16;
+    uint64_t grid = (uint64_t)cus / ks;
+    if (grid > tiles) grid = tiles;
+    if (grid == 0) grid = 1;
+    return sc.part && sc.count && tiles * ks * mt <= sc.part_tiles && tiles <= sc.count_tiles &&
+           (tiles + grid - 1) / grid <= 64;
 }
 
 // The three-tile ring (bf16 activations, K 2048 or 4096) pays from two tiles
@@ -354,7 +440,7 @@ bool tile_ring(const GemvArgs& a, int cus) {
 // with fewer tiles (each workgroup one tile or two) keep two units per tile,
 // which measured 0.3-0.8 us faster there.
 template <bool XBF16, int MT>
-hipError_t go_k(const GemvArgs& a, int cus) {
+hipError_t go_k(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
     constexpr int U = (XBF16 && MT == 1) ? 2 : 1;
     constexpr int TW = 8;
     // bf16 activations of up to 16 tokens stay resident in registers for K up
@@ -373,7 +459,22 @@ hipError_t go_k(const GemvArgs& a, int cus) {
         // wider rows keep the per-tile activation loads: resident in registers
         // they need 16 or 12 waves per workgroup and measured slower (down)
         case 8192: return go<XBF16, MT, U, 8 / U, TW, false>(a, cus);
-        case 12288: return go<XBF16, MT, U, 12 / U, TW, false>(a, cus);
+        case 12288:
+            // bf16 x from 8 tokens on: four workgroups per tile, each over a
+            // 3072-wide K slice with its activations resident and the
+            // three-tile ring, so that every workgroup reads a quarter of x
+            // instead of all of it. 8B down at 8 / 12 / 16 / 24 / 32 tokens:
+            // 11.8 / 14.2 / 16.5 / 26.8 / 32.7 -> 11.6 / 12.1 / 12.5 / 15.5 /
+            // 16.6 us (12 waves of two chunks for one token tile, 6 waves of
+            // four for two; three-chunk units, with half-line loads, measured
+            // 0.8-1.4 us slower). Below 8 tokens the end-of-launch count costs
+            // more than the activation loads it saves.
+            if constexpr (XBF16)
+                if (a.m >= 8 && split_fits(a, cus, sc, 4, MT)) {
+                    if constexpr (MT == 1) return go<XBF16, 1, 2, 1, 12, true, 4>(a, cus, sc);
+                    else return go<XBF16, MT, 4, 1, 6, true, 4>(a, cus, sc);
+                }
+            return go<XBF16, MT, U, 12 / U, TW, false>(a, cus);
         default: return hipErrorNotSupported;
     }
 }
@@ -392,11 +493,11 @@ bool skinny_supported(uint32_t m, uint32_t k) {
 // per launch cannot afford in registers (lm_head at 17-32 tokens: 256-357 us
 // in one launch, 115-125 in two; gate 29-40 -> 18-20 us). Shorter weights
 // measured faster in one launch with two token tiles.
-hipError_t launch_skinny(const GemvArgs& a, int cus) {
+hipError_t launch_skinny(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
     if (!skinny_supported(a.m, a.k)) return hipErrorNotSupported;
-    auto one = [&](const GemvArgs& b) { return b.x_bf16 ? go_k<true, 1>(b, cus) : go_k<false, 1>(b, cus); };
+    auto one = [&](const GemvArgs& b) { return b.x_bf16 ? go_k<true, 1>(b, cus, sc) : go_k<false, 1>(b, cus, sc); };
     if (a.m <= 16) return one(a);
-    if (!tile_ring(a, cus)) return a.x_bf16 ? go_k<true, 2>(a, cus) : go_k<false, 2>(a, cus);
+    if (!tile_ring(a, cus)) return a.x_bf16 ? go_k<true, 2>(a, cus, sc) : go_k<false, 2>(a, cus, sc);
     GemvArgs lo = a, hi = a;
     lo.m = 16;
     hi.m = a.m - 16;

@@ -759,6 +759,39 @@ def test_skinny_tile_ring(mx4, ctx, oracle, n, k):
         assert_close(y[:, rows], ref, f"ring {k}->{n} m={m}")
 
 
+@pytest.mark.parametrize("n", [4096 + 5, 8192 + 37])
+def test_skinny_split_k(mx4, ctx, oracle, n):
+    """K = 12288 with bf16 activations from 8 tokens on: four workgroups per
+    16-row tile, each over a quarter of K, the last to finish adding the four
+    partials (fewer tokens run unsplit, on the same weights). One-hot
+    activations return every decoded weight row bit for bit (a tile whose sum
+    went missing would show), random activations match the oracle on sampled
+    rows, a repeated call is bit-identical (the arrival counts are re-armed),
+    and 17-32 tokens on 8229 rows (more partial tiles than the context's
+    scratch holds) run unsplit with the same results."""
+    k = 12288
+    say(f"skinny split K {k}->{n}")
+    rng = np.random.default_rng(n)
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(112, 136, (n, k // 32), dtype=np.uint8)
+    w = ctx.upload_weight(packed, scales, n, k)
+    dec = oracle.dequantize(packed, scales)
+    for m in (1, 8, 16, 17, 32):
+        cols = rng.choice(k, m, replace=False)
+        x = np.zeros((m, k), np.float32)
+        x[np.arange(m), cols] = 1.0
+        y = run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.BF16)
+        assert np.array_equal(y, dec[:, cols].T), f"identity m={m}"
+    rows = _sample_rows(n, 128, rng)
+    for m in (5, 12, 29):
+        x = oracle.bf16_to_f32(oracle.synth_bf16(1700 + m, 1.0, m * k)).reshape(m, k)
+        ref = np.concatenate([oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), int(r), int(r) + 1)
+                              for r in rows], axis=1)
+        y = run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.BF16)
+        assert_close(y[:, rows], ref, f"split K {k}->{n} m={m}")
+        assert np.array_equal(run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.BF16), y), f"repeat m={m}"
+
+
 def test_skinny_ragged_rows_and_identity(mx4, ctx, oracle):
     """Weight rows not a multiple of the 16-row tile, and an exact identity KAT:
     one-hot activations return the decoded weights bit for bit."""
