@@ -453,6 +453,17 @@ hipError_t go_k(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
             return go<XBF16, MT, U, 16 / (U * 4), 4, R>(a, cus);
         case 4096:
             if constexpr (R) if (ring) return go<XBF16, MT, 4, 1, TW, R>(a, cus);
+            // 17-32 bf16 tokens: split K, four ways (4-wave workgroups) when
+            // that gives each CU one tile, else two ways (8 waves) from 20
+            // tokens on, two chunks per wave, activations resident. 8B k at
+            // 17 / 24 / 32 tokens: 8.6 / 10.0 / 11.7 -> 6.0 / 6.3 / 6.5 us; q at
+            // 24 / 32: 10.4 / 12.0 -> 9.7 / 10.3 us (at 17 it measured
+            // 0.1-0.4 us slower than unsplit)
+            if constexpr (XBF16 && MT == 2) {
+                if (4 * ((a.n + 15) / 16) <= (uint32_t)cus && split_fits(a, cus, sc, 4, MT))
+                    return go<XBF16, MT, 2, 1, 4, true, 4>(a, cus, sc);
+                if (a.m >= 20 && split_fits(a, cus, sc, 2, MT)) return go<XBF16, MT, 2, 1, 8, true, 2>(a, cus, sc);
+            }
             return go<XBF16, MT, U, 4 / U, TW, R>(a, cus);
         case 6144:  // (a one-unit tile of 6 chunks would spill)
             return go<XBF16, MT, R ? 3 : U, R ? 2 : 6 / U, TW, R>(a, cus);

@@ -759,17 +759,19 @@ def test_skinny_tile_ring(mx4, ctx, oracle, n, k):
         assert_close(y[:, rows], ref, f"ring {k}->{n} m={m}")
 
 
-@pytest.mark.parametrize("n", [4096 + 5, 8192 + 37])
-def test_skinny_split_k(mx4, ctx, oracle, n):
-    """K = 12288 with bf16 activations from 8 tokens on: four workgroups per
-    16-row tile, each over a quarter of K, the last to finish adding the four
-    partials (fewer tokens run unsplit, on the same weights). One-hot
+@pytest.mark.parametrize("n,k", [(4096 + 5, 12288), (8192 + 37, 12288), (1024 - 5, 4096), (4096 + 5, 4096)])
+def test_skinny_split_k(mx4, ctx, oracle, n, k):
+    """Split K with bf16 activations: K = 12288 from 8 tokens on (four
+    workgroups per 16-row tile, each over a quarter of K), K = 4096 from 17 on
+    (four slices when every CU gets one tile, as for 1019 rows, else two from
+    20 tokens on); the
+    last workgroup of a tile adds the partials (fewer tokens run unsplit, on the
+    same weights). One-hot
     activations return every decoded weight row bit for bit (a tile whose sum
     went missing would show), random activations match the oracle on sampled
     rows, a repeated call is bit-identical (the arrival counts are re-armed),
-    and 17-32 tokens on 8229 rows (more partial tiles than the context's
+    and 17-32 tokens on 8229 x 12288 (more partial tiles than the context's
     scratch holds) run unsplit with the same results."""
-    k = 12288
     say(f"skinny split K {k}->{n}")
     rng = np.random.default_rng(n)
     packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
