@@ -503,12 +503,17 @@ bool skinny_supported(uint32_t m, uint32_t k) {
 // activations resident and streams through the ring, which two token tiles
 // per launch cannot afford in registers (lm_head at 17-32 tokens: 256-357 us
 // in one launch, 115-125 in two; gate 29-40 -> 18-20 us). Shorter weights
-// measured faster in one launch with two token tiles.
+// measured faster in one launch with two token tiles. From 20 tokens on at
+// K = 4096, one split-K launch beats the two where its partials fit (8B gate
+// at 20 / 32 tokens: 18.3 / 20.2 -> 16.1 / 16.9 us).
 hipError_t launch_skinny(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
     if (!skinny_supported(a.m, a.k)) return hipErrorNotSupported;
     auto one = [&](const GemvArgs& b) { return b.x_bf16 ? go_k<true, 1>(b, cus, sc) : go_k<false, 1>(b, cus, sc); };
     if (a.m <= 16) return one(a);
     if (!tile_ring(a, cus)) return a.x_bf16 ? go_k<true, 2>(a, cus, sc) : go_k<false, 2>(a, cus, sc);
+    // K = 4096 from 20 tokens on, when the partial tiles fit (8B gate/up, not
+    // the lm_head): one two-way split-K launch reads the weights once
+    if (a.x_bf16 && a.k == 4096 && a.m >= 20 && split_fits(a, cus, sc, 2, 2)) return go_k<true, 2>(a, cus, sc);
     GemvArgs lo = a, hi = a;
     lo.m = 16;
     hi.m = a.m - 16;
