@@ -99,7 +99,11 @@ void qwen_hip_set_cache_limit(void *context, uint64_t bytes);
  * ------------------------------------------------------------------------ */
 
 /* gpu_create (engine/src/gpu.m:27-49): binds HIP device `device` and creates
- * the context's stream (default priority). */
+ * the context's stream (default priority) and its device scratch (argmax
+ * partials, and 4 MiB of split-K partial tiles with their arrival counts).
+ * The scratch is shared by every call on the context, so calls on one context
+ * must stay ordered: after mx4_set_stream, work still queued on the previous
+ * stream must finish before the new stream runs more. */
 mx4_status mx4_create(int device, mx4_context **out);
 void mx4_destroy(mx4_context *ctx);
 const char *mx4_last_error(void);
