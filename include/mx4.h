@@ -218,7 +218,15 @@ mx4_status mx4_matmul_batch(mx4_context *ctx, const mx4_op *ops, uint32_t count)
  * mx4_pass_begin and mx4_pass_end is captured into a HIP graph and replayed by
  * mx4_pass_launch -- the analogue of the reference's one command buffer per
  * forward pass (engine/src/gpu.rs:157, engine/src/gpu.m:87-128). No device
- * memory is allocated or freed while recording. */
+ * memory is allocated or freed while recording.
+ *
+ * A pass keeps raw device pointers: the caller's buffers and weights it
+ * names must outlive it, and so does the context (launching a pass on another
+ * or a destroyed context fails). The context's own workspace (prefill
+ * requantization, argmax logits) may still grow after recording, through a
+ * larger eager call: while any pass of the context is alive the old buffer is
+ * kept and freed only when the last pass is released, so replays stay valid.
+ * mx4_pass_release waits for the context stream first. */
 typedef struct mx4_pass mx4_pass;
 mx4_status mx4_pass_begin(mx4_context *ctx);
 mx4_status mx4_pass_end(mx4_context *ctx, mx4_pass **out);

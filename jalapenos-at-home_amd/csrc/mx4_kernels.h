@@ -55,12 +55,14 @@ hipError_t launch_gemv_m1_argmax(const GemvArgs& a, uint64_t* partial, uint32_t 
 hipError_t launch_embed(const uint8_t* packed, const uint8_t* scales, const uint16_t* bf16, const uint32_t* ids,
                         uint32_t count, uint32_t rows, uint32_t cols, uint16_t* out, hipStream_t s);
 
-// Exact skinny path (2 <= m <= 16) on bf16 MFMA with decoded weights.
+// Exact skinny path (1 <= m <= 32) on bf16 MFMA with decoded weights.
 bool skinny_supported(uint32_t m, uint32_t k);
-// Device scratch of the split-K launches (K = 12288): part_tiles partial tiles
-// of 1 KiB and count_tiles arrival counts, which must be zero before the first
-// launch and are left at zero by every launch. Launches that share it must be
-// ordered (one stream). With no scratch, or too little, the kernel runs unsplit.
+// Device scratch of the split-K launches (bf16 x; K = 12288 from 8 tokens,
+// K = 4096 from 17 tokens on 1024-row weights and from 20 tokens on wider
+// ones, when the partial tiles fit): part_tiles partial tiles of 1 KiB and
+// count_tiles arrival counts, which must be zero before the first launch and
+// are left at zero by every launch. Launches that share it must be ordered
+// (one stream). With no scratch, or too little, the kernel runs unsplit.
 struct SkinnyScratch {
     float* part = nullptr;
     uint32_t* count = nullptr;

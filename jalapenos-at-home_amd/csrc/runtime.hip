@@ -13,6 +13,8 @@
 #include <list>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
+#include <vector>
 
 #include "mx4.h"
 #include "mx4_kernels.h"
@@ -78,6 +80,7 @@ struct mx4_pass {
     hipGraph_t graph;
     hipGraphExec_t exec;
     int device;
+    mx4_context* ctx;  // null once the context is destroyed
 };
 
 struct CacheEntry {
@@ -114,6 +117,11 @@ struct mx4_context {
     // arrival counts (zero between launches); calls are ordered on `stream`
     float* split_part = nullptr;
     uint32_t* split_count = nullptr;
+    // recorded passes alive on this context: a pass holds raw pointers to
+    // `work` and `logits`, so while any is alive a buffer that has to grow
+    // is retired (freed when the last pass is released) instead of freed
+    std::unordered_set<mx4_pass*> passes;
+    std::vector<void*> retired;
 };
 
 constexpr uint32_t kArgmaxPartials = 8192;
@@ -144,7 +152,11 @@ bool is_gfx950(int dev) {
     return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
 }
 
-mx4_status ensure_buffer(mx4_context* ctx, void** buf, uint64_t* cap, uint64_t need) {
+// Grow a context buffer to `need` bytes. A buffer that recorded passes may
+// read (`pass_visible`: the prefill workspace, the argmax logits) is kept
+// alive until every pass of the context is released, so replaying an older
+// pass never touches freed memory.
+mx4_status ensure_buffer(mx4_context* ctx, void** buf, uint64_t* cap, uint64_t need, bool pass_visible = false) {
     if (need <= *cap) return MX4_OK;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
@@ -153,7 +165,11 @@ mx4_status ensure_buffer(mx4_context* ctx, void** buf, uint64_t* cap, uint64_t n
                     (unsigned long long)need);
     if (*buf) {
         HIP_TRY(hipStreamSynchronize(ctx->stream));
-        HIP_TRY(hipFree(*buf));
+        if (pass_visible && !ctx->passes.empty()) {
+            ctx->retired.push_back(*buf);
+        } else {
+            HIP_TRY(hipFree(*buf));
+        }
         *buf = nullptr;
         *cap = 0;
     }
@@ -374,6 +390,8 @@ void mx4_destroy(mx4_context* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (auto& kv : ctx->cache) mx4_weight_release(kv.second.w);
     ctx->cache.clear();
+    for (mx4_pass* p : ctx->passes) p->ctx = nullptr;
+    for (void* b : ctx->retired) (void)hipFree(b);
     if (ctx->x_stage) (void)hipFree(ctx->x_stage);
     if (ctx->y_stage) (void)hipFree(ctx->y_stage);
     if (ctx->work) (void)hipFree(ctx->work);
@@ -689,7 +707,7 @@ mx4_status mx4_matmul_prefill(mx4_context* ctx, const void* x, mx4_dtype xt, uin
     st = prepare_fragments(ctx, wm);
     if (st != MX4_OK) return st;
     const uint64_t qoff = (mx4::fragment_bytes(m, w->cols, fp8) + 255) & ~255ull;
-    st = ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(m, w->cols, fp8));
+    st = ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(m, w->cols, fp8), true);
     if (st != MX4_OK) return st;
     uint8_t* xf = static_cast<uint8_t*>(ctx->work);
     uint8_t* xsf = xf + qoff;
@@ -734,19 +752,20 @@ mx4_status mx4_pass_end(mx4_context* ctx, mx4_pass** out) {
         (void)hipGraphDestroy(graph);
         return fail(MX4_ERR_DEVICE, "graph instantiate failed: %s", hipGetErrorString(e));
     }
-    mx4_pass* p = new (std::nothrow) mx4_pass{graph, exec, ctx->device};
+    mx4_pass* p = new (std::nothrow) mx4_pass{graph, exec, ctx->device, ctx};
     if (!p) {
         (void)hipGraphExecDestroy(exec);
         (void)hipGraphDestroy(graph);
         return fail(MX4_ERR_NO_MEMORY, "out of host memory");
     }
+    ctx->passes.insert(p);
     *out = p;
     return MX4_OK;
 }
 
 mx4_status mx4_pass_launch(mx4_context* ctx, const mx4_pass* pass) {
     if (!ctx || !pass) return fail(MX4_ERR_ARGUMENT, "null argument");
-    if (pass->device != ctx->device) return fail(MX4_ERR_ARGUMENT, "pass recorded on another device");
+    if (pass->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "pass recorded on another context");
     DeviceGuard g(ctx->device);
     HIP_TRY(hipGraphLaunch(pass->exec, ctx->stream));
     return MX4_OK;
@@ -755,15 +774,24 @@ mx4_status mx4_pass_launch(mx4_context* ctx, const mx4_pass* pass) {
 void mx4_pass_release(mx4_pass* pass) {
     if (!pass) return;
     DeviceGuard g(pass->device);
+    mx4_context* ctx = pass->ctx;
+    if (ctx) (void)hipStreamSynchronize(ctx->stream);  // a replay may still run
     (void)hipGraphExecDestroy(pass->exec);
     (void)hipGraphDestroy(pass->graph);
+    if (ctx) {
+        ctx->passes.erase(pass);
+        if (ctx->passes.empty()) {
+            for (void* b : ctx->retired) (void)hipFree(b);
+            ctx->retired.clear();
+        }
+    }
     delete pass;
 }
 
 mx4_status mx4_reserve_prefill(mx4_context* ctx, uint32_t max_m, uint32_t max_cols) {
     if (!ctx) return fail(MX4_ERR_ARGUMENT, "null context");
     DeviceGuard g(ctx->device);
-    return ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(max_m, max_cols, true));
+    return ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(max_m, max_cols, true), true);
 }
 
 mx4_status mx4_matmul_mx(mx4_context* ctx, const uint8_t* xq, const uint8_t* xs, mx4_act_format act, uint32_t m,
@@ -781,7 +809,7 @@ mx4_status mx4_matmul_mx(mx4_context* ctx, const uint8_t* xq, const uint8_t* xs,
     mx4_status st = prepare_fragments(ctx, wm);
     if (st != MX4_OK) return st;
     const uint64_t qoff = (mx4::fragment_bytes(m, w->cols, fp8) + 255) & ~255ull;
-    st = ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(m, w->cols, fp8));
+    st = ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(m, w->cols, fp8), true);
     if (st != MX4_OK) return st;
     uint8_t* xf = static_cast<uint8_t*>(ctx->work);
     uint8_t* xsf = xf + qoff;
@@ -917,7 +945,7 @@ mx4_status mx4_matmul_prefill_group(mx4_context* ctx, const void* x, mx4_dtype x
         if (st != MX4_OK) return st;
     }
     const uint64_t qoff = (mx4::fragment_bytes(m, cols, fp8) + 255) & ~255ull;
-    mx4_status st = ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(m, cols, fp8));
+    mx4_status st = ensure_buffer(ctx, &ctx->work, &ctx->work_cap, prefill_workspace_bytes(m, cols, fp8), true);
     if (st != MX4_OK) return st;
     uint8_t* xf = static_cast<uint8_t*>(ctx->work);
     uint8_t* xsf = xf + qoff;
@@ -943,7 +971,7 @@ mx4_status mx4_matmul_argmax(mx4_context* ctx, const void* x, mx4_dtype xt, cons
     // no fused instance for this shape: the projection, then the argmax kernel
     float* logits = y;
     if (!logits) {
-        mx4_status st = ensure_buffer(ctx, &ctx->logits, &ctx->logits_cap, (uint64_t)w->rows * 4);
+        mx4_status st = ensure_buffer(ctx, &ctx->logits, &ctx->logits_cap, (uint64_t)w->rows * 4, true);
         if (st != MX4_OK) return st;
         logits = static_cast<float*>(ctx->logits);
     }

@@ -244,8 +244,8 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
 
     __shared__ f32x4 red[2][TW][MT][64];
     uint32_t parity = 0;
-    // Split K: partials are stored and loaded with device scope, so the
-    // per-XCD L2s keep no stale copy of them.
+    // Split K: partials are stored and loaded with device scope (SC1), so
+    // they are not kept in the per-XCD L2s; the fences below order them.
     constexpr int kDeviceScope = 0x10;
     auto write_y = [&](uint32_t tile, uint32_t j, const f32x4& sum) {
         const uint32_t row = tile * 16 + col;
@@ -355,22 +355,28 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
         }
     }
     if constexpr (KS > 1) {
-        // Wave 0 counts its tiles once all its partial stores are complete
-        // (one drain per workgroup, not per tile: stores and loads share one
-        // in-order counter). Lane i counts the workgroup's i-th tile; the
-        // last of a tile's KS workgroups to count it reads the KS partials
-        // (after the count's return), adds them in slice order, writes y and
-        // re-arms the count for the next launch. No wave waits for another
-        // workgroup.
+        // Wave 0 counts its tiles once, after its last partial store (one
+        // release per workgroup, not per tile). Lane i counts the workgroup's
+        // i-th tile; the last of a tile's KS workgroups to count it reads the
+        // KS partials, adds them in slice order, writes y and re-arms the
+        // count for the next launch. No wave waits for another workgroup.
+        //
+        // Ordering (HIP memory model, agent scope): the release fence makes
+        // this wave's partial stores visible device-wide before its counts
+        // increment; a wave that reads KS - 1 from a count runs an acquire
+        // fence before it loads the partials, so it sees every slice's
+        // stores. Only a workgroup that finishes some tile pays the acquire
+        // (on gfx950 it invalidates this XCD's L2; the release writes back
+        // the L2's dirty lines): together about 2 us per launch.
         if (wave != 0) return;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         const uint32_t first = blockIdx.x / KS;
         const uint32_t mine = (tiles - first + stride - 1) / stride;  // <= 64, checked at launch
         uint32_t before = 0;
         if (lane < mine)
             before = __hip_atomic_fetch_add(count + first + lane * stride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const uint64_t last = __ballot(lane < mine && before == KS - 1);
-        asm volatile("" ::: "memory");
+        if (last != 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         for (uint32_t i = 0; i < mine; ++i) {
             if (!((last >> i) & 1)) continue;
             const uint32_t t = first + i * stride;
@@ -454,15 +460,18 @@ hipError_t go_k(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
         case 4096:
             if constexpr (R) if (ring) return go<XBF16, MT, 4, 1, TW, R>(a, cus);
             // 17-32 bf16 tokens: split K, four ways (4-wave workgroups) when
-            // that gives each CU one tile, else two ways (8 waves) from 20
-            // tokens on, two chunks per wave, activations resident. 8B k at
-            // 17 / 24 / 32 tokens: 8.6 / 10.0 / 11.7 -> 6.0 / 6.3 / 6.5 us; q at
-            // 24 / 32: 10.4 / 12.0 -> 9.7 / 10.3 us (at 17 it measured
-            // 0.1-0.4 us slower than unsplit)
+            // that gives each CU one tile, two chunks per wave, activations
+            // resident: 8B k at 32 tokens 11.7 -> 9.1 us (6.5 us before the
+            // agent-scope fences of the arrival count, which cost about 2 us
+            // per launch). Two ways (8 waves) from 20 tokens on only for the
+            // ring-length weights that launch_skinny sends here (gate/up): on
+            // q/o the fenced split measured slower than unsplit (12.9 against
+            // 12.0 us at 32 tokens).
             if constexpr (XBF16 && MT == 2) {
                 if (4 * ((a.n + 15) / 16) <= (uint32_t)cus && split_fits(a, cus, sc, 4, MT))
                     return go<XBF16, MT, 2, 1, 4, true, 4>(a, cus, sc);
-                if (a.m >= 20 && split_fits(a, cus, sc, 2, MT)) return go<XBF16, MT, 2, 1, 8, true, 2>(a, cus, sc);
+                if (a.m >= 20 && tile_ring(a, cus) && split_fits(a, cus, sc, 2, MT))
+                    return go<XBF16, MT, 2, 1, 8, true, 2>(a, cus, sc);
             }
             return go<XBF16, MT, U, 4 / U, TW, R>(a, cus);
         case 6144:  // (a one-unit tile of 6 chunks would spill)
@@ -475,13 +484,15 @@ hipError_t go_k(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
             // 3072-wide K slice with its activations resident and the
             // three-tile ring, so that every workgroup reads a quarter of x
             // instead of all of it. 8B down at 8 / 12 / 16 / 24 / 32 tokens:
-            // 11.8 / 14.2 / 16.5 / 26.8 / 32.7 -> 11.6 / 12.1 / 12.5 / 15.5 /
-            // 16.6 us (12 waves of two chunks for one token tile, 6 waves of
-            // four for two; three-chunk units, with half-line loads, measured
-            // 0.8-1.4 us slower). Below 8 tokens the end-of-launch count costs
-            // more than the activation loads it saves.
+            // 11.8 / 14.2 / 16.5 / 26.8 / 32.7 unsplit; split, with the
+            // agent-scope fences of the arrival count (about 2 us per
+            // launch), 13.5 at 8 and 14.3 / 18.6 at 16 / 32 (12 waves of two
+            // chunks for one token tile, 6 waves of four for two;
+            // three-chunk units, with half-line loads, measured 0.8-1.4 us
+            // slower). Below 12 tokens the end-of-launch count and fences
+            // cost more than the activation loads they save.
             if constexpr (XBF16)
-                if (a.m >= 8 && split_fits(a, cus, sc, 4, MT)) {
+                if (a.m >= 12 && split_fits(a, cus, sc, 4, MT)) {
                     if constexpr (MT == 1) return go<XBF16, 1, 2, 1, 12, true, 4>(a, cus, sc);
                     else return go<XBF16, MT, 4, 1, 6, true, 4>(a, cus, sc);
                 }

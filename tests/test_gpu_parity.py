@@ -1,9 +1,15 @@
 """GPU parity: the HIP kernels, called through the C ABI, against the CPU oracle.
 
-Bars: bit-exact for decode, quantize, requantize, the generator and argmax;
-max_i |y_i - r_i| / max_i |r_i| <= 1e-3 for matmuls against the oracle r
-(engine/src/lib.rs:240-266), plus the reference's own per-element bound
-|a - b| < 1e-3 + 1e-5 |b| (engine/src/metal.rs:110). Observed errors are ~1e-6.
+Bars: bit-exact for decode, quantize, requantize, the generator and argmax.
+Matmuls against the oracle r (engine/src/lib.rs:240-266), all three at once:
+  * max_i |y_i - r_i| / max_i |r_i| <= 1e-3 (the BASELINE tolerance);
+  * the reference's own per-element bound |y - r| < 1e-3 + 1e-5 |r|
+    (engine/src/metal.rs:110) on the raw values; only tests whose weights use
+    deliberately large scale bytes (outputs of 1e2..1e5) apply it to values
+    divided by max |r|, and say so at the call (scaled=True);
+  * ||y - r||_2 / ||r||_2 <= 1e-5, the reference's normwise form
+    (engine/tests/mxfp4.rs:76-84). Every path here multiplies exactly and sums
+    in f32, so only the summation order differs from the oracle (~1e-6).
 """
 import json
 import sys
@@ -54,14 +60,31 @@ def max_rel(y, r):
     return float(np.max(np.abs(y.astype(np.float64) - r.astype(np.float64)))) / (denom if denom else 1.0)
 
 
-def assert_close(y, r, what):
+RMS_TOL = 1e-5
+
+
+def rel_rms(y, r):
+    d = y.astype(np.float64) - r.astype(np.float64)
+    den = float(np.sqrt(np.sum(r.astype(np.float64) ** 2)))
+    return float(np.sqrt(np.sum(d * d))) / (den if den else 1.0)
+
+
+def assert_close(y, r, what, scaled=False):
+    """The three bars of the module docstring. scaled=True divides both sides
+    by max |r| before the per-element bound (large-scale test weights only)."""
+    y = np.asarray(y, np.float32)
+    r = np.asarray(r, np.float32)
+    assert y.shape == r.shape, f"{what}: shape {y.shape} != {r.shape}"
     rel = max_rel(y, r)
     assert rel <= REL_TOL, f"{what}: max rel err {rel:.3e}"
-    ok = np.abs(y - r) < 1e-3 + 1e-5 * np.abs(r)
-    if not np.all(ok):
-        # the absolute form assumes O(1) outputs; apply it to the normalised values
-        scale = max(float(np.max(np.abs(r))), 1.0)
-        assert np.all(np.abs(y - r) / scale < 1e-3 + 1e-5 * np.abs(r) / scale), what
+    yy, rr = y.astype(np.float64), r.astype(np.float64)
+    if scaled:
+        s = max(float(np.max(np.abs(rr))), 1.0)
+        yy, rr = yy / s, rr / s
+    bad = ~(np.abs(yy - rr) < 1e-3 + 1e-5 * np.abs(rr))
+    assert not np.any(bad), f"{what}: {int(bad.sum())} elements outside |a-b| < 1e-3 + 1e-5|b|"
+    rms = rel_rms(y, r)
+    assert rms <= RMS_TOL, f"{what}: relative RMS error {rms:.3e}"
     return rel
 
 
@@ -364,6 +387,70 @@ def test_lm_head_greedy_argmax_identical(mx4, ctx, oracle):
         assert np.array_equal(y2.download(np.float32).reshape(1, n), y)
 
 
+def test_lm_head_8b_greedy_argmax_identical(mx4, ctx, oracle):
+    """The Qwen3-8B lm_head (4096 -> 151936) at M = 1 against the full oracle
+    logits, three activation seeds: the logits within the bars, and the greedy
+    pick (engine/src/model.rs:228-238 then :288-296) identical through the
+    projection + mx4_argmax_rows and through the fused mx4_matmul_argmax, with
+    and without writing the logits (its one-wave lm_head instance, whose
+    logits are checked against the oracle too)."""
+    n, k = QWEN8["lm_head"]
+    w = ctx.synth_weight(8, n, k, 0.02)
+    packed, scales = ctx.download_weight(w)
+    idx = ctx.buffer(4 * 4)
+    for seed in (1, 2, 3):
+        say(f"lm_head 8B argmax 4096->151936, full oracle, x seed {seed}")
+        x = oracle.bf16_to_f32(oracle.synth_bf16(seed, 1.0, k)).reshape(1, k)
+        ref = oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), 0, n, threads=16)
+        want = oracle.argmax(ref[0])
+        xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+        yb = ctx.buffer(n * 4)
+        ctx.matmul(xb, mx4.BF16, 1, w, yb)
+        idx.upload(np.full(4, 0xFFFFFFFF, np.uint32))
+        ctx.argmax_rows(yb, 1, n, idx)
+        y = yb.download(np.float32).reshape(1, n)
+        assert_close(y, ref, f"8B lm_head seed {seed}")
+        assert int(idx.download(np.uint32, 1)[0]) == want
+        assert oracle.argmax(y[0]) == want
+        y2 = ctx.buffer(n * 4)
+        for yy in (y2, None):
+            idx.upload(np.full(4, 0xFFFFFFFF, np.uint32))
+            ctx.matmul_argmax(xb, mx4.BF16, w, yy, idx)
+            assert int(idx.download(np.uint32, 1)[0]) == want, f"fused, logits {'written' if yy else 'not written'}"
+        # the fused instance (one-wave teams) sums in another order than the
+        # projection's default (two-wave teams split K): equal within the bars
+        assert_close(y2.download(np.float32).reshape(1, n), ref, f"8B lm_head fused logits seed {seed}")
+    w.release()
+
+
+def test_lm_head_8b_verify_rows(mx4, ctx, oracle):
+    """Speculative verify on the Qwen3-8B lm_head (engine/src/gpu.rs:614-626:
+    lm_head over the draft + 1 token rows, then argmax_rows): AUTO at M = 2, 4,
+    8, 16 and 32 token rows (few-token GEMV, skinny kernel with the three-tile
+    ring, the two-launch split above 16 rows) against the full oracle logits;
+    mx4_argmax_rows over the M rows gives the oracle's pick for every row."""
+    n, k = QWEN8["lm_head"]
+    mmax = 32
+    w = ctx.synth_weight(9, n, k, 0.02)
+    packed, scales = ctx.download_weight(w)
+    x = oracle.bf16_to_f32(oracle.synth_bf16(19, 1.0, mmax * k)).reshape(mmax, k)
+    say("lm_head 8B verify rows: full oracle logits for 32 token rows")
+    ref = oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), 0, n, threads=16)
+    want = np.array([oracle.argmax(r) for r in ref], np.uint32)
+    xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+    yb = ctx.buffer(mmax * n * 4)
+    idx = ctx.buffer(mmax * 4)
+    for m in (2, 4, 8, 16, 32):
+        say(f"lm_head 8B verify m={m}")
+        ctx.matmul(xb, mx4.BF16, m, w, yb)
+        idx.upload(np.full(mmax, 0xFFFFFFFF, np.uint32))
+        ctx.argmax_rows(yb, m, n, idx)
+        y = yb.download(np.float32, m * n).reshape(m, n)
+        assert_close(y, ref[:m], f"8B lm_head m={m}")
+        assert np.array_equal(idx.download(np.uint32, m), want[:m]), m
+    w.release()
+
+
 def test_recorded_decode_tail_replays(mx4, ctx, oracle):
     """A recorded pass (HIP graph) holding the fused lm_head argmax, a separate
     argmax over rows and a few-token GEMV: every replay, with new activations
@@ -514,7 +601,7 @@ def test_generic_shapes(mx4, ctx, oracle, m, n, k):
     ref = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
     for path in (mx4.PATH_AUTO, mx4.PATH_GENERIC):
         y = run_matmul(mx4, ctx, x, w, path)
-        assert_close(y, ref, f"m={m} n={n} k={k} path={path}")
+        assert_close(y, ref, f"m={m} n={n} k={k} path={path}", scaled=True)
 
 
 def test_errors_are_reported_not_launched(mx4, ctx):
@@ -638,7 +725,7 @@ def test_extreme_scales_take_the_exact_path(mx4, ctx, oracle):
     w = ctx.upload_weight(packed, scales, n, k)
     ref = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
     y = run_matmul(mx4, ctx, x, w, mx4.PATH_AUTO, mx4.BF16)
-    assert_close(y, ref, "subnormal scales")
+    assert_close(y, ref, "subnormal scales", scaled=True)
     with pytest.raises(mx4.Mx4Error, match="2..252"):
         run_matmul(mx4, ctx, x, w, mx4.PATH_GEMV, mx4.BF16)
     # a row made only of scale-0 blocks: every weight is subnormal, exact products
@@ -657,7 +744,7 @@ def test_extreme_scales_take_the_exact_path(mx4, ctx, oracle):
     ref3 = oracle.matmul(x, packed.reshape(-1), scales3.reshape(-1))
     assert np.array_equal(np.isnan(y3), np.isnan(ref3)) and np.array_equal(np.isinf(y3), np.isinf(ref3))
     fin = np.isfinite(ref3)
-    assert_close(y3[fin].reshape(1, -1), ref3[fin].reshape(1, -1), "finite rows next to inf rows")
+    assert_close(y3[fin].reshape(1, -1), ref3[fin].reshape(1, -1), "finite rows next to inf rows", scaled=True)
 
 
 # ------------------------------------------------------------------ skinny (speculative verify)
@@ -756,17 +843,18 @@ def test_skinny_tile_ring(mx4, ctx, oracle, n, k):
         ref = np.concatenate([oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), int(r), int(r) + 1)
                               for r in rows], axis=1)
         y = run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.BF16)
-        assert_close(y[:, rows], ref, f"ring {k}->{n} m={m}")
+        assert_close(y[:, rows], ref, f"ring {k}->{n} m={m}", scaled=True)
 
 
-@pytest.mark.parametrize("n,k", [(4096 + 5, 12288), (8192 + 37, 12288), (1024 - 5, 4096), (4096 + 5, 4096)])
+@pytest.mark.parametrize("n,k", [(4096 + 5, 12288), (8192 + 37, 12288), (1024 - 5, 4096), (4096 + 5, 4096),
+                                 (8192 + 5, 4096)])
 def test_skinny_split_k(mx4, ctx, oracle, n, k):
-    """Split K with bf16 activations: K = 12288 from 8 tokens on (four
+    """Split K with bf16 activations: K = 12288 from 12 tokens on (four
     workgroups per 16-row tile, each over a quarter of K), K = 4096 from 17 on
-    (four slices when every CU gets one tile, as for 1019 rows, else two from
-    20 tokens on); the
-    last workgroup of a tile adds the partials (fewer tokens run unsplit, on the
-    same weights). One-hot
+    (four slices when every CU gets one tile, as for 1019 rows; two from 20
+    tokens on for weights long enough for the tile ring, as 8197 rows; 4101
+    rows stay unsplit); the last workgroup of a tile adds the partials (fewer
+    tokens run unsplit, on the same weights). One-hot
     activations return every decoded weight row bit for bit (a tile whose sum
     went missing would show), random activations match the oracle on sampled
     rows, a repeated call is bit-identical (the arrival counts are re-armed),
@@ -790,7 +878,7 @@ def test_skinny_split_k(mx4, ctx, oracle, n, k):
         ref = np.concatenate([oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), int(r), int(r) + 1)
                               for r in rows], axis=1)
         y = run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.BF16)
-        assert_close(y[:, rows], ref, f"split K {k}->{n} m={m}")
+        assert_close(y[:, rows], ref, f"split K {k}->{n} m={m}", scaled=True)
         assert np.array_equal(run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.BF16), y), f"repeat m={m}"
 
 
@@ -812,7 +900,7 @@ def test_skinny_ragged_rows_and_identity(mx4, ctx, oracle):
         assert np.array_equal(y, dec[:, cols].T), xtype
     x2 = rng.standard_normal((5, k)).astype(np.float32)
     ref = oracle.matmul(x2, packed.reshape(-1), scales.reshape(-1))
-    assert_close(run_matmul(mx4, ctx, x2, w, mx4.PATH_AUTO, mx4.F32), ref, "ragged f32")
+    assert_close(run_matmul(mx4, ctx, x2, w, mx4.PATH_AUTO, mx4.F32), ref, "ragged f32", scaled=True)
 
 
 # ------------------------------------------------------------------ prefill (block-scaled MFMA)
@@ -1122,21 +1210,100 @@ def test_prefill_recorded_pass_after_prepare(mx4, ctx, oracle):
     p.release()
 
 
-def test_prefill_8b_shapes_sampled(mx4, ctx, oracle):
-    """M = 512 at the Qwen3-8B q and down shapes, sampled rows/cols against the oracle."""
+def _requant(oracle, x, act):
+    if act == "mxfp4":
+        return oracle.dequantize(*oracle.quantize(x))
+    return oracle.dequantize_fp8(*oracle.quantize_fp8(x))
+
+
+def _sampled_ref(oracle, xd, packed, scales, cols):
+    return np.concatenate([oracle.matmul_rows(xd, packed.reshape(-1), scales.reshape(-1), int(c), int(c) + 1)
+                           for c in cols], axis=1)
+
+
+def test_recorded_pass_survives_workspace_growth(mx4, ctx, oracle):
+    """A recorded prefill reads the context's requantization workspace. A later
+    eager call that needs a larger workspace must not free the buffer the pass
+    holds: every replay afterwards still equals the eager result, and the
+    larger call itself is correct."""
+    m, n, k = 64, 256, 2048
+    w = ctx.synth_weight(85, n, k, 0.02)
+    w.prepare_prefill()
+    x = oracle.bf16_to_f32(oracle.synth_bf16(86, 1.0, m * k)).reshape(m, k)
+    xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+    yb = ctx.buffer(m * n * 4)
+    ctx.reserve_prefill(m, k)
+    eager = _run_prefill(mx4, ctx, x, w, "mxfp4", mx4.BF16)
+    p = ctx.record(lambda: ctx.matmul_prefill(xb, mx4.BF16, m, w, mx4.ACT_MXFP4, yb))
+    # an eager prefill 16x larger than the reservation grows the workspace
+    m2, k2 = 512, 8192
+    w2 = ctx.synth_weight(87, 64, k2, 0.02)
+    x2 = oracle.bf16_to_f32(oracle.synth_bf16(88, 1.0, m2 * k2)).reshape(m2, k2)
+    y2 = _run_prefill(mx4, ctx, x2, w2, "mxfp8", mx4.BF16)
+    packed2, scales2 = ctx.download_weight(w2)
+    rows = np.arange(0, m2, 37)
+    ref2, _ = _prefill_ref(oracle, x2[rows], packed2, scales2, "mxfp8")
+    assert_close(y2[rows], ref2, "grown workspace")
+    for _ in range(3):
+        yb.upload(np.zeros(m * n, np.float32))
+        p.launch()
+        ctx.synchronize()
+        assert np.array_equal(yb.download(np.float32).reshape(m, n), eager)
+    p.release()
+    # with no pass alive the next growth frees at once; results stay right
+    y3 = _run_prefill(mx4, ctx, x, w, "mxfp4", mx4.BF16)
+    assert np.array_equal(y3, eager)
+    w.release()
+    w2.release()
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+@pytest.mark.parametrize("name", ["q", "o", "gate", "up", "down"])
+def test_prefill_8b_shapes_sampled(mx4, ctx, oracle, name, act):
+    """M = 512 at every Qwen3-8B prefill shape (config 5: q/o 4096->4096,
+    gate/up 4096->12288, down 12288->4096), MXFP4 and MX-FP8 activations: 24
+    token rows x sampled weight rows against the oracle on dequant(requant(x)),
+    through the default instance of each shape."""
     rng = np.random.default_rng(77)
-    for name in ("q", "down"):
-        n, k = QWEN8[name]
-        say(f"prefill 8B {name} 512 x {k} -> {n}")
-        m = 512
-        w = ctx.synth_weight(400, n, k, 0.02)
+    n, k = QWEN8[name]
+    m = 512
+    say(f"prefill 8B {name} {act} 512 x {k} -> {n}")
+    w = ctx.synth_weight(400 + list(QWEN8).index(name), n, k, 0.02)
+    packed, scales = ctx.download_weight(w)
+    x = oracle.bf16_to_f32(oracle.synth_bf16(401, 1.0, m * k)).reshape(m, k)
+    rows = np.unique(np.concatenate([[0, m - 1], rng.choice(m, 22, replace=False)]))
+    cols = _sample_rows(n, 96, rng)
+    ref = _sampled_ref(oracle, _requant(oracle, x[rows], act), packed, scales, cols)
+    y = _run_prefill(mx4, ctx, x, w, act, mx4.BF16)
+    assert_close(y[np.ix_(rows, cols)], ref, f"prefill 8B {name} {act}")
+    w.release()
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+def test_prefill_8b_gate_up_group(mx4, ctx, oracle, act):
+    """gate|up at M = 512 through mx4_matmul_prefill_group (engine/src/lib.rs:459-467:
+    both read the same activations; one requantization, one launch) against the
+    oracle on sampled rows and columns, and bit for bit equal to the single-weight
+    launches (the group's default instance is the weights' own)."""
+    rng = np.random.default_rng(78)
+    n, k = QWEN8["gate"]
+    m = 512
+    say(f"prefill 8B gate|up group {act}")
+    ws = [ctx.synth_weight(410 + i, n, k, 0.02) for i in range(2)]
+    x = oracle.bf16_to_f32(oracle.synth_bf16(411, 1.0, m * k)).reshape(m, k)
+    xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+    code = mx4.ACT_MXFP4 if act == "mxfp4" else mx4.ACT_MXFP8
+    ys = [ctx.buffer(m * n * 4) for _ in ws]
+    ctx.matmul_prefill_group(xb, mx4.BF16, m, ws, code, ys)
+    rows = np.unique(np.concatenate([[0, m - 1], rng.choice(m, 14, replace=False)]))
+    xd = _requant(oracle, x[rows], act)
+    for i, w in enumerate(ws):
+        got = ys[i].download(np.float32).reshape(m, n)
         packed, scales = ctx.download_weight(w)
-        x = oracle.bf16_to_f32(oracle.synth_bf16(401, 1.0, m * k)).reshape(m, k)
-        rows = rng.choice(m, 24, replace=False)
-        cols = _sample_rows(n, 96, rng)
-        xq, xs = oracle.quantize(x[rows])
-        xd = oracle.dequantize(xq, xs)
-        ref = np.concatenate([oracle.matmul_rows(xd, packed.reshape(-1), scales.reshape(-1), int(c), int(c) + 1)
-                              for c in cols], axis=1)
-        y = _run_prefill(mx4, ctx, x, w, "mxfp4", mx4.BF16)
-        assert_close(y[np.ix_(rows, cols)], ref, f"prefill 8B {name}")
+        cols = _sample_rows(n, 64, rng)
+        assert_close(got[np.ix_(rows, cols)], _sampled_ref(oracle, xd, packed, scales, cols),
+                     f"gate|up group {act} weight {i}")
+        single = _run_prefill(mx4, ctx, x, w, act, mx4.BF16)
+        assert np.array_equal(single, got), f"group output {i} differs from its single launch"
+    for w in ws:
+        w.release()
