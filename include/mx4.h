@@ -190,6 +190,26 @@ mx4_status mx4_gemv_tokens_config(mx4_context *ctx, const void *x_dev, uint32_t 
 mx4_status mx4_matmul_prefill(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m,
                               const mx4_weight *w, mx4_act_format act, float *y_dev);
 
+/* mx4_matmul_prefill without any allocation. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The same
+ * kernels and the same result, bit for bit, as mx4_matmul_prefill; the
+ * requantized activations go to a fixed workspace of the library instead of
+ * the context's growable one: a file-scope device array of 8 MiB that every
+ * GPU the library runs on holds until the process ends (set up by the first
+ * mx4_create on the device). Limits and rules:
+ *  - 256 + codes + scales of the requantized x must fit 8 MiB (m x cols
+ *    MXFP4: m * cols / 2 + m * cols / 32, rows rounded up to 32; MX-FP8:
+ *    m * cols + m * cols / 32): M = 512 at K = 12288 fits in both formats;
+ *    larger inputs fail with MX4_ERR_TOO_LARGE;
+ *  - the weight's matrix-core copy must exist (mx4_weight_prepare_prefill),
+ *    else MX4_ERR_UNSUPPORTED;
+ *  - calls on one GPU share the workspace, which keeps the last call's
+ *    contents: calls that overlap on one GPU (other streams, other contexts on
+ *    the same device) race; keep them ordered. */
+mx4_status mx4_matmul_prefill_noalloc(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m,
+                                      const mx4_weight *w, mx4_act_format act, float *y_dev);
+
 /* mx4_matmul_prefill for up to 4 weights of the same width that read the
  * same activations (q|k|v at engine/src/lib.rs:353-355, gate|up at
  * :459-467): one requantization and one block-scaled MFMA launch, the

@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <list>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 #include <unordered_set>
@@ -124,6 +125,16 @@ struct mx4_context {
     std::vector<void*> retired;
 };
 
+// Workspace of mx4_matmul_prefill_noalloc: the requantized activations in
+// the fragment-native layout (codes, 256-byte aligned, then scales) after a
+// 256-byte head holding the requantizer's non-finite flag. A file-scope device
+// array: every GPU the library runs on holds its own copy until the process
+// ends, and host code reaches it only through the address hipGetSymbolAddress
+// returns for that device (the array's name is a host-side stand-in).
+constexpr uint64_t kNoAllocScratchBytes = 8ull << 20;
+constexpr uint64_t kNoAllocHead = 256;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 constexpr uint32_t kArgmaxPartials = 8192;
 // 4 MiB of partial tiles: four K slices of up to 8192 rows at 32 tokens
 constexpr uint32_t kSplitPartTiles = 4096;
@@ -134,6 +145,29 @@ hipError_t launch_fill_u32(uint32_t* p, uint32_t count, uint32_t value, hipStrea
 }
 
 namespace {
+
+// Device address of `scratch` on each device, looked up once per device (by
+// the first mx4_create on it, with that device current).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+uint8_t* g_scratch_ptr[kMaxDevices] = {};
+
+hipError_t scratch_lookup(int device) {
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[device]) return hipSuccess;
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[device] = static_cast<uint8_t*>(ptr);
+    return hipSuccess;
+}
+
+uint8_t* scratch_of(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    return g_scratch_ptr[device];
+}
 
 struct DeviceGuard {
     int prev = -1;
@@ -378,6 +412,13 @@ mx4_status mx4_create(int device, mx4_context** out) {
         hipStreamSynchronize(ctx->own) != hipSuccess) {
         mx4_destroy(ctx);
         return fail(MX4_ERR_DEVICE, "could not create stream, events or scratch on device %d", device);
+    }
+    // the no-alloc entry point's device workspace on this device
+    const hipError_t se = scratch_lookup(device);
+    if (se != hipSuccess) {
+        mx4_destroy(ctx);
+        return fail(MX4_ERR_DEVICE, "hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+                    hipGetErrorString(se));
     }
     ctx->stream = ctx->own;
     *out = ctx;
@@ -714,6 +755,40 @@ mx4_status mx4_matmul_prefill(mx4_context* ctx, const void* x, mx4_dtype xt, uin
     hipError_t e = mx4::launch_quantize_fragments(x, xt == MX4_BF16, m, w->cols, fp8, xf, xsf, ctx->flags, ctx->stream);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "requantize launch failed: %s", hipGetErrorString(e));
     e = mx4::launch_prefill(prefill_args(ctx, wm, xf, xsf, y, m, fp8), ctx->cus);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status mx4_matmul_prefill_noalloc(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, const mx4_weight* w,
+                                      mx4_act_format act, float* y) {
+    mx4_status st = check_matmul_args(ctx, x, xt, m, w, y);
+    if (st != MX4_OK) return st;
+    if (act != MX4_ACT_MXFP4 && act != MX4_ACT_MXFP8) return fail(MX4_ERR_ARGUMENT, "bad activation format");
+    if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
+    if (!mx4::prefill_supported(m, w->rows, w->cols))
+        return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0 and operands under 2 GiB");
+    if (!w->frag)
+        return fail(MX4_ERR_UNSUPPORTED,
+                    "the weight has no matrix-core copy; call mx4_weight_prepare_prefill first (this entry point "
+                    "allocates nothing)");
+    const bool fp8 = act == MX4_ACT_MXFP8;
+    const uint64_t need = kNoAllocHead + prefill_workspace_bytes(m, w->cols, fp8);
+    if (need > kNoAllocScratchBytes)
+        return fail(MX4_ERR_TOO_LARGE,
+                    "requantized activations of %u x %u (%s) need %llu bytes; the no-alloc workspace holds %llu",
+                    m, w->cols, fp8 ? "MX-FP8" : "MXFP4", (unsigned long long)need,
+                    (unsigned long long)kNoAllocScratchBytes);
+    uint8_t* base = scratch_of(ctx->device);
+    if (!base) return fail(MX4_ERR_DEVICE, "no-alloc workspace not set up on device %d", ctx->device);
+    DeviceGuard g(ctx->device);
+    // head: the requantizer's non-finite flag (written, never read here: such
+    // rows come out as NaN); then codes and scales as in the context workspace
+    uint32_t* flag = reinterpret_cast<uint32_t*>(base);
+    uint8_t* xf = base + kNoAllocHead;
+    uint8_t* xsf = xf + ((mx4::fragment_bytes(m, w->cols, fp8) + 255) & ~255ull);
+    hipError_t e = mx4::launch_quantize_fragments(x, xt == MX4_BF16, m, w->cols, fp8, xf, xsf, flag, ctx->stream);
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "requantize launch failed: %s", hipGetErrorString(e));
+    e = mx4::launch_prefill(prefill_args(ctx, w, xf, xsf, y, m, fp8), ctx->cus);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "prefill launch failed: %s", hipGetErrorString(e));
     return MX4_OK;
 }

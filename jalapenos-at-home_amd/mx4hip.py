@@ -23,6 +23,7 @@ STATUS = {
     4: "MX4_ERR_LENGTH", 5: "MX4_ERR_NAN_SCALE", 6: "MX4_ERR_NON_FINITE",
     7: "MX4_ERR_DEVICE", 8: "MX4_ERR_NO_MEMORY", 9: "MX4_ERR_UNSUPPORTED",
 }
+ERR_TOO_LARGE = 3
 ERR_UNSUPPORTED = 9
 F32, BF16 = 0, 1
 PATH_AUTO, PATH_GEMV, PATH_SKINNY, PATH_GENERIC, PATH_PREFILL = 0, 1, 2, 3, 4
@@ -62,6 +63,7 @@ SIGNATURES = {
     "mx4_matmul": (_int, [_vp, _vp, _int, _u32, _vp, _vp]),
     "mx4_matmul_path": (_int, [_vp, _vp, _int, _u32, _vp, _vp, _int]),
     "mx4_matmul_prefill": (_int, [_vp, _vp, _int, _u32, _vp, _int, _vp]),
+    "mx4_matmul_prefill_noalloc": (_int, [_vp, _vp, _int, _u32, _vp, _int, _vp]),
     "mx4_matmul_group": (_int, [_vp, _vp, _int, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32]),
     "mx4_gemv_config": (_int, [_vp, _vp, _int, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32, _int, _int, _int, _u32]),
     "mx4_gemv_tokens_config": (_int, [_vp, _vp, _u32, _vp, _vp, _u32, _u32]),
@@ -334,6 +336,11 @@ class Context:
 
     def matmul_prefill(self, x: DeviceBuffer, xtype: int, m: int, w: Weight, act: int, y: DeviceBuffer) -> None:
         check(lib().mx4_matmul_prefill(self.handle, x.ptr, xtype, m, w.handle, act, y.ptr))
+
+    def matmul_prefill_noalloc(self, x: DeviceBuffer, xtype: int, m: int, w: Weight, act: int,
+                               y: DeviceBuffer) -> None:
+        """mx4_matmul_prefill with the library's fixed per-device workspace (allocates nothing)."""
+        check(lib().mx4_matmul_prefill_noalloc(self.handle, x.ptr, xtype, m, w.handle, act, y.ptr))
 
     def matmul_prefill_group(self, x: DeviceBuffer, xtype: int, m: int, ws, act: int, ys) -> None:
         """Requantize x once, then one block-scaled MFMA launch for 1..4 weights (ys: DeviceBuffers)."""
