@@ -7,38 +7,55 @@ gate 4096->12288, up 4096->12288, down 12288->4096} plus lm_head 4096->151936,
 253 GEMVs over 4,029,425,152 algorithmic bytes. Every projection has its own
 resident weight (4.03 GB in HBM, far beyond the 256 MB Infinity Cache), made on
 the GPU by the weight recipe (bf16 N(0, 0.02), MXFP4 by the reference rule;
-tensor j uses seed 1000 + j). Activations are bf16 N(0, 1) from seed 1, already
-in HBM; outputs are f32. Projections that read the same activations in the
-model share a launch, as a decode step allows: q|k|v and gate|up, so a layer
-is 4 launches (qkv, o, gate|up, down) and the step 145. A step is replayed as
-one recorded pass (HIP graph) unless --eager is given; --separate launches all
-253 GEMVs one by one.
+tensor j uses seed 1000 + j) in one device allocation, each weight on its own
+2 MiB-aligned slice. Activations are bf16 N(0, 1) from seed 1, already in HBM;
+outputs are f32. Projections that read the same activations in the model share
+a launch, as a decode step allows: q|k|v and gate|up, so a layer is 4 launches
+(qkv, o, gate|up, down) and the step 145. A step is replayed as one recorded
+pass (HIP graph) unless --eager is given; --separate launches all 253 GEMVs
+one by one.
 
 Algorithmic bytes of one GEMV: N*K/2 (nibbles) + N*K/32 (scales) + M*K*2 (bf16
 x) + M*N*4 (f32 y). value = bytes per step / wall time per step.
 
-extra.dropin_per_call times the per-call drop-in (qwen_hip_matmul: host f32 x
-and y, synchronous) on layer 0 and the lm_head: the PCIe-inclusive rate.
+Timing protocol of every figure in `extra` (engine/src/model.rs:259-264,
+engine/src/main.rs:70): a recorded pass of distinct weight copies totalling at
+least 512 MiB per shape (cold: twice the Infinity Cache), 2 untimed launches,
+then the median of 15 timed launches; per-call time = pass time / calls.
+
+extra also carries the other workloads: the Qwen3-1.7B decode step (28 layers,
+tensor j from seed 2000 + j) with its per-shape figures, the single 6144 x 2048
+GEMV of config 1 (weight seed 0, x seed 1; cold over copies, and warm on one
+weight, labelled), speculative verify (8B shapes at M = 1..32), prefill at
+M = 512 (block-scaled MFMA; exact bf16-MFMA AUTO path), the per-call drop-in
+(PCIe-inclusive), and the CPU legs below.
 
 cpu_baseline: the CPU oracle (a restatement of engine/src/lib.rs:240-266) on
 the box's host, one thread, over a bounded sample with the step's shape mix:
 all 7 projections of the first 9 layers plus the matching 9/36 of lm_head's
-rows. extra.cpu_all_cores runs the same sample on every host thread (the
-oracle parallelises over output elements; each element keeps its order).
+rows. extra.cpu holds the same sample on every host thread, configs 4 and 5
+(row subsets, extrapolated to the full shapes, as stated in each entry), and
+the host CPU model and core counts.
 
-extra also carries the other M = 1 workloads: the Qwen3-1.7B decode step (28
-layers x {q 2048->2048, k/v 2048->1024, o 2048->2048, gate/up 2048->6144,
-down 6144->2048} + lm_head 2048->151936, tensor j from seed 2000 + j, grouped
-and recorded like the 8B step) with its per-shape figures, and the single
-6144 x 2048 GEMV of the weight from seed 0 and x from seed 1.
+Profile modes (for rocprofv3; see profiles/): --profile-step, --profile-traffic,
+--profile-prefill run only the work their summaries cover and print a stamp
+(library sha256); --summarize KIND DIR [DIR] turns rocprofv3 CSV output into
+the committed summaries. roofline.traffic is taken from
+profiles/gemv_qwen3_8b_m1_step_traffic.md only when its stamp matches the
+library this run loaded, and is null otherwise.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import ctypes
+import hashlib
 import json
 import os
+import subprocess
 import sys
 import time
+from collections import defaultdict
 from pathlib import Path
 
 import numpy as np
@@ -53,32 +70,88 @@ LAYER = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 40
 LM_HEAD = ("lm_head", 151936, 4096)
 LAYERS = 36
 HBM_PEAK_GBS = 8000.0
+PEAK_TFLOPS = {"mxfp4": 10100.0, "mxfp8": 5000.0, "bf16": 2500.0}
 LAYER_1P7B = [("q", 2048, 2048), ("k", 1024, 2048), ("v", 1024, 2048), ("o", 2048, 2048),
               ("gate", 6144, 2048), ("up", 6144, 2048), ("down", 2048, 6144)]
 LM_HEAD_1P7B = ("lm_head", 151936, 2048)
 LAYERS_1P7B = 28
+ROTATION_BYTES = 512 << 20   # distinct weight bytes per timed shape (2 x the Infinity Cache)
+REPS, WARM = 15, 2           # timed launches (median) and untimed ones before them
+ARENA_ALIGN = 2 << 20
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemv_qwen3_8b_m1_step_traffic.md"
 
 
 def gemv_bytes(m: int, n: int, k: int, x_bytes: int = 2) -> int:
     return n * k // 2 + n * k // 32 + m * k * x_bytes + m * n * 4
 
 
+def weight_bytes(n: int, k: int) -> int:
+    return n * k // 2 + n * k // 32
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def build_step(ctx: mx4hip.Context, layer=LAYER, lm_head=LM_HEAD, layers=LAYERS, seed0=1000):
-    """Distinct resident weights for every projection of the step."""
-    weights = []
+def library_sha256() -> str:
+    return hashlib.sha256(mx4hip.LIB_PATH.read_bytes()).hexdigest()
+
+
+# ---------------------------------------------------------------- weights
+
+class Arena:
+    """Synthesized MXFP4 weights in one device allocation, each on its own
+    2 MiB-aligned slice (packed bytes, then its scales), wrapped as resident
+    weights. specs: (rows, cols, seed)."""
+
+    def __init__(self, ctx: mx4hip.Context, specs):
+        L = mx4hip.lib()
+        self.ctx = ctx
+        offs, total = [], 0
+        for (n, k, _) in specs:
+            total = (total + ARENA_ALIGN - 1) // ARENA_ALIGN * ARENA_ALIGN
+            po = total
+            so = (po + n * k // 2 + 255) // 256 * 256
+            offs.append((po, so))
+            total = so + n * k // 32
+        base = ctypes.c_void_p()
+        mx4hip.check(L.mx4_malloc(ctx.handle, max(total, 1), ctypes.byref(base)))
+        self.base = base.value
+        self.nbytes = total
+        self.weights = []
+        for (n, k, seed), (po, so) in zip(specs, offs):
+            p, s = ctypes.c_void_p(self.base + po), ctypes.c_void_p(self.base + so)
+            mx4hip.check(L.mx4_synth_weight(ctx.handle, seed, ctypes.c_double(0.02), n, k, p, s))
+            h = ctypes.c_void_p()
+            mx4hip.check(L.mx4_weight_wrap(ctx.handle, p, s, n, k, ctypes.byref(h)))
+            self.weights.append(ctx._track(mx4hip.Weight(ctx, h.value, n, k)))
+        ctx.synchronize()
+
+    def release(self) -> None:
+        self.ctx.synchronize()
+        for w in self.weights:
+            w.release()
+        self.weights = []
+        if self.base:
+            mx4hip.check(mx4hip.lib().mx4_free(self.ctx.handle, ctypes.c_void_p(self.base)))
+            self.base = None
+
+
+def build_step(ctx, layer=LAYER, lm_head=LM_HEAD, layers=LAYERS, seed0=1000):
+    """Distinct resident weights for every projection of the step, one arena."""
+    specs, names = [], []
     seed = seed0
     for _ in range(layers):
         for name, n, k in layer:
-            weights.append((name, n, k, ctx.synth_weight(seed, n, k, 0.02)))
+            specs.append((n, k, seed))
+            names.append(name)
             seed += 1
     name, n, k = lm_head
-    weights.append((name, n, k, ctx.synth_weight(seed, n, k, 0.02)))
-    ctx.synchronize()
-    return weights
+    specs.append((n, k, seed))
+    names.append(name)
+    arena = Arena(ctx, specs)
+    weights = [(nm, n, k, w) for nm, (n, k, _), w in zip(names, specs, arena.weights)]
+    return weights, arena
 
 
 def enqueue_grouped_step(ctx, weights, xs, yq, layer=LAYER, layers=LAYERS):
@@ -98,183 +171,214 @@ def enqueue_grouped_step(ctx, weights, xs, yq, layer=LAYER, layers=LAYERS):
     ctx.matmul_ptr(xs[k].ptr, mx4hip.BF16, 1, w, yq["lm_head"].ptr)
 
 
-MIN_COPIES = 4
+def rotation(ctx, members, seed0: int, min_bytes: int = ROTATION_BYTES) -> tuple[Arena, list]:
+    """Copies of a shape (one member) or of a group of shapes read together
+    (q|k|v, gate|up): as many distinct copies as make up min_bytes of
+    weights. members: [(rows, cols)]. Returns the arena and the copies, each a
+    list of weights (one per member)."""
+    per = sum(weight_bytes(n, k) for n, k in members)
+    copies = max(2, -(-min_bytes // per))
+    specs = [(n, k, seed0 + c * len(members) + i) for c in range(copies) for i, (n, k) in enumerate(members)]
+    arena = Arena(ctx, specs)
+    ws = arena.weights
+    return arena, [ws[c * len(members):(c + 1) * len(members)] for c in range(copies)]
 
 
-def copies_by_name(ctx, weights, seed0: int = 9000):
-    """The weights grouped by projection name, each with at least MIN_COPIES
-    distinct copies: a shape with a single weight (lm_head) gets extra copies
-    from the same recipe, so that its per-launch time is taken over several
-    cold launches in one recorded pass, as for the per-layer shapes. Returns
-    the groups and the extra weights (to release afterwards)."""
-    by, extra = {}, []
-    for (nm, n, k, w) in weights:
-        by.setdefault(nm, []).append((n, k, w))
-    for nm, lst in by.items():
-        n, k, _ = lst[0]
-        while len(lst) < MIN_COPIES:
-            w = ctx.synth_weight(seed0 + len(extra), n, k, 0.02)
-            extra.append(w)
-            lst.append((n, k, w))
+# ---------------------------------------------------------------- timing
+
+def time_pass(ctx, enqueue, calls: int, reps: int = REPS, warm: int = WARM) -> dict:
+    """Record `enqueue` as a pass, launch it `warm` times untimed, then `reps`
+    timed launches; per-call median and minimum in microseconds."""
+    p = ctx.record(enqueue)
+    for _ in range(warm):
+        p.launch()
     ctx.synchronize()
-    return by, extra
+    ts = []
+    for _ in range(reps):
+        ctx.timer_begin()
+        p.launch()
+        ts.append(ctx.timer_end() / calls * 1e3)
+    p.release()
+    return {"us": round(float(np.median(ts)), 3), "us_min": round(float(np.min(ts)), 3)}
 
 
-def release(ctx, extra) -> None:
-    ctx.synchronize()
-    for w in extra:
-        w.release()
+def hbm_entry(t: dict, nbytes: int, extra: dict | None = None) -> dict:
+    gbps = nbytes / (t["us"] * 1e-6) / 1e9
+    out = dict(extra or {})
+    out.update({"bytes": nbytes, "us": t["us"], "us_min": t["us_min"], "GBps": round(gbps, 1),
+                "frac": round(gbps / HBM_PEAK_GBS, 4)})
+    return out
 
 
-def time_shapes(ctx, weights, xs, ys, reps: int = 3, layer=LAYER):
-    """Per-launch GPU time of each projection shape and of the grouped launches:
-    the distinct copies of each (one per layer; lm_head in four copies) back to
-    back, cold, in a recorded pass, timed with events on the context stream."""
-    by, extra = copies_by_name(ctx, weights)
+def time_shapes(ctx, xs, layer=LAYER, lm_head=LM_HEAD, seed0=20000) -> dict:
+    """Per-launch time of each projection shape and of the grouped launches
+    (q|k|v, gate|up), each over >= 512 MiB of distinct cold copies."""
+    dims = {name: (n, k) for name, n, k in layer + [lm_head]}
     plans = [(name, [name]) for name, _, _ in layer] + [("qkv", ["q", "k", "v"]), ("gate_up", ["gate", "up"]),
-                                                         ("lm_head", ["lm_head"])]
+                                                        (lm_head[0], [lm_head[0]])]
     table = {}
-    for label, members in plans:
-        copies = len(by[members[0]])
-        k = by[members[0]][0][1]
-        ybufs = [ys[by[m][0][0]] for m in members]
-        if len(members) > 1:
-            yext = [ctx.buffer(by[m][0][0] * 4) for m in members]
-            ybufs = yext
+    for i, (label, members) in enumerate(plans):
+        mdims = [dims[m] for m in members]
+        k = mdims[0][1]
+        arena, copies = rotation(ctx, mdims, seed0 + 1000 * i)
+        ys = [ctx.buffer(n * 4) for n, _ in mdims]
 
         def enqueue():
-            for c in range(copies):
-                ws = [by[m][c][2] for m in members]
+            for ws in copies:
                 if len(ws) == 1:
-                    ctx.matmul_ptr(xs[k].ptr, mx4hip.BF16, 1, ws[0], ybufs[0].ptr)
+                    ctx.matmul_ptr(xs[k].ptr, mx4hip.BF16, 1, ws[0], ys[0].ptr)
                 else:
-                    ctx.matmul_group(xs[k].ptr, mx4hip.BF16, 1, ws, [y.ptr for y in ybufs])
+                    ctx.matmul_group(xs[k].ptr, mx4hip.BF16, 1, ws, [y.ptr for y in ys])
 
-        p = ctx.record(enqueue)
-        p.launch()
-        best = None
-        for _ in range(reps):
-            ctx.synchronize()
-            ctx.timer_begin()
-            p.launch()
-            ms = ctx.timer_end() / copies
-            best = ms if best is None else min(best, ms)
-        p.release()
-        b = sum(gemv_bytes(1, by[m][0][0], k) for m in members)
-        n = sum(by[m][0][0] for m in members)
-        table[label] = {"k": k, "n": n, "bytes": b, "us": round(best * 1e3, 3),
-                        "GBps": round(b / (best * 1e-3) / 1e9, 1),
-                        "frac": round(b / (best * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-    release(ctx, extra)
+        t = time_pass(ctx, enqueue, len(copies))
+        b = sum(gemv_bytes(1, n, k) for n, _ in mdims)
+        table[label] = hbm_entry(t, b, {"k": k, "n": sum(n for n, _ in mdims), "copies": len(copies)})
+        arena.release()
     return table
 
 
-def time_skinny(ctx, weights, ms=(1, 2, 4, 8, 16, 32), reps: int = 3):
-    """Speculative-verify shapes: each 8B projection at M token rows (exact path:
-    GEMV for M = 1, skinny bf16-MFMA kernel above), 36 cold copies (lm_head: 4)
-    in a recorded pass, per-call latency and effective GB/s (bytes with
-    M*K*2 + M*N*4)."""
-    by, extra = copies_by_name(ctx, weights)
+def time_lm_head_argmax(ctx, xs) -> dict:
+    """Greedy pick after the lm_head (engine/src/model.rs:228-238, :288-296) at
+    M = 1 over two cold copies (662 MB): the projection alone, followed by a
+    separate argmax over the 151936 logits, and the fused epilogue with and
+    without writing the logits."""
+    _, n, k = LM_HEAD
+    arena, copies = rotation(ctx, [(n, k)], 30000)
+    y = ctx.buffer(n * 4)
+    idx = ctx.buffer(4)
+    x = xs[k]
+    forms = (("projection", lambda w: ctx.matmul_ptr(x.ptr, mx4hip.BF16, 1, w, y.ptr)),
+             ("projection+argmax_rows", lambda w: (ctx.matmul_ptr(x.ptr, mx4hip.BF16, 1, w, y.ptr),
+                                                   ctx.argmax_rows(y, 1, n, idx))),
+             ("fused, logits written", lambda w: ctx.matmul_argmax(x, mx4hip.BF16, w, y, idx)),
+             ("fused, no logits", lambda w: ctx.matmul_argmax(x, mx4hip.BF16, w, None, idx)))
     out = {}
-    for name, n, k in LAYER + [LM_HEAD]:
-        ws = [w for (_, _, w) in by[name]]
+    for label, fn in forms:
+        out[label] = time_pass(ctx, lambda: [fn(ws[0]) for ws in copies], len(copies))["us"]
+    arena.release()
+    return {"n": n, "k": k, "copies": len(copies), "us": out}
+
+
+def time_skinny(ctx, ms=(1, 2, 4, 8, 16, 32)) -> dict:
+    """Speculative-verify shapes (config 4): each 8B projection at M token rows
+    through AUTO (GEMV at M = 1, few-token GEMV or skinny bf16-MFMA kernel
+    above), over >= 512 MiB of cold copies per shape; per-call latency and
+    effective GB/s (bytes with M*K*2 + M*N*4)."""
+    out = {}
+    for i, (name, n, k) in enumerate(LAYER + [LM_HEAD]):
+        arena, copies = rotation(ctx, [(n, k)], 40000 + 1000 * i)
         row = {}
         for m in ms:
             xb = ctx.buffer(m * k * 2)
             ctx.synth_bf16(2, 1.0, m * k, xb)
             yb = ctx.buffer(m * n * 4)
-
-            def enqueue():
-                for w in ws:
-                    ctx.matmul_ptr(xb.ptr, mx4hip.BF16, m, w, yb.ptr)
-
-            p = ctx.record(enqueue)
-            p.launch()
-            best = None
-            for _ in range(reps):
-                ctx.synchronize()
-                ctx.timer_begin()
-                p.launch()
-                t = ctx.timer_end() / len(ws)
-                best = t if best is None else min(best, t)
-            p.release()
+            t = time_pass(ctx, lambda: [ctx.matmul_ptr(xb.ptr, mx4hip.BF16, m, ws[0], yb.ptr) for ws in copies],
+                          len(copies))
             b = gemv_bytes(m, n, k)
-            row[f"M{m}"] = {"us": round(best * 1e3, 3), "GBps": round(b / (best * 1e-3) / 1e9, 1)}
+            row[f"M{m}"] = {"us": t["us"], "GBps": round(b / (t["us"] * 1e-6) / 1e9, 1)}
         out[name] = row
-    release(ctx, extra)
+        arena.release()
     return out
 
 
-def time_lm_head_argmax(ctx, weights, xs, reps: int = 5):
-    """Greedy pick after the lm_head (engine/src/model.rs:228-238, :288-296) at
-    M = 1: the projection followed by a separate argmax over the 151936 logits,
-    against the fused epilogue with and without writing the logits. 8 calls
-    per recorded pass; per-call GPU time."""
-    _, n, k, w = weights[-1]
-    y = ctx.buffer(n * 4)
-    idx = ctx.buffer(4)
-    x = xs[k]
-    forms = (("projection", lambda: ctx.matmul_ptr(x.ptr, mx4hip.BF16, 1, w, y.ptr)),
-             ("projection+argmax_rows", lambda: (ctx.matmul_ptr(x.ptr, mx4hip.BF16, 1, w, y.ptr),
-                                                 ctx.argmax_rows(y, 1, n, idx))),
-             ("fused, logits written", lambda: ctx.matmul_argmax(x, mx4hip.BF16, w, y, idx)),
-             ("fused, no logits", lambda: ctx.matmul_argmax(x, mx4hip.BF16, w, None, idx)))
+def time_prefill(ctx, m: int = 512) -> dict:
+    """Prefill (config 5) on block-scaled MFMA: each 8B q/o/gate/up/down shape
+    at M = 512, activations bf16 N(0, 1) requantized per 32 along K (MXFP4 and
+    MX-FP8), over >= 512 MiB of cold weight copies. The GEMM kernel alone
+    (activations requantized beforehand, as when q|k|v or gate|up share them)
+    and requant + GEMM, as TFLOP/s of 2*M*N*K."""
     out = {}
-    for label, fn in forms:
-        p = ctx.record(lambda: [fn() for _ in range(8)])
-        p.launch()
-        best = None
-        for _ in range(reps):
-            ctx.synchronize()
-            ctx.timer_begin()
-            p.launch()
-            t = ctx.timer_end() / 8
-            best = t if best is None else min(best, t)
-        p.release()
-        out[label] = round(best * 1e3, 2)
-    return {"n": n, "k": k, "us": out}
-
-
-def time_prefill(ctx, weights, m: int = 512, reps: int = 5):
-    """Prefill on block-scaled MFMA: each 8B q/o/gate/up/down shape at M = 512,
-    activations bf16 N(0, 1) requantized per 32 along K (MXFP4, and MX-FP8).
-    Reports the GEMM kernel alone (activations requantized beforehand, as when
-    q|k|v or gate|up share them) and requant + GEMM, as TFLOP/s of 2*M*N*K."""
-    by = {}
-    for (nm, n, k, w) in weights:
-        by.setdefault(nm, (n, k, w))
-    peaks = {"mxfp4": 10.1e15, "mxfp8": 5.0e15}
-    ctx.reserve_prefill(m, max(k for (_, k, _) in by.values()))
-    out = {}
-    for name in ("q", "o", "gate", "up", "down"):
-        n, k, w = by[name]
+    dims = {name: (n, k) for name, n, k in LAYER}
+    ctx.reserve_prefill(m, 12288)
+    for i, name in enumerate(("q", "o", "gate", "up", "down")):
+        n, k = dims[name]
+        arena, copies = rotation(ctx, [(n, k)], 50000 + 1000 * i)
+        for ws in copies:
+            ws[0].prepare_prefill()  # the matrix-core copy of each weight, outside the timed passes
         xb = ctx.buffer(m * k * 2)
         ctx.synth_bf16(3, 1.0, m * k, xb)
         yb = ctx.buffer(m * n * 4)
-        row = {}
-        w.prepare_prefill()  # the matrix-core copy of the weight is built outside the timed passes
+        flops = 2.0 * m * n * k
+        row = {"m": m, "n": n, "k": k, "copies": len(copies)}
         for act, code in (("mxfp4", mx4hip.ACT_MXFP4), ("mxfp8", mx4hip.ACT_MXFP8)):
-            xq, xs = ctx.prefill_act_buffers(m, k, code)
-            ctx.prefill_quantize(xb, mx4hip.BF16, m, k, code, xq, xs)
-            flops = 2.0 * m * n * k
+            xq, xsc = ctx.prefill_act_buffers(m, k, code)
+            ctx.prefill_quantize(xb, mx4hip.BF16, m, k, code, xq, xsc)
             res = {}
-            for label, fn in (("gemm", lambda: ctx.prefill_matmul(xq, xs, code, m, w, yb)),
-                              ("requant+gemm", lambda: ctx.matmul_prefill(xb, mx4hip.BF16, m, w, code, yb))):
-                p = ctx.record(lambda: [fn() for _ in range(8)])
-                p.launch()
-                best = None
-                for _ in range(reps):
-                    ctx.synchronize()
-                    ctx.timer_begin()
-                    p.launch()
-                    t = ctx.timer_end() / 8
-                    best = t if best is None else min(best, t)
-                p.release()
-                tf = flops / (best * 1e-3)
-                res[label] = {"us": round(best * 1e3, 2), "TFLOPs": round(tf / 1e12, 1),
-                              "frac": round(tf / peaks[act], 4)}
+            for label, fn in (("gemm", lambda w: ctx.prefill_matmul(xq, xsc, code, m, w, yb)),
+                              ("requant+gemm", lambda w: ctx.matmul_prefill(xb, mx4hip.BF16, m, w, code, yb))):
+                t = time_pass(ctx, lambda: [fn(ws[0]) for ws in copies], len(copies))
+                tf = flops / (t["us"] * 1e-6) / 1e12
+                res[label] = {"us": t["us"], "TFLOPs": round(tf, 1), "frac": round(tf / PEAK_TFLOPS[act], 4)}
             row[act] = res
-        out[name] = {"m": m, "n": n, "k": k, **row}
+        out[name] = row
+        arena.release()
+    return out
+
+
+def time_prefill_layer(ctx, weights, m: int = 512) -> dict:
+    """All seven projections of an 8B layer at M = 512 as a model issues them:
+    q|k|v as one grouped launch on one requantization, o, gate|up grouped, and
+    down (4 requantizations + 4 GEMMs), against the seven projections launched
+    one by one (7 + 7). Eight distinct layers of the step per pass (0.82 GB of
+    weights, cold)."""
+    per = len(LAYER)
+    layers = [{name: w for (name, _, _, w) in weights[li * per:(li + 1) * per]} for li in range(8)]
+    for lw in layers:
+        for w in lw.values():
+            w.prepare_prefill()
+    dims = {name: (n, k) for name, n, k in LAYER}
+    ctx.reserve_prefill(m, 12288)
+    xb = {k: ctx.buffer(m * k * 2) for k in {k for (_, k) in dims.values()}}
+    for k, b in xb.items():
+        ctx.synth_bf16(3, 1.0, m * k, b)
+    ys = {name: ctx.buffer(m * n * 4) for name, (n, _) in dims.items()}
+    flops = sum(2.0 * m * n * k for (n, k) in dims.values())
+    out = {"m": m, "flops": flops, "layers_per_pass": len(layers)}
+    for act, code in (("mxfp4", mx4hip.ACT_MXFP4), ("mxfp8", mx4hip.ACT_MXFP8)):
+        def grouped():
+            for lw in layers:
+                ctx.matmul_prefill_group(xb[4096], mx4hip.BF16, m, [lw["q"], lw["k"], lw["v"]], code,
+                                         [ys["q"], ys["k"], ys["v"]])
+                ctx.matmul_prefill(xb[4096], mx4hip.BF16, m, lw["o"], code, ys["o"])
+                ctx.matmul_prefill_group(xb[4096], mx4hip.BF16, m, [lw["gate"], lw["up"]], code,
+                                         [ys["gate"], ys["up"]])
+                ctx.matmul_prefill(xb[12288], mx4hip.BF16, m, lw["down"], code, ys["down"])
+
+        def separate():
+            for lw in layers:
+                for name, (_, k) in dims.items():
+                    ctx.matmul_prefill(xb[k], mx4hip.BF16, m, lw[name], code, ys[name])
+
+        res = {}
+        for label, fn in (("grouped", grouped), ("separate", separate)):
+            t = time_pass(ctx, fn, len(layers))
+            tf = flops / (t["us"] * 1e-6) / 1e12
+            res[label] = {"us": t["us"], "TFLOPs": round(tf, 1), "frac": round(tf / PEAK_TFLOPS[act], 4)}
+        out[act] = res
+    return out
+
+
+def time_prefill_exact(ctx, ms=(33, 128, 512)) -> dict:
+    """The exact path a drop-in call takes for M > 32 (AUTO: bf16 x, no
+    requantization, f32 accumulation of exact products) on the 8B q/gate/down
+    shapes, over >= 512 MiB of cold copies; TFLOP/s against the dense bf16 MFMA
+    peak (2.5 PFLOP/s)."""
+    out = {}
+    dims = {name: (n, k) for name, n, k in LAYER}
+    for i, name in enumerate(("q", "gate", "down")):
+        n, k = dims[name]
+        arena, copies = rotation(ctx, [(n, k)], 60000 + 1000 * i)
+        row = {"n": n, "k": k, "copies": len(copies)}
+        for m in ms:
+            xb = ctx.buffer(m * k * 2)
+            ctx.synth_bf16(4, 1.0, m * k, xb)
+            yb = ctx.buffer(m * n * 4)
+            t = time_pass(ctx, lambda: [ctx.matmul_ptr(xb.ptr, mx4hip.BF16, m, ws[0], yb.ptr) for ws in copies],
+                          len(copies))
+            tf = 2.0 * m * n * k / (t["us"] * 1e-6) / 1e12
+            row[f"M{m}"] = {"us": t["us"], "TFLOPs": round(tf, 1), "frac_bf16": round(tf / PEAK_TFLOPS["bf16"], 4)}
+        out[name] = row
+        arena.release()
     return out
 
 
@@ -288,135 +392,114 @@ def time_dropin(ctx, weights, x_host: dict, reps: int = 5) -> dict:
     hip = mx4hip.Hip()
     for n, k, packed, scales in host:  # uploads and caches the weights
         hip.matmul(x_host[k], packed, scales)
-    best = None
+    ts = []
     for _ in range(reps):
         t0 = time.perf_counter()
         for n, k, packed, scales in host:
             hip.matmul(x_host[k], packed, scales)
-        t = time.perf_counter() - t0
-        best = t if best is None else min(best, t)
+        ts.append(time.perf_counter() - t0)
     hip.close()
+    t = float(np.median(ts))
     b = sum(gemv_bytes(1, n, k, 4) for (n, k, _, _) in host)
-    return {"calls": len(host), "us_per_call": round(best / len(host) * 1e6, 2),
-            "GBps": round(b / best / 1e9, 1), "bytes": b,
-            "sample": "layer 0 (q, k, v, o, gate, up, down) + lm_head, f32 x, host buffers, one call each"}
+    return {"calls": len(host), "us_per_call": round(t / len(host) * 1e6, 2),
+            "GBps": round(b / t / 1e9, 1), "bytes": b,
+            "sample": "layer 0 (q, k, v, o, gate, up, down) + lm_head, f32 x, host buffers, one call each, "
+                      f"median of {reps}"}
 
 
-def time_model_1p7b(ctx, steps: int, warmup: int, reps: int = 3) -> dict:
+def time_step(ctx, p, steps: int, reps: int = REPS, warm: int = WARM) -> float:
+    """Median GPU milliseconds per step over `reps` runs of `steps` replays."""
+    for _ in range(warm):
+        p.launch()
+    ctx.synchronize()
+    ts = []
+    for _ in range(reps):
+        ctx.timer_begin()
+        for _ in range(steps):
+            p.launch()
+        ts.append(ctx.timer_end() / steps)
+    return float(np.median(ts))
+
+
+def time_model_1p7b(ctx, steps: int) -> dict:
     """The Qwen3-1.7B decode step at M = 1 (28 layers, 0.92 GB of distinct
-    resident weights), grouped and recorded like the 8B step, plus its
-    per-shape figures. The weights are released afterwards."""
-    weights = build_step(ctx, LAYER_1P7B, LM_HEAD_1P7B, LAYERS_1P7B, seed0=2000)
+    resident weights, cold), grouped and recorded like the 8B step, plus its
+    per-shape figures over cold copies."""
+    weights, arena = build_step(ctx, LAYER_1P7B, LM_HEAD_1P7B, LAYERS_1P7B, seed0=2000)
     xs = {}
     for k in sorted({k for (_, _, k, _) in weights}):
         xs[k] = ctx.buffer(k * 2)
         ctx.synth_bf16(1, 1.0, k, xs[k])
-    ys = {n: ctx.buffer(n * 4) for n in sorted({n for (_, n, _, _) in weights})}
     yq = {name: ctx.buffer(n * 4) for name, n, _ in LAYER_1P7B + [LM_HEAD_1P7B]}
     step_bytes = sum(gemv_bytes(1, n, k) for (_, n, k, _) in weights)
     p = ctx.record(lambda: enqueue_grouped_step(ctx, weights, xs, yq, LAYER_1P7B, LAYERS_1P7B))
-    for _ in range(warmup):
-        p.launch()
-    ctx.synchronize()
-    best = None
-    for _ in range(reps):
-        ctx.synchronize()
-        ctx.timer_begin()
-        for _ in range(steps):
-            p.launch()
-        ms = ctx.timer_end() / steps
-        best = ms if best is None else min(best, ms)
+    ms = time_step(ctx, p, steps)
     p.release()
-    gbps = step_bytes / (best * 1e-3) / 1e9
-    out = {"workload": "qwen3-1.7b decode step, M=1: 28 layers x 7 projections + lm_head (197 GEMVs, "
-                       f"{LAYERS_1P7B * 4 + 1} launches)",
-           "bytes_per_step": step_bytes, "ms_per_step": round(best, 4), "GBps": round(gbps, 1),
-           "frac": round(gbps / HBM_PEAK_GBS, 4),
-           "shapes": time_shapes(ctx, weights, xs, ys, layer=LAYER_1P7B)}
-    ctx.synchronize()
-    for (_, _, _, w) in weights:
-        w.release()
-    return out
+    arena.release()
+    gbps = step_bytes / (ms * 1e-3) / 1e9
+    return {"workload": "qwen3-1.7b decode step, M=1: 28 layers x 7 projections + lm_head (197 GEMVs, "
+                        f"{LAYERS_1P7B * 4 + 1} launches)",
+            "bytes_per_step": step_bytes, "ms_per_step": round(ms, 4), "GBps": round(gbps, 1),
+            "frac": round(gbps / HBM_PEAK_GBS, 4),
+            "shapes": time_shapes(ctx, xs, LAYER_1P7B, LM_HEAD_1P7B, seed0=70000)}
 
 
-def time_config1(ctx, reps: int = 5) -> dict:
-    """The single GEMV of the CPU reference case: W 6144 x 2048 from seed 0,
-    x bf16 [1, 2048] from seed 1, y f32 [1, 6144]; 8 calls per recorded pass
-    on the same (warm) weight."""
+def time_config1(ctx) -> dict:
+    """The single GEMV of the CPU reference case: W 6144 x 2048 (seed 0; the
+    cold figure also uses copies of the same recipe), x bf16 [1, 2048] from
+    seed 1, y f32 [1, 6144]. Cold: over >= 512 MiB of distinct copies. Warm:
+    the seed-0 weight called repeatedly (served from the Infinity Cache after
+    the first call; not an HBM figure)."""
     n, k = 6144, 2048
-    w = ctx.synth_weight(0, n, k, 0.02)
     x = ctx.buffer(k * 2)
     ctx.synth_bf16(1, 1.0, k, x)
     y = ctx.buffer(n * 4)
-    p = ctx.record(lambda: [ctx.matmul_ptr(x.ptr, mx4hip.BF16, 1, w, y.ptr) for _ in range(8)])
-    p.launch()
-    best = None
-    for _ in range(reps):
-        ctx.synchronize()
-        ctx.timer_begin()
-        p.launch()
-        t = ctx.timer_end() / 8
-        best = t if best is None else min(best, t)
-    p.release()
+    arena, copies = rotation(ctx, [(n, k)], 80000)
+    cold = time_pass(ctx, lambda: [ctx.matmul_ptr(x.ptr, mx4hip.BF16, 1, ws[0], y.ptr) for ws in copies],
+                     len(copies))
+    arena.release()
+    w = ctx.synth_weight(0, n, k, 0.02)
+    warm = time_pass(ctx, lambda: [ctx.matmul_ptr(x.ptr, mx4hip.BF16, 1, w, y.ptr) for _ in range(16)], 16)
     ctx.synchronize()
     w.release()
     b = gemv_bytes(1, n, k)
-    return {"n": n, "k": k, "bytes": b, "us": round(best * 1e3, 3), "GBps": round(b / (best * 1e-3) / 1e9, 1)}
+    return {"n": n, "k": k, "cold": hbm_entry(cold, b, {"copies": len(copies)}),
+            "warm_infinity_cache": {"us": warm["us"], "GBps": round(b / (warm["us"] * 1e-6) / 1e9, 1)}}
 
 
-def time_prefill_layer(ctx, weights, m: int = 512, reps: int = 5) -> dict:
-    """All seven projections of one 8B layer at M = 512 as a model issues them:
-    q|k|v as one grouped launch on one requantization, o, gate|up grouped, and
-    down (4 requantizations + 4 GEMMs), against the seven projections launched
-    one by one (7 + 7). Layer 0's weights; 8 layers per recorded pass."""
-    lw = {name: w for (name, _, _, w) in weights[:len(LAYER)]}
-    for w in lw.values():
-        w.prepare_prefill()
-    dims = {name: (n, k) for name, n, k in LAYER}
-    ctx.reserve_prefill(m, max(k for (_, k) in dims.values()))
-    xb = {k: ctx.buffer(m * k * 2) for k in {k for (_, k) in dims.values()}}
-    for k, b in xb.items():
-        ctx.synth_bf16(3, 1.0, m * k, b)
-    ys = {name: ctx.buffer(m * n * 4) for name, (n, _) in dims.items()}
-    flops = sum(2.0 * m * n * k for (n, k) in dims.values())
-    peaks = {"mxfp4": 10.1e15, "mxfp8": 5.0e15}
-    out = {"m": m, "flops": flops}
-    for act, code in (("mxfp4", mx4hip.ACT_MXFP4), ("mxfp8", mx4hip.ACT_MXFP8)):
-        def grouped():
-            ctx.matmul_prefill_group(xb[4096], mx4hip.BF16, m, [lw["q"], lw["k"], lw["v"]], code,
-                                     [ys["q"], ys["k"], ys["v"]])
-            ctx.matmul_prefill(xb[4096], mx4hip.BF16, m, lw["o"], code, ys["o"])
-            ctx.matmul_prefill_group(xb[4096], mx4hip.BF16, m, [lw["gate"], lw["up"]], code, [ys["gate"], ys["up"]])
-            ctx.matmul_prefill(xb[12288], mx4hip.BF16, m, lw["down"], code, ys["down"])
+# ---------------------------------------------------------------- CPU legs
 
-        def separate():
-            for name, (_, k) in dims.items():
-                ctx.matmul_prefill(xb[k], mx4hip.BF16, m, lw[name], code, ys[name])
-
-        res = {}
-        for label, fn in (("grouped", grouped), ("separate", separate)):
-            p = ctx.record(lambda: [fn() for _ in range(8)])
-            p.launch()
-            best = None
-            for _ in range(reps):
-                ctx.synchronize()
-                ctx.timer_begin()
-                p.launch()
-                t = ctx.timer_end() / 8
-                best = t if best is None else min(best, t)
-            p.release()
-            tf = flops / (best * 1e-3)
-            res[label] = {"us": round(best * 1e3, 2), "TFLOPs": round(tf / 1e12, 1), "frac": round(tf / peaks[act], 4)}
-        out[act] = res
-    return out
+def host_threads() -> int:
+    """Threads this process may use: the scheduler's CPU set, capped by OMP_NUM_THREADS when set."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(env))) if env.isdigit() else n
 
 
-def cpu_baseline(ctx, weights, x_host: dict, layers: int = 9, threads: int = 1) -> dict:
-    """The oracle on the host: `threads` threads, `layers` layers + the matching share of lm_head."""
+def host_cpu() -> dict:
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": model, "box_logical_cpus": os.cpu_count(),
+            "lease_cpus": len(os.sched_getaffinity(0)), "threads_used_all": host_threads()}
+
+
+def _oracle():
     from oracle import mx4_oracle as oracle
 
     if not oracle.LIB_PATH.exists():
         oracle.build()
+    return oracle
+
+
+def cpu_baseline(ctx, weights, x_host: dict, layers: int = 9, threads: int = 1) -> dict:
+    """The oracle on the host: `threads` threads, `layers` layers + the matching share of lm_head."""
+    oracle = _oracle()
     jobs = []
     for name, n, k, w in weights[: layers * len(LAYER)]:
         jobs.append((n, k, w, n))
@@ -437,12 +520,214 @@ def cpu_baseline(ctx, weights, x_host: dict, layers: int = 9, threads: int = 1) 
                       "engine/src/lib.rs:240-266"}
 
 
-def host_threads() -> int:
-    """Threads this process may use: the scheduler's CPU set, capped by OMP_NUM_THREADS when set."""
-    n = len(os.sched_getaffinity(0))
-    env = os.environ.get("OMP_NUM_THREADS", "")
-    return max(1, min(n, int(env))) if env.isdigit() else n
+def _rows_for(work_macs: float, per_row_macs: int, n: int) -> int:
+    return int(min(n, max(16, -(-int(work_macs) // per_row_macs))))
 
+
+def cpu_verify(ctx, weights, threads: int) -> dict:
+    """Config 4 on the host: each 8B shape at M = 2, 4, 8, 16 (bf16 N(0, 1) rows,
+    seed 2), the oracle over the first R weight rows (about 5e6 multiply-adds
+    per thread), extrapolated to all N rows: us per call = t * N / R."""
+    oracle = _oracle()
+    first = {name: w for (name, _, _, w) in weights}
+    out = {}
+    for name, n, k in LAYER + [LM_HEAD]:
+        packed, scales = ctx.download_weight(first[name])
+        row = {}
+        for m in (2, 4, 8, 16):
+            x = oracle.bf16_to_f32(oracle.synth_bf16(2, 1.0, m * k)).reshape(m, k)
+            r = _rows_for(5e6 * threads, m * k, n)
+            t0 = time.perf_counter()
+            oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), 0, r, threads=threads)
+            t = time.perf_counter() - t0
+            us = t * n / r * 1e6
+            row[f"M{m}"] = {"rows": r, "us_per_call": round(us, 1),
+                            "GBps": round(gemv_bytes(m, n, k) / (us * 1e-6) / 1e9, 4)}
+        out[name] = row
+    return {"threads": threads, "shapes": out,
+            "method": "oracle over the first R of N weight rows (all M token rows), us_per_call = time * N / R"}
+
+
+def cpu_prefill(ctx, weights, threads: int) -> dict:
+    """Config 5 on the host: each 8B q/o/gate/up/down shape at M = 512, the
+    oracle (no requantization: engine/src/lib.rs:240-266 on the bf16 rows) over
+    8 of the 512 token rows and the first R weight rows (about 5e6
+    multiply-adds per thread), extrapolated: seconds per call = t * (512 / 8)
+    * (N / R)."""
+    oracle = _oracle()
+    first = {name: w for (name, _, _, w) in weights}
+    out = {}
+    m, mt = 512, 8
+    for name, n, k in LAYER:
+        if name in ("k", "v"):
+            continue
+        packed, scales = ctx.download_weight(first[name])
+        x = oracle.bf16_to_f32(oracle.synth_bf16(3, 1.0, mt * k)).reshape(mt, k)
+        r = _rows_for(5e6 * threads, mt * k, n)
+        t0 = time.perf_counter()
+        oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), 0, r, threads=threads)
+        t = time.perf_counter() - t0
+        s = t * (m / mt) * (n / r)
+        out[name] = {"rows": r, "token_rows": mt, "s_per_call": round(s, 3),
+                     "GFLOPs": round(2.0 * m * n * k / s / 1e9, 3)}
+    return {"threads": threads, "m": m, "shapes": out,
+            "method": "oracle over 8 of 512 token rows and the first R of N weight rows, "
+                      "s_per_call = time * 64 * N / R"}
+
+
+# ---------------------------------------------------------------- profiles
+
+def traffic_from_profile() -> tuple[int | None, str]:
+    """HBM bytes per step from the committed counter summary, when its stamp
+    names the library this process loaded."""
+    if not TRAFFIC_PROFILE.exists():
+        return None, "no traffic profile"
+    fields = {}
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        if ":" in line and not line.startswith(("|", " ", "#")):
+            key, val = line.split(":", 1)
+            fields[key.strip()] = val.strip()
+    sha = library_sha256()
+    if fields.get("library_sha256") != sha:
+        return None, f"profile stamp {fields.get('library_sha256', 'missing')[:12]} != loaded library {sha[:12]}"
+    return int(fields["hbm_bytes_per_step"]), f"profile stamp matches the loaded library ({sha[:12]})"
+
+
+def write_stamp(path: str | None, info: dict) -> None:
+    info = dict(info)
+    info["library_sha256"] = library_sha256()
+    print(json.dumps(info), flush=True)
+    if path:
+        Path(path).parent.mkdir(parents=True, exist_ok=True)
+        Path(path).write_text(json.dumps(info) + "\n")
+
+
+def _read_csv(d: Path, suffix: str) -> list[dict]:
+    files = sorted(d.glob(f"*{suffix}"))
+    if not files:
+        raise SystemExit(f"no *{suffix} under {d}")
+    with open(files[0], newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _short(name: str) -> str:
+    name = name.replace("(anonymous namespace)::", "")
+    return name.split("(")[0] if not name.startswith("void ") else name[5:].split("(")[0]
+
+
+def _stamp_of(d: Path) -> dict:
+    f = d / "stamp.json"
+    return json.loads(f.read_text()) if f.exists() else {}
+
+
+def _git_head() -> str:
+    try:
+        return subprocess.run(["git", "-C", str(ROOT), "rev-parse", "--short=12", "HEAD"], capture_output=True,
+                              text=True, check=True).stdout.strip()
+    except (OSError, subprocess.CalledProcessError):
+        return "unknown"
+
+
+def summarize(kind: str, dirs: list[str]) -> None:
+    """Markdown summaries of rocprofv3 CSV output (run here, on the pulled-back
+    files): `trace DIR` (kernel stats of --profile-step), `traffic FETCH_DIR
+    WRITE_DIR` (FETCH_SIZE / WRITE_SIZE of --profile-traffic, calibrated by the
+    1 GiB copy), `prefill-trace DIR` and `prefill-pmc DIR` (--profile-prefill)."""
+    d0 = Path(dirs[0])
+    st = _stamp_of(d0)
+    print(f"commit: {_git_head()}")
+    print(f"library_sha256: {st.get('library_sha256', 'unknown')}")
+    if kind == "trace":
+        rows = _read_csv(d0, "kernel_stats.csv")
+        steps = st.get("steps", 0) + st.get("warmup", 0)
+        print(f"steps_traced: {steps}\n")
+        print("| kernel | calls | calls per step | average us | min us | max us |")
+        print("|---|---|---|---|---|---|")
+        step_us = 0.0
+        for r in rows:
+            nm = _short(r["Name"])
+            calls = int(r["Calls"])
+            avg = float(r["AverageNs"]) / 1e3
+            per = calls / steps if steps else 0
+            if nm.startswith("mx4::gemv"):
+                step_us += avg * per
+            print(f"| {nm} | {calls} | {per:.0f} | {avg:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                  f"{float(r['MaxNs']) / 1e3:.2f} |")
+        print(f"\nsum of GEMV kernel durations per step: {step_us:.1f} us")
+    elif kind == "traffic":
+        cal = st.get("calibration_copy_bytes", 1 << 30)
+        steps = st.get("steps", 2)
+        out = {}
+        for d, counter in ((Path(dirs[0]), "FETCH_SIZE"), (Path(dirs[1]), "WRITE_SIZE")):
+            rows = _read_csv(d, "counter_collection.csv")
+            per = defaultdict(lambda: [0, 0.0])
+            copy_kib = 0.0
+            for r in rows:
+                if r["Counter_Name"] != counter:
+                    continue
+                nm = _short(r["Kernel_Name"])
+                v = float(r["Counter_Value"])
+                if "copyBuffer" in nm or "copy" in nm.lower() and not nm.startswith("mx4::"):
+                    copy_kib += v
+                elif nm.startswith("mx4::gemv"):
+                    per[nm][0] += 1
+                    per[nm][1] += v
+            factor = cal / (copy_kib * 1024) if counter == "FETCH_SIZE" else (cal / (copy_kib * 1024))
+            out[counter] = (per, factor, copy_kib)
+        fper, ff, fcopy = out["FETCH_SIZE"]
+        wper, wf, wcopy = out["WRITE_SIZE"]
+        print(f"calibration: {cal} B device copy read {fcopy:.1f} KiB FETCH_SIZE and wrote {wcopy:.1f} KiB "
+              f"WRITE_SIZE -> factors {ff:.4f}, {wf:.4f}\n")
+        print("| kernel | launches per step | HBM fetch MB per step | HBM write MB per step |")
+        print("|---|---|---|---|")
+        tf = tw = 0.0
+        for nm in sorted(fper):
+            n, fk = fper[nm]
+            wk = wper.get(nm, [0, 0.0])[1]
+            fb, wb = fk * 1024 * ff / steps, wk * 1024 * wf / steps
+            tf += fb
+            tw += wb
+            print(f"| {nm} | {n / steps:.0f} | {fb / 1e6:.2f} | {wb / 1e6:.3f} |")
+        alg = st.get("bytes_per_step", 0)
+        print(f"\nper step: HBM fetch {tf:.6g} B, write {tw:.6g} B, total {tf + tw:.6g} B; algorithmic {alg} B; "
+              f"ratio {(tf + tw) / alg if alg else 0:.4f}\n")
+        print(f"hbm_bytes_per_step: {int(round(tf + tw))}")
+    elif kind == "prefill-trace":
+        rows = _read_csv(d0, "kernel_trace.csv")
+        per = defaultdict(list)
+        for r in rows:
+            nm = _short(r["Kernel_Name"])
+            if nm.startswith("mx4::prefill") or nm.startswith("mx4::quantize_fragments"):
+                per[(nm, r["Grid_Size"])].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        print("\n| kernel | grid | dispatches | median us | min us |")
+        print("|---|---|---|---|---|")
+        for (nm, g), ts in sorted(per.items()):
+            print(f"| {nm} | {g} | {len(ts)} | {np.median(ts):.2f} | {min(ts):.2f} |")
+    elif kind == "prefill-pmc":
+        rows = _read_csv(d0, "counter_collection.csv")
+        per = defaultdict(lambda: defaultdict(float))
+        meta = {}
+        for r in rows:
+            nm = _short(r["Kernel_Name"])
+            if not nm.startswith("mx4::prefill"):
+                continue
+            did = r["Dispatch_Id"]
+            per[did][r["Counter_Name"]] += float(r["Counter_Value"])
+            meta[did] = (nm, r["Grid_Size"])
+        groups = defaultdict(list)
+        for did, c in per.items():
+            groups[meta[did]].append(c)
+        names = sorted({cn for c in per.values() for cn in c})
+        print("\n| kernel | grid | dispatches | " + " | ".join(names) + " |")
+        print("|---|---|---|" + "---|" * len(names))
+        for (nm, g), lst in sorted(groups.items()):
+            avg = [sum(c.get(cn, 0.0) for c in lst) / len(lst) for cn in names]
+            print(f"| {nm} | {g} | {len(lst)} | " + " | ".join(f"{v:.4g}" for v in avg) + " |")
+    else:
+        raise SystemExit(f"unknown summary kind {kind}")
+
+
+# ---------------------------------------------------------------- main
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
@@ -456,12 +741,22 @@ def main() -> int:
     ap.add_argument("--no-skinny", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-1p7b", action="store_true", help="skip the Qwen3-1.7B step and the single config-1 GEMV")
+    ap.add_argument("--profile-step", action="store_true",
+                    help="for kernel traces: only the recorded decode step (warmup + steps replays)")
     ap.add_argument("--profile-traffic", action="store_true",
                     help="for counter runs: 2 eager grouped steps, then a 1 GiB device copy as the byte calibration")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="for profiler runs: only the M=512 prefill (q, o, gate, up, down; MXFP4 and MX-FP8 "
                          "activations): 5 GEMMs on requantized activations, then 5 requantize + GEMM calls")
+    ap.add_argument("--stamp", help="profile modes: also write the stamp (library sha256, workload) to this file")
+    ap.add_argument("--summarize", nargs="+", metavar=("KIND", "DIR"),
+                    help="print the markdown summary of rocprofv3 CSV output: trace DIR | traffic FETCH_DIR "
+                         "WRITE_DIR | prefill-trace DIR | prefill-pmc DIR")
     args = ap.parse_args()
+
+    if args.summarize:
+        summarize(args.summarize[0], args.summarize[1:])
+        return 0
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (the GEMV would shard "
@@ -474,8 +769,8 @@ def main() -> int:
         return 1
 
     ctx = mx4hip.Context(0)
-    log("synthesizing 253 resident MXFP4 weights (4.03 GB) on the GPU")
-    weights = build_step(ctx)
+    log("synthesizing 253 resident MXFP4 weights (4.03 GB, one arena) on the GPU")
+    weights, arena = build_step(ctx)
 
     ks = sorted({k for (_, _, k, _) in weights})
     x_host = {}
@@ -501,11 +796,13 @@ def main() -> int:
     else:
         enqueue = enqueue_grouped
         launches = LAYERS * 4 + 1
+
     if args.profile_prefill:
         m = 512
         by = {}
         for (nm, n, k, w) in weights:
             by.setdefault(nm, (n, k, w))
+        ctx.reserve_prefill(m, 12288)
         for name in ("q", "o", "gate", "up", "down"):
             n, k, w = by[name]
             w.prepare_prefill()
@@ -520,8 +817,8 @@ def main() -> int:
                 for _ in range(5):
                     ctx.matmul_prefill(xb, mx4hip.BF16, m, w, code, yb)
             ctx.synchronize()
-        print(json.dumps({"profile_prefill": True, "m": m, "gemm_launches_per_shape_and_format": 10,
-                          "requant_launches_per_shape_and_format": 6}), flush=True)
+        write_stamp(args.stamp, {"profile_prefill": True, "m": m, "gemm_launches_per_shape_and_format": 10,
+                                 "requant_launches_per_shape_and_format": 6})
         ctx.close()
         return 0
 
@@ -532,18 +829,28 @@ def main() -> int:
         src, dst = ctx.buffer(1 << 30), ctx.buffer(1 << 30)
         mx4hip.check(mx4hip.lib().mx4_copy(ctx.handle, dst.ptr, src.ptr, 1 << 30))
         ctx.synchronize()
-        print(json.dumps({"profile_traffic": True, "steps": 2, "launches_per_step": launches,
-                          "bytes_per_step": step_bytes, "calibration_copy_bytes": 1 << 30}), flush=True)
+        write_stamp(args.stamp, {"profile_traffic": True, "steps": 2, "launches_per_step": launches,
+                                 "bytes_per_step": step_bytes, "calibration_copy_bytes": 1 << 30})
         ctx.close()
         return 0
 
     if args.eager:
         step = enqueue
         launch = f"eager, {launches} launches per step"
+        pss = None
     else:
         pss = ctx.record(enqueue)
         step = pss.launch
         launch = f"recorded pass (HIP graph), {launches} launches per step"
+
+    if args.profile_step:
+        for _ in range(args.warmup + args.steps):
+            step()
+        ctx.synchronize()
+        write_stamp(args.stamp, {"profile_step": True, "steps": args.steps, "warmup": args.warmup,
+                                 "launches_per_step": launches, "bytes_per_step": step_bytes})
+        ctx.close()
+        return 0
 
     for _ in range(args.warmup):
         step()
@@ -561,46 +868,54 @@ def main() -> int:
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     achieved = step_bytes / (gpu_ms_per_step * 1e-3) / 1e9
 
-    extra = {"gpu_ms_per_step": round(gpu_ms_per_step, 4), "launch": launch}
+    extra = {"gpu_ms_per_step": round(gpu_ms_per_step, 4), "launch": launch,
+             "weights": "one device allocation, each weight on its own 2 MiB-aligned slice"}
+    if pss is not None:
+        extra["gpu_ms_per_step_median"] = round(time_step(ctx, pss, max(5, args.steps // 2)), 4)
+        extra["gpu_ms_per_step_median_protocol"] = f"median of {REPS} runs of {max(5, args.steps // 2)} replays"
     if not args.no_shapes:
-        log("per-shape timing")
-        extra["shapes"] = time_shapes(ctx, weights, xs, ys)
-
+        log("per-shape timing (>= 512 MiB of cold copies per shape)")
+        extra["shapes"] = time_shapes(ctx, xs)
         log("lm_head + greedy argmax timing")
-        extra["lm_head_argmax"] = time_lm_head_argmax(ctx, weights, xs)
+        extra["lm_head_argmax"] = time_lm_head_argmax(ctx, xs)
 
     if not args.no_skinny:
         log("skinny (speculative verify) timing")
-        extra["skinny"] = time_skinny(ctx, weights)
+        extra["skinny"] = time_skinny(ctx)
 
     if not args.no_prefill:
         log("prefill (M=512, block-scaled MFMA) timing")
-        extra["prefill"] = time_prefill(ctx, weights)
+        extra["prefill"] = time_prefill(ctx)
         extra["prefill_layer"] = time_prefill_layer(ctx, weights)
+        log("exact matrix-core path for M > 32 (AUTO)")
+        extra["prefill_exact_auto"] = time_prefill_exact(ctx)
 
     if not args.no_1p7b:
         log("qwen3-1.7b decode step and the config-1 GEMV")
-        extra["qwen3_1p7b"] = time_model_1p7b(ctx, max(5, args.steps // 2), max(1, args.warmup))
+        extra["qwen3_1p7b"] = time_model_1p7b(ctx, max(5, args.steps // 2))
         extra["single_gemv_6144x2048"] = time_config1(ctx)
         log("per-call drop-in (host buffers)")
         extra["dropin_per_call"] = time_dropin(ctx, weights, x_host)
 
     cpu = None
     if not args.no_cpu_baseline:
+        nt = host_threads()
+        cpu_extra = {"host": host_cpu()}
         log("cpu baseline (oracle, 1 thread)")
         cpu = cpu_baseline(ctx, weights, x_host)
-        nt = host_threads()
         if nt > 1:
             log(f"cpu baseline (oracle, {nt} threads)")
-            extra["cpu_all_cores"] = cpu_baseline(ctx, weights, x_host, threads=nt)
+            cpu_extra["step_sample_all_threads"] = cpu_baseline(ctx, weights, x_host, threads=nt)
+        log("cpu legs: verify (config 4) and prefill (config 5)")
+        cpu_extra["verify_1_thread"] = cpu_verify(ctx, weights, 1)
+        cpu_extra["prefill_1_thread"] = cpu_prefill(ctx, weights, 1)
+        if nt > 1:
+            cpu_extra["verify_all_threads"] = cpu_verify(ctx, weights, nt)
+            cpu_extra["prefill_all_threads"] = cpu_prefill(ctx, weights, nt)
+        extra["cpu"] = cpu_extra
 
-    # HBM bytes per step from the committed FETCH_SIZE + WRITE_SIZE counter runs
-    traffic = None
-    tf = ROOT / "profiles" / "gemv_qwen3_8b_m1_step_traffic.md"
-    if tf.exists() and not args.separate:
-        for line in tf.read_text().splitlines():
-            if line.startswith("hbm_bytes_per_step:"):
-                traffic = int(line.split(":")[1])
+    traffic, traffic_note = (None, "--separate launches differ from the profiled step") if args.separate \
+        else traffic_from_profile()
 
     out = {
         "metric": "MXFP4 GEMV HBM GB/s + % peak, Qwen3-8B M=1; M=512 prefill TFLOP/s",
@@ -621,12 +936,14 @@ def main() -> int:
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "M=1 GEMV (gemv_m1_head_kernel, gemv_m1_one_kernel: all launches of the step)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,
                      "basis": "algorithmic bytes of one decode step / GPU event time of one step"},
         "cpu_baseline": cpu,
         "extra": extra,
     }
     print(json.dumps(out), flush=True)
+    ctx.synchronize()
+    arena.release()
     ctx.close()
     return 0
 
