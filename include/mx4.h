@@ -56,7 +56,8 @@ typedef enum mx4_path {
     MX4_PATH_GEMV = 1,     /* decode GEMV (no MFMA): M == 1, or 2 <= M <= 4 with bf16 x */
     MX4_PATH_SKINNY = 2,   /* exact skinny kernel on bf16 MFMA, M <= 32, K in {2,4,6,8,12}*1024 */
     MX4_PATH_GENERIC = 3,  /* exact fallback for any M and K % 32 == 0 */
-    MX4_PATH_PREFILL = 4   /* block-scaled MFMA on requantized activations */
+    MX4_PATH_PREFILL = 4,  /* block-scaled MFMA on requantized activations */
+    MX4_PATH_GEMM = 5      /* exact tiled GEMM on bf16 MFMA, any M, K % 128 == 0 */
 } mx4_path;
 
 /* Activation format on the block-scaled MFMA path (north-star prefill). */
@@ -150,8 +151,12 @@ mx4_status mx4_weight_info(const mx4_weight *w, uint32_t *rows, uint32_t *cols,
 
 /* GpuModel::matmul (engine/src/gpu.rs:469-515): y_dev[m][rows] =
  * x_dev[m][cols] . W^T, enqueued on the context stream, exact arithmetic
- * (f32 accumulation of exact products). AUTO picks GEMV for m == 1, the exact
- * skinny kernel for 2 <= m <= 32 and the exact generic kernel beyond. */
+ * (f32 accumulation of exact products). AUTO picks GEMV for m == 1, the
+ * few-token GEMV or the exact skinny kernel for 2 <= m <= 32, and the exact
+ * tiled GEMM on bf16 MFMA (MX4_PATH_GEMM) beyond -- the analogue of the
+ * reference's M > 32 GEMM (engine/src/matmul.metal:65-97). Shapes the fast
+ * kernels do not take (K not a multiple of 128, scale bytes outside 2..252)
+ * run the exact generic kernel. */
 mx4_status mx4_matmul(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m,
                       const mx4_weight *w, float *y_dev);
 /* The same with an explicit kernel family (MX4_PATH_PREFILL is not exact:
@@ -182,6 +187,13 @@ mx4_status mx4_gemv_config(mx4_context *ctx, const void *x_dev, mx4_dtype x_type
  * keeps the default; a shape that cannot be launched gives MX4_ERR_UNSUPPORTED. */
 mx4_status mx4_gemv_tokens_config(mx4_context *ctx, const void *x_dev, uint32_t m, const mx4_weight *w,
                                   float *y_dev, uint32_t teams, uint32_t teams_per_workgroup);
+
+/* Tuning hook for the exact tiled GEMM (MX4_PATH_GEMM): waves per workgroup
+ * along M and N and 32x32 MFMA tiles per wave along M and N, one of the
+ * compiled instances (2x2 waves of 2x2, 2x1, 1x2 or 1x1 tiles; 4x1 waves of
+ * 1x2 tiles); MX4_ERR_UNSUPPORTED otherwise. Zeros keep the default. */
+mx4_status mx4_gemm_config(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m, const mx4_weight *w,
+                           float *y_dev, int waves_m, int waves_n, int tiles_m, int tiles_n);
 
 /* Prefill on CDNA4 block-scaled MFMA (V_MFMA_SCALE_F32_*_F8F6F4): x is
  * requantized per 32 along K (MXFP4 by python/quantize_mxfp4.py:18-39, or MX

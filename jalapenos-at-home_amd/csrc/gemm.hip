@@ -1,0 +1,340 @@
+// gemm.hip -- exact matrix-core GEMM for more than 32 token rows:
+// y[m, r] = sum_k x[m, k] * w(r, k), f32 accumulation of exact products.
+//
+// The reference sends every projection with M > 32 token rows (and, through
+// its per-call bridge, every M > 1) to a tiled FP32 GEMM that decodes the
+// weights into threadgroup tiles (project_mxfp4, engine/src/matmul.metal:65-97;
+// dispatch engine/src/gpu.rs:510-514, engine/src/metal.m:103-105). Here the
+// multiply-accumulate runs on gfx950's V_MFMA_F32_32X32X16_BF16 while the
+// weights stay 4-bit in HBM, in the stored row-major layout:
+//  * a workgroup owns a BM x BN output tile (token rows x weight rows) and
+//    walks K in stages of 128. Each stage's activations (BM rows x 256 bytes
+//    of bf16) and weights (BN rows x 64 packed bytes + 4 scale bytes) are
+//    loaded straight into LDS (direct-to-LDS buffer loads, whole rows per
+//    instruction) into a ring of D stages, D - 1 of them in flight while one
+//    is computed (one barrier per stage);
+//  * a wave owns TM x TN 32x32 MFMA tiles. Lane l (row l % 32, half h = l / 32)
+//    takes elements [64h, 64h + 64) of the stage for both operands; k-step s
+//    of the stage contracts elements [64h + 8s, +8). The contraction is over
+//    K, so this order, shared by A and B, changes nothing in the result;
+//  * a weight lane reads its row's 32 packed bytes once per stage and decodes
+//    8 elements per k-step with the hardware E2M1 converter, the E8M0 scale
+//    folded in (exact in bf16 for scale bytes 2..252, which the dispatcher
+//    guarantees);
+//  * bf16 activations are exact operands; f32 activations are split into three
+//    bf16 terms hi + mid + lo (24 significant bits), three MFMAs each, so every
+//    product is exact and only the f32 summation order differs from the
+//    reference's sequential loop (engine/src/lib.rs:240-266);
+//  * every global load goes through a buffer resource: token rows >= M and
+//    weight rows >= N read as zeros without touching memory, and their outputs
+//    are not stored.
+#include "mx4_device.h"
+#include "mx4_kernels.h"
+
+namespace mx4 {
+
+namespace {
+
+// Three bf16 terms of eight f32 values, hi + mid + lo = x exactly.
+__device__ __forceinline__ void split3x8(const f32x4 a, const f32x4 b, bf16x8& hi, bf16x8& mid, bf16x8& lo) {
+    const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const __bf16 h = (__bf16)v[e];
+        const float r1 = v[e] - (float)h;
+        const __bf16 md = (__bf16)r1;
+        const float r2 = r1 - (float)md;
+        hi[e] = h;
+        mid[e] = md;
+        lo[e] = (__bf16)r2;
+    }
+}
+
+// Eight weights of one lane at one k-step: packed word `word` (elements
+// [8s, 8s + 8) of the lane's 64), block scale 2^(s - 127) folded in.
+__device__ __forceinline__ bf16x8 decode8(uint32_t word, float sc) {
+    const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 0);
+    const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 1);
+    const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 2);
+    const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 3);
+    bf16x8 r;
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+    return r;
+}
+
+// Wait states after the last MFMAs before their accumulators are read (the
+// compiler has placed such reads after a branch without them on gfx950).
+__device__ __forceinline__ void mfma_drain() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// LDS barrier that does not wait for outstanding global loads (the next
+// stage's prefetch stays in flight across it).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+constexpr int kBK = 128;  // K elements per stage
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// Direct-to-LDS buffer loads of 16 or 4 bytes per lane: lane l's bytes land
+// at dst + l * size. (Only the device pass sees the builtin: the host pass
+// checks the size against its own target, rejects 16, and would then drop
+// the kernels' launch stubs without a word.)
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, lds_ptr dst, uint32_t voffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voffset, 0, 0, 0);
+#else
+    (void)r; (void)dst; (void)voffset;
+#endif
+}
+__device__ __forceinline__ void load_lds4(__amdgpu_buffer_rsrc_t r, lds_ptr dst, uint32_t voffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 4, voffset, 0, 0, 0);
+#else
+    (void)r; (void)dst; (void)voffset;
+#endif
+}
+
+// Stage layout in LDS (no padding): activations BM rows x A_CPR 16-byte slots,
+// packed weights BN rows x 4 slots, then BN scale words. Slots are written by
+// direct-to-LDS buffer loads, lane l of a load instruction at slot base + l,
+// so the layout is chosen through which global chunk each lane loads: chunk c
+// of row r sits in slot c ^ (r % 16) of an activation row and c ^ ((r / 4) % 4)
+// of a weight row. The MFMA-operand reads (32 rows, one logical chunk) then
+// spread over all LDS banks.
+template <bool XBF16, int WM, int WN, int TM, int TN, int D>
+struct Geometry {
+    static constexpr int NW = WM * WN, NT = 64 * NW;
+    static constexpr int BM = 32 * TM * WM, BN = 32 * TN * WN;
+    static constexpr int XB = XBF16 ? 2 : 4;              // bytes per activation element
+    static constexpr int A_CPR = kBK * XB / 16;           // 16-byte chunks per activation row
+    static constexpr int A_BYTES = BM * A_CPR * 16, B_BYTES = BN * 4 * 16, S_BYTES = BN * 4;
+    static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+    static constexpr int A_INSTR = BM * A_CPR / NT;       // 64-lane loads per wave per stage
+    static constexpr int B_INSTR = BN * 4 / NT;
+    static constexpr int S_ROWS = BN / NW;                // scale words per wave per stage
+    static constexpr int LPS = A_INSTR + B_INSTR + 1;     // vector memory instructions per stage
+    static_assert(BM * A_CPR % NT == 0 && BN * 4 % NT == 0 && BN % NW == 0 && S_ROWS <= 64, "stage split");
+    static_assert(D >= 2 && D <= 4 && (D - 2) * LPS <= 63, "vmcnt range");
+    static_assert(D * STAGE <= 160 * 1024, "the stages must fit the LDS");
+};
+
+template <bool XBF16, int WM, int WN, int TM, int TN, int D>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_exact_kernel(const uint8_t* __restrict__ packed,
+                                                                  const uint8_t* __restrict__ scales,
+                                                                  const void* __restrict__ x, float* __restrict__ y,
+                                                                  uint32_t m, uint32_t n, uint32_t k,
+                                                                  uint32_t tiles_n) {
+    using G = Geometry<XBF16, WM, WN, TM, TN, D>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[D * G::STAGE];
+    const uint32_t lane = threadIdx.x % 64, h = lane / 32, r32 = lane % 32;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t wm = wave / WN, wn = wave % WN;
+    const uint32_t tn = blockIdx.x % tiles_n, tm = blockIdx.x / tiles_n;
+    const uint32_t row0 = tm * G::BM, col0 = tn * G::BN;
+    const uint32_t stages = k / kBK;
+
+    const __amdgpu_buffer_rsrc_t xr = rsrc(x, m * k * G::XB);
+    const __amdgpu_buffer_rsrc_t pr = rsrc(packed, n * (k / 2));
+    const __amdgpu_buffer_rsrc_t sr = rsrc(scales, n * (k / 32));
+
+    // this lane's global offsets (stage 0) of its loads; LDS slot p = (q NW + wave) 64 + lane
+    uint32_t a_goff[G::A_INSTR], b_goff[G::B_INSTR];
+#pragma unroll
+    for (int q = 0; q < G::A_INSTR; ++q) {
+        const uint32_t p = (q * G::NW + wave) * 64 + lane, row = p / G::A_CPR, c = (p % G::A_CPR) ^ (row % 16);
+        a_goff[q] = (row0 + row) * k * G::XB + c * 16;
+    }
+#pragma unroll
+    for (int q = 0; q < G::B_INSTR; ++q) {
+        const uint32_t p = (q * G::NW + wave) * 64 + lane, row = p / 4, c = (p % 4) ^ ((row >> 2) & 3);
+        b_goff[q] = (col0 + row) * (k / 2) + c * 16;
+    }
+    const uint32_t s_row = wave * G::S_ROWS + lane;
+    const uint32_t s_goff = (col0 + s_row) * (k / 32);
+
+    auto issue = [&](uint32_t st, uint32_t slot) {
+        uint8_t* base = lds + slot * G::STAGE;
+#pragma unroll
+        for (int q = 0; q < G::A_INSTR; ++q)
+            load_lds16(xr, (lds_ptr)(base + (q * G::NW + wave) * 1024), a_goff[q] + st * kBK * G::XB);
+#pragma unroll
+        for (int q = 0; q < G::B_INSTR; ++q)
+            load_lds16(pr, (lds_ptr)(base + G::A_BYTES + (q * G::NW + wave) * 1024), b_goff[q] + st * (kBK / 2));
+        // the wave's S_ROWS scale words; lanes past them stay inactive, so they
+        // write nothing into the next wave's words (the instruction still
+        // counts once in vmcnt: lane 0 is always active)
+        if (lane < (uint32_t)G::S_ROWS)
+            load_lds4(sr, (lds_ptr)(base + G::A_BYTES + G::B_BYTES + wave * G::S_ROWS * 4), s_goff + st * (kBK / 32));
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    auto compute = [&](uint32_t slot) {
+        const uint8_t* base = lds + slot * G::STAGE;
+        u32x4 wq[TN][2];
+        uint32_t sw[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint32_t r = (wn * TN + j) * 32 + r32, f = (r >> 2) & 3;
+            const uint8_t* bp = base + G::A_BYTES + r * 64;
+            wq[j][0] = *reinterpret_cast<const u32x4*>(bp + ((2 * h) ^ f) * 16);
+            wq[j][1] = *reinterpret_cast<const u32x4*>(bp + ((2 * h + 1) ^ f) * 16);
+            sw[j] = *reinterpret_cast<const uint32_t*>(base + G::A_BYTES + G::B_BYTES + r * 4);
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            bf16x8 b[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                // elements [64h + 8s, +8) lie in block 2h + s / 4 of the stage
+                const uint32_t sb = (sw[j] >> (8 * (2 * h + s / 4))) & 0xffu;
+                b[j] = decode8(wq[j][s / 4][s % 4], __uint_as_float(sb << 23));
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const uint32_t r = (wm * TM + i) * 32 + r32, sw16 = r % 16;
+                const uint8_t* ap = base + r * (G::A_CPR * 16);
+                if constexpr (XBF16) {
+                    const uint32_t c = (8 * h + s) ^ sw16;
+                    const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ap + c * 16));
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j], acc[i][j], 0, 0, 0);
+                } else {
+                    const uint32_t c0 = (16 * h + 2 * s) ^ sw16, c1 = (16 * h + 2 * s + 1) ^ sw16;
+                    const f32x4 v0 = __builtin_bit_cast(f32x4, *reinterpret_cast<const u32x4*>(ap + c0 * 16));
+                    const f32x4 v1 = __builtin_bit_cast(f32x4, *reinterpret_cast<const u32x4*>(ap + c1 * 16));
+                    bf16x8 hi, mid, lo;
+                    split3x8(v0, v1, hi, mid, lo);
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, b[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mid, b[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, b[j], acc[i][j], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    };
+
+    // D-stage ring: stages st + 1 .. st + D - 2 stay in flight while stage st
+    // is computed; stage st + D - 1 is issued into the slot stage st - 1 used,
+    // after the barrier that ends every wave's reads of it
+#pragma unroll
+    for (int p = 0; p < D - 1; ++p)
+        if ((uint32_t)p < stages) issue(p, p);
+    for (uint32_t st = 0; st < stages; ++st) {
+        const uint32_t ahead = stages - 1 - st;  // stages issued after st, at most D - 2
+        if (ahead >= (uint32_t)(D - 2)) wait_vm<(D - 2) * G::LPS>();
+        else if (D > 3 && ahead == 1) wait_vm<(D > 3 ? 1 : 0) * G::LPS>();
+        else wait_vm<0>();
+        lds_barrier();
+        if (st + D - 1 < stages) issue(st + D - 1, (st + D - 1) % D);
+        compute(st % D);
+    }
+    mfma_drain();
+
+    // D[i][j] of a 32x32 tile: lane l holds column l % 32 and, in register r,
+    // row 8 (r / 4) + 4 (l / 32) + r % 4
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint32_t col = col0 + (wn * TN + j) * 32 + r32;
+            if (col >= n) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = row0 + (wm * TM + i) * 32 + 8 * (r / 4) + 4 * h + r % 4;
+                if (row < m) y[(size_t)row * n + col] = acc[i][j][r];
+            }
+        }
+}
+
+template <bool XBF16, int WM, int WN, int TM, int TN>
+hipError_t go(const GemvArgs& a) {
+    // deepest ring that fits: 3 stages of a 128 x 128 bf16 tile (121.5 KiB)
+    constexpr int D3 = Geometry<XBF16, WM, WN, TM, TN, 2>::STAGE * 3 <= 160 * 1024 ? 3 : 2;
+    constexpr int D = (Geometry<XBF16, WM, WN, TM, TN, 2>::STAGE * 4 <= 160 * 1024 &&
+                       2 * Geometry<XBF16, WM, WN, TM, TN, 2>::LPS <= 63) ? 4 : D3;
+    using G = Geometry<XBF16, WM, WN, TM, TN, D>;
+    const uint32_t tiles_n = (a.n + G::BN - 1) / G::BN, tiles_m = (a.m + G::BM - 1) / G::BM;
+    hipLaunchKernelGGL((gemm_exact_kernel<XBF16, WM, WN, TM, TN, D>), dim3(tiles_n * tiles_m), dim3(G::NT), 0,
+                       a.stream, a.packed, a.scales, a.x, a.y, a.m, a.n, a.k, tiles_n);
+    return hipGetLastError();
+}
+
+template <bool XBF16>
+hipError_t dispatch(const GemvArgs& a, const GemmConfig& c) {
+    // instances: (waves along M x along N, MFMA tiles per wave along M x N)
+    if (c.wm == 2 && c.wn == 2 && c.tm == 2 && c.tn == 2) return go<XBF16, 2, 2, 2, 2>(a);
+    if (c.wm == 2 && c.wn == 2 && c.tm == 2 && c.tn == 1) return go<XBF16, 2, 2, 2, 1>(a);
+    if (c.wm == 2 && c.wn == 2 && c.tm == 1 && c.tn == 2) return go<XBF16, 2, 2, 1, 2>(a);
+    if (c.wm == 4 && c.wn == 1 && c.tm == 1 && c.tn == 2) return go<XBF16, 4, 1, 1, 2>(a);
+    if (c.wm == 2 && c.wn == 2 && c.tm == 1 && c.tn == 1) return go<XBF16, 2, 2, 1, 1>(a);
+    if (c.wm == 1 && c.wn == 4 && c.tm == 2 && c.tn == 2) return go<XBF16, 1, 4, 2, 2>(a);
+    if (c.wm == 1 && c.wn == 4 && c.tm == 2 && c.tn == 1) return go<XBF16, 1, 4, 2, 1>(a);
+    if (c.wm == 1 && c.wn == 4 && c.tm == 1 && c.tn == 2) return go<XBF16, 1, 4, 1, 2>(a);
+    if (c.wm == 1 && c.wn == 4 && c.tm == 1 && c.tn == 1) return go<XBF16, 1, 4, 1, 1>(a);
+    // a 128 x 256 tile of f32 activations would leave room for one stage only
+    if constexpr (XBF16)
+        if (c.wm == 2 && c.wn == 4 && c.tm == 2 && c.tn == 2) return go<XBF16, 2, 4, 2, 2>(a);
+    if (c.wm == 2 && c.wn == 4 && c.tm == 1 && c.tn == 2) return go<XBF16, 2, 4, 1, 2>(a);
+    return hipErrorNotSupported;
+}
+
+}  // namespace
+
+bool gemm_exact_supported(uint32_t m, uint32_t n, uint32_t k, bool x_bf16) {
+    // 32-bit buffer offsets over x and the packed weights
+    const uint64_t xb = (uint64_t)m * k * (x_bf16 ? 2 : 4);
+    return m >= 1 && n >= 1 && k % kBK == 0 && k >= kBK && xb + 256 * k * 4 < (1ull << 31) &&
+           (uint64_t)(n + 256) * (k / 2) < (1ull << 31);
+}
+
+hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* forced) {
+    if (!gemm_exact_supported(a.m, a.n, a.k, a.x_bf16)) return hipErrorNotSupported;
+    GemmConfig c;
+    if (forced && forced->wm) {
+        c = *forced;
+    } else {
+        // The largest tile whose grid still reaches three quarters of the CUs
+        // (larger tiles re-read fewer operand bytes; a grid below that leaves
+        // CUs idle), else the smallest. From a sweep of every instance on the
+        // Qwen3-8B q/gate/down weights at M = 33..512 (bf16 x, cold weights):
+        // gate at M = 512 128 x 256 (8 waves) 51 us, at 256 64 x 256 34 us, at
+        // 128 64 x 128 23 us; q and down at 512 64 x 128 (24 / 64 us); 64 x 64
+        // below (q 16-17 us, down 42-46 us, latency-bound: too few tiles).
+        struct Cand { int wm, wn, tm, tn, bm, bn; };
+        const Cand cands[] = {{2, 4, 2, 2, 128, 256}, {1, 4, 2, 2, 64, 256}, {1, 4, 2, 1, 64, 128},
+                              {2, 2, 1, 1, 64, 64}};
+        const uint64_t want = (uint64_t)(cus > 0 ? cus : 256) * 3 / 4;
+        Cand pick = cands[3];
+        for (const Cand& cd : cands) {
+            if (!a.x_bf16 && cd.wn == 4 && cd.wm == 2) continue;  // no f32 instance of 128 x 256
+            const uint64_t tiles = (uint64_t)((a.m + cd.bm - 1) / cd.bm) * ((a.n + cd.bn - 1) / cd.bn);
+            if (tiles >= want) {
+                pick = cd;
+                break;
+            }
+        }
+        c.wm = pick.wm; c.wn = pick.wn; c.tm = pick.tm; c.tn = pick.tn;
+    }
+    return a.x_bf16 ? dispatch<true>(a, c) : dispatch<false>(a, c);
+}
+
+}  // namespace mx4

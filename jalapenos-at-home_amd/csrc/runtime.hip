@@ -306,6 +306,8 @@ mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
             path = MX4_PATH_GEMV;
         else if (m >= 2 && mx4::skinny_supported(m, w->cols) && scales_foldable(w))
             path = MX4_PATH_SKINNY;
+        else if (m > 32 && mx4::gemm_exact_supported(m, w->rows, w->cols, xt == MX4_BF16) && scales_foldable(w))
+            path = MX4_PATH_GEMM;
         else
             path = MX4_PATH_GENERIC;
     }
@@ -326,6 +328,13 @@ mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
             if (!scales_foldable(w))
                 return fail(MX4_ERR_UNSUPPORTED, "skinny path folds scales into bf16; scale bytes outside 2..252 need GENERIC");
             e = mx4::launch_skinny(a, ctx->cus, {ctx->split_part, ctx->split_count, kSplitPartTiles, kSplitCounts});
+            break;
+        case MX4_PATH_GEMM:
+            if (!mx4::gemm_exact_supported(m, w->rows, w->cols, xt == MX4_BF16))
+                return fail(MX4_ERR_UNSUPPORTED, "GEMM path needs K %% 128 == 0 and operands under 2 GiB");
+            if (!scales_foldable(w))
+                return fail(MX4_ERR_UNSUPPORTED, "GEMM path folds scales into bf16; scale bytes outside 2..252 need GENERIC");
+            e = mx4::launch_gemm_exact(a, ctx->cus, nullptr);
             break;
         case MX4_PATH_GENERIC:
             e = mx4::launch_gemv_generic(a);
@@ -714,6 +723,28 @@ mx4_status mx4_gemv_config(mx4_context* ctx, const void* x, mx4_dtype xt, const 
     c.grid = teams;
     hipError_t e = mx4::launch_gemv_m1_group(gg, ctx->cus, &c);
     if (e == hipErrorNotSupported) return fail(MX4_ERR_UNSUPPORTED, "configuration not instantiated");
+    if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status mx4_gemm_config(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, const mx4_weight* w, float* y,
+                           int waves_m, int waves_n, int tiles_m, int tiles_n) {
+    mx4_status st = check_matmul_args(ctx, x, xt, m, w, y);
+    if (st != MX4_OK) return st;
+    if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the GEMM configurations are for MXFP4 weights");
+    if (!scales_foldable(w)) return fail(MX4_ERR_UNSUPPORTED, "scale bytes outside 2..252 need the generic kernel");
+    if (!mx4::gemm_exact_supported(m, w->rows, w->cols, xt == MX4_BF16))
+        return fail(MX4_ERR_UNSUPPORTED, "GEMM path needs K %% 128 == 0 and operands under 2 GiB");
+    if (waves_m < 0 || waves_n < 0 || tiles_m < 0 || tiles_n < 0) return fail(MX4_ERR_ARGUMENT, "negative configuration");
+    DeviceGuard g(ctx->device);
+    mx4::GemvArgs a{w->packed, w->scales, x, y, m, w->rows, w->cols, xt == MX4_BF16, ctx->stream};
+    mx4::GemmConfig c;
+    c.wm = waves_m;
+    c.wn = waves_n;
+    c.tm = tiles_m;
+    c.tn = tiles_n;
+    hipError_t e = mx4::launch_gemm_exact(a, ctx->cus, &c);
+    if (e == hipErrorNotSupported) return fail(MX4_ERR_UNSUPPORTED, "GEMM instance not compiled");
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
     return MX4_OK;
 }

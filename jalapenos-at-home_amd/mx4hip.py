@@ -26,7 +26,7 @@ STATUS = {
 ERR_TOO_LARGE = 3
 ERR_UNSUPPORTED = 9
 F32, BF16 = 0, 1
-PATH_AUTO, PATH_GEMV, PATH_SKINNY, PATH_GENERIC, PATH_PREFILL = 0, 1, 2, 3, 4
+PATH_AUTO, PATH_GEMV, PATH_SKINNY, PATH_GENERIC, PATH_PREFILL, PATH_GEMM = 0, 1, 2, 3, 4, 5
 ACT_MXFP4, ACT_MXFP8 = 1, 2
 
 _vp = ctypes.c_void_p
@@ -67,6 +67,7 @@ SIGNATURES = {
     "mx4_matmul_group": (_int, [_vp, _vp, _int, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32]),
     "mx4_gemv_config": (_int, [_vp, _vp, _int, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32, _int, _int, _int, _u32]),
     "mx4_gemv_tokens_config": (_int, [_vp, _vp, _u32, _vp, _vp, _u32, _u32]),
+    "mx4_gemm_config": (_int, [_vp, _vp, _int, _u32, _vp, _vp, _int, _int, _int, _int]),
     "mx4_matmul_batch": (_int, [_vp, _vp, _u32]),
     "mx4_matmul_mx": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
     "mx4_reserve_prefill": (_int, [_vp, _u32, _u32]),
@@ -404,6 +405,11 @@ class Context:
         wa, ya = _handles(ws), _ptrs(ys)
         return lib().mx4_prefill_group_config(self.handle, codes.ptr, scales.ptr, act, m, wa, ya, len(ws),
                                               tile_m, tile_n, split_k)
+
+    def gemm_config(self, x: DeviceBuffer, xtype: int, m: int, w: Weight, y: DeviceBuffer, wm: int, wn: int,
+                    tm: int, tn: int) -> int:
+        """Exact tiled GEMM with an explicit instance; returns the status (MX4_ERR_UNSUPPORTED if none)."""
+        return lib().mx4_gemm_config(self.handle, x.ptr, xtype, m, w.handle, y.ptr, wm, wn, tm, tn)
 
     def gemv_tokens_config(self, x: DeviceBuffer, m: int, w: Weight, y: DeviceBuffer, teams: int, tpw: int) -> int:
         """Few-token GEMV (bf16 x) with an explicit launch shape; returns the status."""

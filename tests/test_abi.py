@@ -29,6 +29,22 @@ def test_library_exports_every_header_symbol(mx4):
     assert sorted(mx4.SIGNATURES) == symbols
 
 
+def test_every_kernel_launch_stub_is_defined(mx4):
+    """Every kernel the host code launches has its launch stub in the library.
+    (A device-only builtin that the host pass rejects makes clang drop the
+    stubs of the kernels that use it without an error; the library then fails
+    to load on the GPU box.)"""
+    import shutil
+    import subprocess
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-u", str(mx4.LIB_PATH)], capture_output=True, text=True, check=True).stdout
+    missing = [line.split()[-1] for line in out.splitlines() if "device_stub" in line]
+    assert not missing, missing[:5]
+
+
 def test_library_is_built_for_gfx950_only(mx4):
     data = mx4.LIB_PATH.read_bytes()
     assert b"gfx950" in data

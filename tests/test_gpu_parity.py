@@ -274,6 +274,26 @@ def test_dropin_matches_cpu_for_decode_and_prefill(mx4, oracle):
         hip.close()
 
 
+def test_dropin_fast_paths_match_cpu(mx4, oracle):
+    """qwen_hip_matmul (f32 x from the host, synchronous) on Qwen-width weights,
+    where it takes the fast kernels: the M = 1 GEMV, the skinny kernel
+    (2..32 rows) and the exact tiled GEMM (33 and more rows), each against the
+    oracle with the reference's per-element bound (engine/src/metal.rs:110)."""
+    rng = np.random.default_rng(5)
+    n, k = 300, 2048
+    packed, scales = oracle.synth_weight(17, n, k)
+    hip = mx4.Hip()
+    try:
+        for rows in (1, 3, 16, 33, 70):
+            x = (rng.standard_normal((rows, k)) * 0.5).astype(np.float32)
+            expected = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
+            actual = hip.matmul(x, packed, scales)
+            assert actual.shape == expected.shape
+            assert_close(actual, expected, f"drop-in rows={rows}")
+    finally:
+        hip.close()
+
+
 def test_dropin_bf16_weights_match_cpu(mx4, oracle):
     """engine/src/metal.rs:86-114, the bf16 arm: the decoded quantized weight as
     Tensor::bf16 (scales == NULL), for the same rows, against the reference's
@@ -904,6 +924,110 @@ def test_skinny_ragged_rows_and_identity(mx4, ctx, oracle):
 
 
 # ------------------------------------------------------------------ prefill (block-scaled MFMA)
+
+# ------------------------------------------------------------------ exact GEMM (M > 32)
+
+GEMM_INSTANCES = [(2, 2, 2, 2), (2, 2, 2, 1), (2, 2, 1, 2), (4, 1, 1, 2), (2, 2, 1, 1), (1, 4, 2, 2), (1, 4, 2, 1),
+                  (1, 4, 1, 2), (1, 4, 1, 1), (2, 4, 2, 2), (2, 4, 1, 2)]
+GEMM_BF16_ONLY = {(2, 4, 2, 2)}  # its f32 tile would leave LDS room for one stage only
+
+
+@pytest.mark.parametrize("inst", GEMM_INSTANCES, ids=[f"{a}x{b}w-{c}x{d}t" for a, b, c, d in GEMM_INSTANCES])
+def test_gemm_identity_and_oracle_every_instance(mx4, ctx, oracle, inst):
+    """The exact tiled GEMM (bf16 MFMA, weights decoded on the way from LDS),
+    every compiled instance on ragged M and N: one-hot activations return the
+    decoded weights bit for bit (pins the operand and output layouts and the
+    folded scales), random bf16 and f32 activations match the oracle, and a
+    repeated call is bit-identical."""
+    wm, wn, tm, tn = inst
+    rng = np.random.default_rng(sum(inst))
+    n, k = 333, 1024
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(112, 140, (n, k // 32), dtype=np.uint8)
+    w = ctx.upload_weight(packed, scales, n, k)
+    dec = oracle.dequantize(packed, scales)
+    for m in (33, 77):
+        cols = rng.choice(k, m, replace=False)
+        x = np.zeros((m, k), np.float32)
+        x[np.arange(m), cols] = 1.0
+        xts = (mx4.BF16,) if inst in GEMM_BF16_ONLY else (mx4.BF16, mx4.F32)
+        for xt in xts:
+            xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16) if xt == mx4.BF16 else x)
+            yb = ctx.buffer(m * n * 4)
+            assert ctx.gemm_config(xb, xt, m, w, yb, wm, wn, tm, tn) == 0, mx4.last_error()
+            got = yb.download(np.float32).reshape(m, n)
+            assert np.array_equal(got, dec[:, cols].T), f"identity m={m} xt={xt}"
+        if inst in GEMM_BF16_ONLY:
+            xb = ctx.to_device(x)
+            assert ctx.gemm_config(xb, mx4.F32, m, w, ctx.buffer(m * n * 4), wm, wn, tm, tn) == mx4.ERR_UNSUPPORTED
+        xr = oracle.bf16_to_f32(oracle.synth_bf16(1200 + m, 1.0, m * k)).reshape(m, k)
+        for xt in xts:
+            xin = xr if xt == mx4.BF16 else (xr + rng.standard_normal(xr.shape).astype(np.float32) * 1e-3)
+            ref = oracle.matmul(xin, packed.reshape(-1), scales.reshape(-1))
+            xb = ctx.to_device((f32_bits(xin) >> 16).astype(np.uint16) if xt == mx4.BF16 else xin)
+            yb = ctx.buffer(m * n * 4)
+            assert ctx.gemm_config(xb, xt, m, w, yb, wm, wn, tm, tn) == 0, mx4.last_error()
+            got = yb.download(np.float32).reshape(m, n)
+            assert_close(got, ref, f"gemm {inst} m={m} xt={xt}", scaled=True)
+            assert ctx.gemm_config(xb, xt, m, w, yb, wm, wn, tm, tn) == 0
+            assert np.array_equal(yb.download(np.float32).reshape(m, n), got), "repeat"
+    w.release()
+
+
+@pytest.mark.parametrize("name", ["q", "gate", "down"])
+def test_gemm_auto_8b_shapes(mx4, ctx, oracle, name):
+    """AUTO at M = 33, 128 and 512 token rows on the Qwen3-8B q, gate and down
+    weights (the drop-in's path for a prompt; engine/src/gpu.rs:510-514) takes
+    the exact tiled GEMM: sampled token rows x weight rows against the oracle,
+    bf16 and f32 activations."""
+    n, k = QWEN8[name]
+    rng = np.random.default_rng(91)
+    w = ctx.synth_weight(500 + list(QWEN8).index(name), n, k, 0.02)
+    packed, scales = ctx.download_weight(w)
+    cols = _sample_rows(n, 64, rng)
+    for m in (33, 128, 512):
+        say(f"gemm AUTO 8B {name} m={m}")
+        x = oracle.bf16_to_f32(oracle.synth_bf16(510 + m, 1.0, m * k)).reshape(m, k)
+        rows = np.unique(np.concatenate([[0, m - 1], rng.choice(m, 14, replace=False)]))
+        for xt in (mx4.BF16, mx4.F32):
+            xin = x if xt == mx4.BF16 else (x + rng.standard_normal(x.shape).astype(np.float32) * 1e-3)
+            ref = np.concatenate([oracle.matmul_rows(xin[rows], packed.reshape(-1), scales.reshape(-1), int(c),
+                                                     int(c) + 1) for c in cols], axis=1)
+            y = run_matmul(mx4, ctx, xin, w, mx4.PATH_AUTO, xt)
+            assert np.all(np.isfinite(y))
+            assert_close(y[np.ix_(rows, cols)], ref, f"gemm AUTO {name} m={m} xt={xt}")
+    w.release()
+
+
+def test_gemm_rejects_and_falls_back(mx4, ctx, oracle):
+    """K not a multiple of 128 or scale bytes outside 2..252: AUTO runs the
+    exact generic kernel (still exact), the explicit GEMM path is refused."""
+    rng = np.random.default_rng(3)
+    m, n, k = 40, 50, 160
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(118, 130, (n, k // 32), dtype=np.uint8)
+    w = ctx.upload_weight(packed, scales, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
+    assert_close(run_matmul(mx4, ctx, x, w, mx4.PATH_AUTO), ref, "K=160 AUTO", scaled=True)
+    with pytest.raises(mx4.Mx4Error, match="K % 128"):
+        run_matmul(mx4, ctx, x, w, mx4.PATH_GEMM)
+    k2 = 256
+    packed2 = rng.integers(0, 256, (n, k2 // 2), dtype=np.uint8)
+    scales2 = rng.integers(118, 130, (n, k2 // 32), dtype=np.uint8)
+    scales2[7, 3] = 1
+    w2 = ctx.upload_weight(packed2, scales2, n, k2)
+    x2 = rng.standard_normal((m, k2)).astype(np.float32)
+    ref2 = oracle.matmul(x2, packed2.reshape(-1), scales2.reshape(-1))
+    assert_close(run_matmul(mx4, ctx, x2, w2, mx4.PATH_AUTO), ref2, "scale 1 AUTO", scaled=True)
+    with pytest.raises(mx4.Mx4Error, match="2..252"):
+        run_matmul(mx4, ctx, x2, w2, mx4.PATH_GEMM)
+    yb = ctx.buffer(m * n * 4)
+    xb = ctx.to_device(x2)
+    assert ctx.gemm_config(xb, mx4.F32, m, w2, yb, 3, 3, 1, 1) == mx4.ERR_UNSUPPORTED
+    w.release()
+    w2.release()
+
 
 def _prefill_ref(oracle, x, packed, scales, act):
     """The oracle on requantized activations: dequant(requant(x)) . dequant(W)^T."""
