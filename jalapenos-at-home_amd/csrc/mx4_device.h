@@ -147,4 +147,36 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float v) {
     return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
+// ---------------------------------------------------------------- LDS pipelines
+
+// LDS barrier that does not wait for outstanding global loads (the next
+// stage's prefetch stays in flight across it).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// Direct-to-LDS buffer loads of 16 or 4 bytes per lane: lane l's bytes land
+// at dst + l * size. (Only the device pass sees the builtin: the host pass
+// checks the size against its own target, rejects 16, and would then drop
+// the kernels' launch stubs without a word.)
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, lds_ptr dst, uint32_t voffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voffset, 0, 0, 0);
+#else
+    (void)r; (void)dst; (void)voffset;
+#endif
+}
+__device__ __forceinline__ void load_lds4(__amdgpu_buffer_rsrc_t r, lds_ptr dst, uint32_t voffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 4, voffset, 0, 0, 0);
+#else
+    (void)r; (void)dst; (void)voffset;
+#endif
+}
+
 }  // namespace mx4
