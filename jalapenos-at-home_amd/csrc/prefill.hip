@@ -441,10 +441,16 @@ hipError_t dispatch(const PrefillArgs& a) {
     // workgroup tiles over the full K, 192 workgroups (MXFP4 17.3 -> 15.9 us,
     // MX-FP8 22.4 -> 20.6 us against 2 x 2 tiles in K halves)
     if (ntot > 4096 && a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 1, 2, 0>(a);
-    // MX-FP8 activations on K = 12288 (down): 2 x 4 wave tiles in K quarters
-    // (29.5 -> 27.1 us; MXFP4 gains nothing there)
+    // K = 12288 (down) in K quarters: MX-FP8 on 2 x 4 wave tiles (29.5 -> 27.1 us
+    // warm), MXFP4 on 4 x 2 wave tiles (cold weights: 30.9 -> 26.4 us)
+    if (a.k == 12288 && ntot <= 4096) {
+        if constexpr (A_FP8) return go_parts<true, 2, 4, 4>(a);
+        else return go_parts<false, 4, 2, 4>(a);
+    }
+    // MX-FP8 at K = 4096 up to 4096 rows (q/o): 2 x 4 wave tiles in K quarters
+    // (cold weights: 16.0 -> 14.5 us)
     if constexpr (A_FP8) {
-        if (a.k == 12288 && ntot <= 4096) return go_parts<true, 2, 4, 4>(a);
+        if (a.k == 4096 && ntot <= 4096) return go_parts<true, 2, 4, 4>(a);
     }
     if (a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 2, 2, 32>(a);
     if (a.k == 12288) return go<A_FP8, 2, 2, 2, 4, 2, 2, 96>(a);
