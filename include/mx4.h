@@ -190,10 +190,15 @@ mx4_status mx4_gemv_tokens_config(mx4_context *ctx, const void *x_dev, uint32_t 
 
 /* Tuning hook for the exact tiled GEMM (MX4_PATH_GEMM): waves per workgroup
  * along M and N and 32x32 MFMA tiles per wave along M and N, one of the
- * compiled instances (2x2 waves of 2x2, 2x1, 1x2 or 1x1 tiles; 4x1 waves of
- * 1x2 tiles); MX4_ERR_UNSUPPORTED otherwise. Zeros keep the default. */
+ * compiled instances (2x2 waves of 2x2, 2x1, 1x2 or 1x1 tiles; 1x4 waves of
+ * 2x2, 2x1, 1x2 or 1x1; 2x4 waves of 2x2 (bf16 x only) or 1x2; 4x1 waves of
+ * 1x2), and K slices across workgroups (0 or 1: none; a split needs K a
+ * multiple of 128 * k_slices and k_slices * m * rows * 4 bytes within the
+ * context's 4 MiB split scratch); MX4_ERR_UNSUPPORTED otherwise. Zero waves
+ * keep the default, which splits K on its own when the tiles alone would
+ * leave CUs idle. */
 mx4_status mx4_gemm_config(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m, const mx4_weight *w,
-                           float *y_dev, int waves_m, int waves_n, int tiles_m, int tiles_n);
+                           float *y_dev, int waves_m, int waves_n, int tiles_m, int tiles_n, int k_slices);
 
 /* Prefill on CDNA4 block-scaled MFMA (V_MFMA_SCALE_F32_*_F8F6F4): x is
  * requantized per 32 along K (MXFP4 by python/quantize_mxfp4.py:18-39, or MX

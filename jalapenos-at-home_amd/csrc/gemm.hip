@@ -102,15 +102,20 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_exact_kernel(const uint8_t*
                                                                   const uint8_t* __restrict__ scales,
                                                                   const void* __restrict__ x, float* __restrict__ y,
                                                                   uint32_t m, uint32_t n, uint32_t k,
-                                                                  uint32_t tiles_n) {
+                                                                  uint32_t tiles_n, uint32_t tiles,
+                                                                  uint32_t kslice, float* __restrict__ part) {
     using G = Geometry<XBF16, WM, WN, TM, TN, D>;
     __shared__ __attribute__((aligned(16))) uint8_t lds[D * G::STAGE];
     const uint32_t lane = threadIdx.x % 64, h = lane / 32, r32 = lane % 32;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t wm = wave / WN, wn = wave % WN;
-    const uint32_t tn = blockIdx.x % tiles_n, tm = blockIdx.x / tiles_n;
+    // K split: workgroup b takes tile b % tiles over K slice b / tiles and
+    // writes its partial tile to part[slice][m][n] (summed afterwards in slice order)
+    const uint32_t slice = blockIdx.x / tiles, tile = blockIdx.x % tiles;
+    const uint32_t tn = tile % tiles_n, tm = tile / tiles_n;
     const uint32_t row0 = tm * G::BM, col0 = tn * G::BN;
-    const uint32_t stages = k / kBK;
+    const uint32_t k0 = slice * kslice, stages = kslice / kBK;
+    if (part) y = part + (size_t)slice * m * n;
 
     const __amdgpu_buffer_rsrc_t xr = rsrc(x, m * k * G::XB);
     const __amdgpu_buffer_rsrc_t pr = rsrc(packed, n * (k / 2));
@@ -121,15 +126,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_exact_kernel(const uint8_t*
 #pragma unroll
     for (int q = 0; q < G::A_INSTR; ++q) {
         const uint32_t p = (q * G::NW + wave) * 64 + lane, row = p / G::A_CPR, c = (p % G::A_CPR) ^ (row % 16);
-        a_goff[q] = (row0 + row) * k * G::XB + c * 16;
+        a_goff[q] = (row0 + row) * k * G::XB + k0 * G::XB + c * 16;
     }
 #pragma unroll
     for (int q = 0; q < G::B_INSTR; ++q) {
         const uint32_t p = (q * G::NW + wave) * 64 + lane, row = p / 4, c = (p % 4) ^ ((row >> 2) & 3);
-        b_goff[q] = (col0 + row) * (k / 2) + c * 16;
+        b_goff[q] = (col0 + row) * (k / 2) + k0 / 2 + c * 16;
     }
     const uint32_t s_row = wave * G::S_ROWS + lane;
-    const uint32_t s_goff = (col0 + s_row) * (k / 32);
+    const uint32_t s_goff = (col0 + s_row) * (k / 32) + k0 / 32;
 
     auto issue = [&](uint32_t st, uint32_t slot) {
         uint8_t* base = lds + slot * G::STAGE;
@@ -235,35 +240,59 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_exact_kernel(const uint8_t*
         }
 }
 
+// y = sum over the slices of part[s] (count floats each), in slice order.
+__global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict__ part, uint32_t ks, uint32_t count,
+                                                        float* __restrict__ y) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (count % 4 == 0) {
+        if (4 * i >= count) return;
+        f32x4 a = *reinterpret_cast<const f32x4*>(part + 4 * i);
+        for (uint32_t s = 1; s < ks; ++s) a += *reinterpret_cast<const f32x4*>(part + (size_t)s * count + 4 * i);
+        *reinterpret_cast<f32x4*>(y + 4 * i) = a;
+    } else {
+        if (i >= count) return;
+        float a = part[i];
+        for (uint32_t s = 1; s < ks; ++s) a += part[(size_t)s * count + i];
+        y[i] = a;
+    }
+}
+
 template <bool XBF16, int WM, int WN, int TM, int TN>
-hipError_t go(const GemvArgs& a) {
+hipError_t go(const GemvArgs& a, uint32_t ks, float* part) {
     // deepest ring that fits: 3 stages of a 128 x 128 bf16 tile (121.5 KiB)
     constexpr int D3 = Geometry<XBF16, WM, WN, TM, TN, 2>::STAGE * 3 <= 160 * 1024 ? 3 : 2;
     constexpr int D = (Geometry<XBF16, WM, WN, TM, TN, 2>::STAGE * 4 <= 160 * 1024 &&
                        2 * Geometry<XBF16, WM, WN, TM, TN, 2>::LPS <= 63) ? 4 : D3;
     using G = Geometry<XBF16, WM, WN, TM, TN, D>;
     const uint32_t tiles_n = (a.n + G::BN - 1) / G::BN, tiles_m = (a.m + G::BM - 1) / G::BM;
-    hipLaunchKernelGGL((gemm_exact_kernel<XBF16, WM, WN, TM, TN, D>), dim3(tiles_n * tiles_m), dim3(G::NT), 0,
-                       a.stream, a.packed, a.scales, a.x, a.y, a.m, a.n, a.k, tiles_n);
+    const uint32_t tiles = tiles_n * tiles_m;
+    if (ks < 1) ks = 1;
+    hipLaunchKernelGGL((gemm_exact_kernel<XBF16, WM, WN, TM, TN, D>), dim3(tiles * ks), dim3(G::NT), 0, a.stream,
+                       a.packed, a.scales, a.x, a.y, a.m, a.n, a.k, tiles_n, tiles, a.k / ks, ks > 1 ? part : nullptr);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || ks == 1) return e;
+    const uint32_t count = a.m * a.n, threads = count % 4 == 0 ? count / 4 : count;
+    hipLaunchKernelGGL(split_sum_kernel, dim3((threads + 255) / 256), dim3(256), 0, a.stream, part, ks, count, a.y);
     return hipGetLastError();
 }
 
 template <bool XBF16>
-hipError_t dispatch(const GemvArgs& a, const GemmConfig& c) {
+hipError_t dispatch(const GemvArgs& a, const GemmConfig& c, float* part) {
     // instances: (waves along M x along N, MFMA tiles per wave along M x N)
-    if (c.wm == 2 && c.wn == 2 && c.tm == 2 && c.tn == 2) return go<XBF16, 2, 2, 2, 2>(a);
-    if (c.wm == 2 && c.wn == 2 && c.tm == 2 && c.tn == 1) return go<XBF16, 2, 2, 2, 1>(a);
-    if (c.wm == 2 && c.wn == 2 && c.tm == 1 && c.tn == 2) return go<XBF16, 2, 2, 1, 2>(a);
-    if (c.wm == 4 && c.wn == 1 && c.tm == 1 && c.tn == 2) return go<XBF16, 4, 1, 1, 2>(a);
-    if (c.wm == 2 && c.wn == 2 && c.tm == 1 && c.tn == 1) return go<XBF16, 2, 2, 1, 1>(a);
-    if (c.wm == 1 && c.wn == 4 && c.tm == 2 && c.tn == 2) return go<XBF16, 1, 4, 2, 2>(a);
-    if (c.wm == 1 && c.wn == 4 && c.tm == 2 && c.tn == 1) return go<XBF16, 1, 4, 2, 1>(a);
-    if (c.wm == 1 && c.wn == 4 && c.tm == 1 && c.tn == 2) return go<XBF16, 1, 4, 1, 2>(a);
-    if (c.wm == 1 && c.wn == 4 && c.tm == 1 && c.tn == 1) return go<XBF16, 1, 4, 1, 1>(a);
+    const uint32_t ks = c.ks < 1 ? 1u : (uint32_t)c.ks;
+    if (c.wm == 2 && c.wn == 2 && c.tm == 2 && c.tn == 2) return go<XBF16, 2, 2, 2, 2>(a, ks, part);
+    if (c.wm == 2 && c.wn == 2 && c.tm == 2 && c.tn == 1) return go<XBF16, 2, 2, 2, 1>(a, ks, part);
+    if (c.wm == 2 && c.wn == 2 && c.tm == 1 && c.tn == 2) return go<XBF16, 2, 2, 1, 2>(a, ks, part);
+    if (c.wm == 4 && c.wn == 1 && c.tm == 1 && c.tn == 2) return go<XBF16, 4, 1, 1, 2>(a, ks, part);
+    if (c.wm == 2 && c.wn == 2 && c.tm == 1 && c.tn == 1) return go<XBF16, 2, 2, 1, 1>(a, ks, part);
+    if (c.wm == 1 && c.wn == 4 && c.tm == 2 && c.tn == 2) return go<XBF16, 1, 4, 2, 2>(a, ks, part);
+    if (c.wm == 1 && c.wn == 4 && c.tm == 2 && c.tn == 1) return go<XBF16, 1, 4, 2, 1>(a, ks, part);
+    if (c.wm == 1 && c.wn == 4 && c.tm == 1 && c.tn == 2) return go<XBF16, 1, 4, 1, 2>(a, ks, part);
+    if (c.wm == 1 && c.wn == 4 && c.tm == 1 && c.tn == 1) return go<XBF16, 1, 4, 1, 1>(a, ks, part);
     // a 128 x 256 tile of f32 activations would leave room for one stage only
     if constexpr (XBF16)
-        if (c.wm == 2 && c.wn == 4 && c.tm == 2 && c.tn == 2) return go<XBF16, 2, 4, 2, 2>(a);
-    if (c.wm == 2 && c.wn == 4 && c.tm == 1 && c.tn == 2) return go<XBF16, 2, 4, 1, 2>(a);
+        if (c.wm == 2 && c.wn == 4 && c.tm == 2 && c.tn == 2) return go<XBF16, 2, 4, 2, 2>(a, ks, part);
+    if (c.wm == 2 && c.wn == 4 && c.tm == 1 && c.tn == 2) return go<XBF16, 2, 4, 1, 2>(a, ks, part);
     return hipErrorNotSupported;
 }
 
@@ -276,11 +305,15 @@ bool gemm_exact_supported(uint32_t m, uint32_t n, uint32_t k, bool x_bf16) {
            (uint64_t)(n + 256) * (k / 2) < (1ull << 31);
 }
 
-hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* forced) {
+hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* forced, float* part, uint64_t part_bytes) {
     if (!gemm_exact_supported(a.m, a.n, a.k, a.x_bf16)) return hipErrorNotSupported;
     GemmConfig c;
     if (forced && forced->wm) {
         c = *forced;
+        // an explicit K split: whole stages per slice and partials within the scratch
+        if (c.ks > 1 && (a.k % ((uint32_t)c.ks * kBK) != 0 || !part ||
+                         (uint64_t)c.ks * a.m * a.n * 4 > part_bytes))
+            return hipErrorNotSupported;
     } else {
         // The largest tile whose grid still reaches three quarters of the CUs
         // (larger tiles re-read fewer operand bytes; a grid below that leaves
@@ -303,8 +336,19 @@ hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* force
             }
         }
         c.wm = pick.wm; c.wn = pick.wn; c.tm = pick.tm; c.tn = pick.tn;
+        // A grid still short of the CUs (few token rows): split K across up to
+        // four workgroups per tile, each slice whole stages, when the partials
+        // fit the scratch; a second small kernel adds them in slice order.
+        const uint64_t tiles = (uint64_t)((a.m + pick.bm - 1) / pick.bm) * ((a.n + pick.bn - 1) / pick.bn);
+        c.ks = 1;
+        for (uint32_t ks = 4; ks >= 2 && tiles < want; --ks) {
+            if (a.k % (ks * kBK) == 0 && part && (uint64_t)ks * a.m * a.n * 4 <= part_bytes) {
+                c.ks = (int)ks;
+                break;
+            }
+        }
     }
-    return a.x_bf16 ? dispatch<true>(a, c) : dispatch<false>(a, c);
+    return a.x_bf16 ? dispatch<true>(a, c, part) : dispatch<false>(a, c, part);
 }
 
 }  // namespace mx4

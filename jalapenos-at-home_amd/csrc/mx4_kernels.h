@@ -72,12 +72,15 @@ hipError_t launch_skinny(const GemvArgs& a, int cus, const SkinnyScratch& sc);
 
 // Exact GEMM on bf16 MFMA for more than 32 token rows (gemm.hip): K % 128 == 0,
 // scale bytes 2..252. GemmConfig picks an instance: waves along M x N and 32x32
-// MFMA tiles per wave along M x N (all zero: the default for the shape).
+// MFMA tiles per wave along M x N (all zero: the default for the shape), and
+// the number of K slices across workgroups (ks <= 1: none). A split writes
+// ks * m * n f32 partials to `part` (part_bytes of device scratch, shared with
+// the other split launches of the stream) and adds them in slice order.
 struct GemmConfig {
-    int wm = 0, wn = 0, tm = 0, tn = 0;
+    int wm = 0, wn = 0, tm = 0, tn = 0, ks = 0;
 };
 bool gemm_exact_supported(uint32_t m, uint32_t n, uint32_t k, bool x_bf16);
-hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* forced);
+hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* forced, float* part, uint64_t part_bytes);
 
 // bf16 weights [n][k] (engine/src/lib.rs:255, None arm), any m, f32 accumulation.
 hipError_t launch_bf16_matmul(const uint16_t* w, const void* x, bool x_bf16, float* y, uint32_t m, uint32_t n,

@@ -334,7 +334,7 @@ mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
                 return fail(MX4_ERR_UNSUPPORTED, "GEMM path needs K %% 128 == 0 and operands under 2 GiB");
             if (!scales_foldable(w))
                 return fail(MX4_ERR_UNSUPPORTED, "GEMM path folds scales into bf16; scale bytes outside 2..252 need GENERIC");
-            e = mx4::launch_gemm_exact(a, ctx->cus, nullptr);
+            e = mx4::launch_gemm_exact(a, ctx->cus, nullptr, ctx->split_part, (uint64_t)kSplitPartTiles * 1024);
             break;
         case MX4_PATH_GENERIC:
             e = mx4::launch_gemv_generic(a);
@@ -728,14 +728,15 @@ mx4_status mx4_gemv_config(mx4_context* ctx, const void* x, mx4_dtype xt, const 
 }
 
 mx4_status mx4_gemm_config(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, const mx4_weight* w, float* y,
-                           int waves_m, int waves_n, int tiles_m, int tiles_n) {
+                           int waves_m, int waves_n, int tiles_m, int tiles_n, int k_slices) {
     mx4_status st = check_matmul_args(ctx, x, xt, m, w, y);
     if (st != MX4_OK) return st;
     if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the GEMM configurations are for MXFP4 weights");
     if (!scales_foldable(w)) return fail(MX4_ERR_UNSUPPORTED, "scale bytes outside 2..252 need the generic kernel");
     if (!mx4::gemm_exact_supported(m, w->rows, w->cols, xt == MX4_BF16))
         return fail(MX4_ERR_UNSUPPORTED, "GEMM path needs K %% 128 == 0 and operands under 2 GiB");
-    if (waves_m < 0 || waves_n < 0 || tiles_m < 0 || tiles_n < 0) return fail(MX4_ERR_ARGUMENT, "negative configuration");
+    if (waves_m < 0 || waves_n < 0 || tiles_m < 0 || tiles_n < 0 || k_slices < 0)
+        return fail(MX4_ERR_ARGUMENT, "negative configuration");
     DeviceGuard g(ctx->device);
     mx4::GemvArgs a{w->packed, w->scales, x, y, m, w->rows, w->cols, xt == MX4_BF16, ctx->stream};
     mx4::GemmConfig c;
@@ -743,7 +744,8 @@ mx4_status mx4_gemm_config(mx4_context* ctx, const void* x, mx4_dtype xt, uint32
     c.wn = waves_n;
     c.tm = tiles_m;
     c.tn = tiles_n;
-    hipError_t e = mx4::launch_gemm_exact(a, ctx->cus, &c);
+    c.ks = k_slices;
+    hipError_t e = mx4::launch_gemm_exact(a, ctx->cus, &c, ctx->split_part, (uint64_t)kSplitPartTiles * 1024);
     if (e == hipErrorNotSupported) return fail(MX4_ERR_UNSUPPORTED, "GEMM instance not compiled");
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
     return MX4_OK;

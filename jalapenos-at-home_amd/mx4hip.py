@@ -67,7 +67,7 @@ SIGNATURES = {
     "mx4_matmul_group": (_int, [_vp, _vp, _int, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32]),
     "mx4_gemv_config": (_int, [_vp, _vp, _int, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32, _int, _int, _int, _u32]),
     "mx4_gemv_tokens_config": (_int, [_vp, _vp, _u32, _vp, _vp, _u32, _u32]),
-    "mx4_gemm_config": (_int, [_vp, _vp, _int, _u32, _vp, _vp, _int, _int, _int, _int]),
+    "mx4_gemm_config": (_int, [_vp, _vp, _int, _u32, _vp, _vp, _int, _int, _int, _int, _int]),
     "mx4_matmul_batch": (_int, [_vp, _vp, _u32]),
     "mx4_matmul_mx": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
     "mx4_reserve_prefill": (_int, [_vp, _u32, _u32]),
@@ -407,9 +407,9 @@ class Context:
                                               tile_m, tile_n, split_k)
 
     def gemm_config(self, x: DeviceBuffer, xtype: int, m: int, w: Weight, y: DeviceBuffer, wm: int, wn: int,
-                    tm: int, tn: int) -> int:
-        """Exact tiled GEMM with an explicit instance; returns the status (MX4_ERR_UNSUPPORTED if none)."""
-        return lib().mx4_gemm_config(self.handle, x.ptr, xtype, m, w.handle, y.ptr, wm, wn, tm, tn)
+                    tm: int, tn: int, ks: int = 0) -> int:
+        """Exact tiled GEMM with an explicit instance and K split; returns the status (MX4_ERR_UNSUPPORTED if none)."""
+        return lib().mx4_gemm_config(self.handle, x.ptr, xtype, m, w.handle, y.ptr, wm, wn, tm, tn, ks)
 
     def gemv_tokens_config(self, x: DeviceBuffer, m: int, w: Weight, y: DeviceBuffer, teams: int, tpw: int) -> int:
         """Few-token GEMV (bf16 x) with an explicit launch shape; returns the status."""

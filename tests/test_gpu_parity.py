@@ -932,13 +932,16 @@ GEMM_INSTANCES = [(2, 2, 2, 2), (2, 2, 2, 1), (2, 2, 1, 2), (4, 1, 1, 2), (2, 2,
 GEMM_BF16_ONLY = {(2, 4, 2, 2)}  # its f32 tile would leave LDS room for one stage only
 
 
+@pytest.mark.parametrize("ks", [1, 2, 4])
 @pytest.mark.parametrize("inst", GEMM_INSTANCES, ids=[f"{a}x{b}w-{c}x{d}t" for a, b, c, d in GEMM_INSTANCES])
-def test_gemm_identity_and_oracle_every_instance(mx4, ctx, oracle, inst):
+def test_gemm_identity_and_oracle_every_instance(mx4, ctx, oracle, inst, ks):
     """The exact tiled GEMM (bf16 MFMA, weights decoded on the way from LDS),
-    every compiled instance on ragged M and N: one-hot activations return the
-    decoded weights bit for bit (pins the operand and output layouts and the
-    folded scales), random bf16 and f32 activations match the oracle, and a
-    repeated call is bit-identical."""
+    every compiled instance on ragged M and N, unsplit and with K split across
+    2 and 4 workgroups (partials added in slice order by a second kernel):
+    one-hot activations return the decoded weights bit for bit (pins the
+    operand and output layouts, the folded scales and the slice offsets),
+    random bf16 and f32 activations match the oracle, and a repeated call is
+    bit-identical."""
     wm, wn, tm, tn = inst
     rng = np.random.default_rng(sum(inst))
     n, k = 333, 1024
@@ -954,22 +957,22 @@ def test_gemm_identity_and_oracle_every_instance(mx4, ctx, oracle, inst):
         for xt in xts:
             xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16) if xt == mx4.BF16 else x)
             yb = ctx.buffer(m * n * 4)
-            assert ctx.gemm_config(xb, xt, m, w, yb, wm, wn, tm, tn) == 0, mx4.last_error()
+            assert ctx.gemm_config(xb, xt, m, w, yb, wm, wn, tm, tn, ks) == 0, mx4.last_error()
             got = yb.download(np.float32).reshape(m, n)
             assert np.array_equal(got, dec[:, cols].T), f"identity m={m} xt={xt}"
         if inst in GEMM_BF16_ONLY:
             xb = ctx.to_device(x)
-            assert ctx.gemm_config(xb, mx4.F32, m, w, ctx.buffer(m * n * 4), wm, wn, tm, tn) == mx4.ERR_UNSUPPORTED
+            assert ctx.gemm_config(xb, mx4.F32, m, w, ctx.buffer(m * n * 4), wm, wn, tm, tn, ks) == mx4.ERR_UNSUPPORTED
         xr = oracle.bf16_to_f32(oracle.synth_bf16(1200 + m, 1.0, m * k)).reshape(m, k)
         for xt in xts:
             xin = xr if xt == mx4.BF16 else (xr + rng.standard_normal(xr.shape).astype(np.float32) * 1e-3)
             ref = oracle.matmul(xin, packed.reshape(-1), scales.reshape(-1))
             xb = ctx.to_device((f32_bits(xin) >> 16).astype(np.uint16) if xt == mx4.BF16 else xin)
             yb = ctx.buffer(m * n * 4)
-            assert ctx.gemm_config(xb, xt, m, w, yb, wm, wn, tm, tn) == 0, mx4.last_error()
+            assert ctx.gemm_config(xb, xt, m, w, yb, wm, wn, tm, tn, ks) == 0, mx4.last_error()
             got = yb.download(np.float32).reshape(m, n)
-            assert_close(got, ref, f"gemm {inst} m={m} xt={xt}", scaled=True)
-            assert ctx.gemm_config(xb, xt, m, w, yb, wm, wn, tm, tn) == 0
+            assert_close(got, ref, f"gemm {inst} ks={ks} m={m} xt={xt}", scaled=True)
+            assert ctx.gemm_config(xb, xt, m, w, yb, wm, wn, tm, tn, ks) == 0
             assert np.array_equal(yb.download(np.float32).reshape(m, n), got), "repeat"
     w.release()
 
@@ -1025,6 +1028,12 @@ def test_gemm_rejects_and_falls_back(mx4, ctx, oracle):
     yb = ctx.buffer(m * n * 4)
     xb = ctx.to_device(x2)
     assert ctx.gemm_config(xb, mx4.F32, m, w2, yb, 3, 3, 1, 1) == mx4.ERR_UNSUPPORTED
+    # a K split must cut K into whole 128-element stages
+    xb3 = ctx.to_device(rng.standard_normal((m, 384)).astype(np.float32))
+    w3 = ctx.synth_weight(7, n, 384, 0.02)
+    assert ctx.gemm_config(xb3, mx4.F32, m, w3, yb, 2, 2, 1, 1, 2) == mx4.ERR_UNSUPPORTED
+    assert ctx.gemm_config(xb3, mx4.F32, m, w3, yb, 2, 2, 1, 1, 3) == 0
+    w3.release()
     w.release()
     w2.release()
 
