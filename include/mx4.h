@@ -149,6 +149,22 @@ void mx4_weight_release(mx4_weight *w);
 mx4_status mx4_weight_info(const mx4_weight *w, uint32_t *rows, uint32_t *cols,
                            const uint8_t **packed_dev, const uint8_t **scales_dev);
 
+/* HBM a weight holds: its stored layout (packed + scales, or the bf16 matrix;
+ * 0 once dropped) and its matrix-core copy for the block-scaled prefill path
+ * (about 1.06x the packed size, 0 while not built). No counterpart in the
+ * reference (its GPU path reads the stored layout only). */
+mx4_status mx4_weight_footprint(const mx4_weight *w, uint64_t *stored_bytes, uint64_t *matrix_core_bytes);
+/* Free the matrix-core copy (after a prefill phase); a later prefill call
+ * builds it again, which allocates. Refused when it is the only layout left. */
+mx4_status mx4_weight_release_prefill(mx4_weight *w);
+/* Keep one resident copy of a weight that serves prefill only: build the
+ * matrix-core copy if needed, then free the stored layout. Afterwards only
+ * the prefill entry points (mx4_matmul_prefill*, mx4_prefill_matmul*,
+ * mx4_matmul_mx, mx4_matmul_prefill_noalloc) take the weight; the others fail
+ * with MX4_ERR_UNSUPPORTED, and mx4_weight_info reports null packed/scales.
+ * Only for weights whose memory the library owns (not mx4_weight_wrap). */
+mx4_status mx4_weight_drop_stored(mx4_weight *w);
+
 /* GpuModel::matmul (engine/src/gpu.rs:469-515): y_dev[m][rows] =
  * x_dev[m][cols] . W^T, enqueued on the context stream, exact arithmetic
  * (f32 accumulation of exact products). AUTO picks GEMV for m == 1, the

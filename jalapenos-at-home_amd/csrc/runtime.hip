@@ -75,6 +75,9 @@ struct mx4_weight {
     // bf16 weight [rows][cols] (a Tensor::bf16 of the reference); packed and
     // scales are null for such a weight
     uint16_t* bf16 = nullptr;
+    // false once mx4_weight_drop_stored freed the row-major layout (only the
+    // matrix-core copy is left: prefill entry points only)
+    bool stored = true;
 };
 
 struct mx4_pass {
@@ -244,6 +247,7 @@ mx4::PrefillArgs prefill_args(mx4_context* ctx, const mx4_weight* w, const uint8
 // The weight's fragment-native copy: built once, outside any recorded pass.
 mx4_status prepare_fragments(mx4_context* ctx, mx4_weight* w) {
     if (w->frag) return MX4_OK;
+    if (!w->stored) return fail(MX4_ERR_UNSUPPORTED, "the weight has neither its stored layout nor its matrix-core copy");
     if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the block-scaled MFMA path takes MXFP4 weights");
     if (w->cols % 256 != 0) return fail(MX4_ERR_UNSUPPORTED, "block-scaled MFMA path needs K %% 256 == 0");
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -284,8 +288,18 @@ mx4_status check_matmul_args(mx4_context* ctx, const void* x, mx4_dtype xt, uint
 // never produces more than 252). Other bytes go to the exact generic kernel.
 bool scales_foldable(const mx4_weight* w) { return w->min_scale >= 2 && w->max_scale <= 252; }
 
+// Entry points that read the weight's stored row-major layout refuse a weight
+// whose layout was dropped (mx4_weight_drop_stored).
+mx4_status need_stored(const mx4_weight* w) {
+    if (!w->stored)
+        return fail(MX4_ERR_UNSUPPORTED,
+                    "the weight's stored layout was dropped; only the prefill entry points take it");
+    return MX4_OK;
+}
+
 mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m, const mx4_weight* w,
                       float* y, mx4_path path) {
+    if (need_stored(w) != MX4_OK) return MX4_ERR_UNSUPPORTED;
     if (w->bf16) {
         // engine/src/lib.rs:255 `None` arm: one exact kernel for every M
         if (path != MX4_PATH_AUTO && path != MX4_PATH_GENERIC)
@@ -635,8 +649,48 @@ mx4_status mx4_weight_info(const mx4_weight* w, uint32_t* rows, uint32_t* cols, 
     if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
     if (rows) *rows = w->rows;
     if (cols) *cols = w->cols;
-    if (packed_dev) *packed_dev = w->packed;
-    if (scales_dev) *scales_dev = w->scales;
+    if (packed_dev) *packed_dev = w->stored ? w->packed : nullptr;
+    if (scales_dev) *scales_dev = w->stored ? w->scales : nullptr;
+    return MX4_OK;
+}
+
+mx4_status mx4_weight_footprint(const mx4_weight* w, uint64_t* stored_bytes, uint64_t* matrix_core_bytes) {
+    if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
+    const uint64_t e = (uint64_t)w->rows * w->cols;
+    if (stored_bytes) *stored_bytes = !w->stored ? 0 : (w->bf16 ? e * 2 : e / 2 + e / 32);
+    if (matrix_core_bytes)
+        *matrix_core_bytes = !w->frag ? 0
+                                      : ((mx4::fragment_bytes(w->rows, w->cols, false) + 255) & ~255ull) +
+                                            mx4::fragment_scale_bytes(w->rows, w->cols);
+    return MX4_OK;
+}
+
+mx4_status mx4_weight_release_prefill(mx4_weight* w) {
+    if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
+    if (!w->frag) return MX4_OK;
+    if (!w->stored) return fail(MX4_ERR_UNSUPPORTED, "the matrix-core copy is the weight's only layout");
+    DeviceGuard g(w->ctx->device);
+    HIP_TRY(hipStreamSynchronize(w->ctx->stream));
+    HIP_TRY(hipFree(w->frag));
+    w->frag = nullptr;
+    w->frag_scales = nullptr;
+    return MX4_OK;
+}
+
+mx4_status mx4_weight_drop_stored(mx4_weight* w) {
+    if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
+    if (!w->stored) return MX4_OK;
+    if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "a bf16 weight has no matrix-core copy");
+    if (!w->allocation) return fail(MX4_ERR_UNSUPPORTED, "a wrapped weight's memory belongs to the caller");
+    DeviceGuard g(w->ctx->device);
+    mx4_status st = prepare_fragments(w->ctx, w);
+    if (st != MX4_OK) return st;
+    HIP_TRY(hipStreamSynchronize(w->ctx->stream));
+    HIP_TRY(hipFree(w->allocation));
+    w->allocation = nullptr;
+    w->packed = nullptr;
+    w->scales = nullptr;
+    w->stored = false;
     return MX4_OK;
 }
 
@@ -661,6 +715,7 @@ mx4_status mx4_matmul_group(mx4_context* ctx, const void* x, mx4_dtype xt, uint3
         mx4_status st = check_matmul_args(ctx, x, xt, m, w[i], y[i]);
         if (st != MX4_OK) return fail(st, "weight %u: %s", i, g_error.c_str());
         if (w[i]->cols != w[0]->cols) return fail(MX4_ERR_SHAPE, "grouped weights must share their width");
+        if (need_stored(w[i]) != MX4_OK) return MX4_ERR_UNSUPPORTED;
     }
     DeviceGuard g(ctx->device);
     bool foldable = true;
@@ -702,6 +757,7 @@ mx4_status mx4_gemv_config(mx4_context* ctx, const void* x, mx4_dtype xt, const 
         if (st != MX4_OK) return st;
         if (w[i]->cols != w[0]->cols) return fail(MX4_ERR_SHAPE, "grouped weights must share their width");
         if (w[i]->bf16) return fail(MX4_ERR_UNSUPPORTED, "the GEMV configurations are for MXFP4 weights");
+        if (need_stored(w[i]) != MX4_OK) return MX4_ERR_UNSUPPORTED;
         if (!scales_foldable(w[i])) return fail(MX4_ERR_UNSUPPORTED, "scale bytes outside 2..252 need the generic kernel");
         gg.packed[i] = w[i]->packed;
         gg.scales[i] = w[i]->scales;
@@ -732,6 +788,7 @@ mx4_status mx4_gemm_config(mx4_context* ctx, const void* x, mx4_dtype xt, uint32
     mx4_status st = check_matmul_args(ctx, x, xt, m, w, y);
     if (st != MX4_OK) return st;
     if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the GEMM configurations are for MXFP4 weights");
+    if (need_stored(w) != MX4_OK) return MX4_ERR_UNSUPPORTED;
     if (!scales_foldable(w)) return fail(MX4_ERR_UNSUPPORTED, "scale bytes outside 2..252 need the generic kernel");
     if (!mx4::gemm_exact_supported(m, w->rows, w->cols, xt == MX4_BF16))
         return fail(MX4_ERR_UNSUPPORTED, "GEMM path needs K %% 128 == 0 and operands under 2 GiB");
@@ -756,6 +813,7 @@ mx4_status mx4_gemv_tokens_config(mx4_context* ctx, const void* x, uint32_t m, c
     mx4_status st = check_matmul_args(ctx, x, MX4_BF16, m, w, y);
     if (st != MX4_OK) return st;
     if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "the GEMV configurations are for MXFP4 weights");
+    if (need_stored(w) != MX4_OK) return MX4_ERR_UNSUPPORTED;
     if (!scales_foldable(w)) return fail(MX4_ERR_UNSUPPORTED, "scale bytes outside 2..252 need the generic kernel");
     if (!mx4::gemv_mt_supported(m, w->cols, true))
         return fail(MX4_ERR_UNSUPPORTED, "few-token GEMV needs 2 <= m <= 4 and K in {2048, 4096, 6144, 8192, 12288}");
@@ -1069,6 +1127,7 @@ mx4_status mx4_matmul_argmax(mx4_context* ctx, const void* x, mx4_dtype xt, cons
     if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
     if (((uintptr_t)x & 15) != 0) return fail(MX4_ERR_ARGUMENT, "x must be 16-byte aligned");
     if (y && ((uintptr_t)y & 3) != 0) return fail(MX4_ERR_ARGUMENT, "y must be 4-byte aligned");
+    if (need_stored(w) != MX4_OK) return MX4_ERR_UNSUPPORTED;
     DeviceGuard g(ctx->device);
     if (!w->bf16 && mx4::gemv_m1_supported(w->cols) && scales_foldable(w)) {
         mx4::GemvArgs a{w->packed, w->scales, x, y, 1, w->rows, w->cols, xt == MX4_BF16, ctx->stream};
@@ -1096,6 +1155,7 @@ mx4_status mx4_embed(mx4_context* ctx, const mx4_weight* w, const uint32_t* ids,
     if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
     if (w->cols % 32 != 0) return fail(MX4_ERR_SHAPE, "embedding rows must be a multiple of 32 wide");
     if (((uintptr_t)out & 15) != 0) return fail(MX4_ERR_ARGUMENT, "out must be 16-byte aligned");
+    if (need_stored(w) != MX4_OK) return MX4_ERR_UNSUPPORTED;
     DeviceGuard g(ctx->device);
     hipError_t e = mx4::launch_embed(w->packed, w->scales, w->bf16, ids, count, w->rows, w->cols, out, ctx->stream);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "embed launch failed: %s", hipGetErrorString(e));
@@ -1105,6 +1165,7 @@ mx4_status mx4_embed(mx4_context* ctx, const mx4_weight* w, const uint32_t* ids,
 mx4_status mx4_dequantize(mx4_context* ctx, const mx4_weight* w, float* out) {
     if (!ctx || !w || !out) return fail(MX4_ERR_ARGUMENT, "null argument");
     if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "not an MXFP4 weight");
+    if (need_stored(w) != MX4_OK) return MX4_ERR_UNSUPPORTED;
     DeviceGuard g(ctx->device);
     hipError_t e = mx4::launch_dequantize(w->packed, w->scales, (uint64_t)w->rows * w->cols, out, ctx->stream);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "dequantize launch failed: %s", hipGetErrorString(e));

@@ -68,6 +68,9 @@ SIGNATURES = {
     "mx4_gemv_config": (_int, [_vp, _vp, _int, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _u32, _int, _int, _int, _u32]),
     "mx4_gemv_tokens_config": (_int, [_vp, _vp, _u32, _vp, _vp, _u32, _u32]),
     "mx4_gemm_config": (_int, [_vp, _vp, _int, _u32, _vp, _vp, _int, _int, _int, _int, _int]),
+    "mx4_weight_footprint": (_int, [_vp, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "mx4_weight_release_prefill": (_int, [_vp]),
+    "mx4_weight_drop_stored": (_int, [_vp]),
     "mx4_matmul_batch": (_int, [_vp, _vp, _u32]),
     "mx4_matmul_mx": (_int, [_vp, _vp, _vp, _int, _u32, _vp, _vp]),
     "mx4_reserve_prefill": (_int, [_vp, _u32, _u32]),
@@ -216,6 +219,18 @@ class Weight:
     def prepare_prefill(self) -> None:
         """Build the matrix-core operand copy now (needed before recording prefill into a pass)."""
         check(lib().mx4_weight_prepare_prefill(self.handle))
+
+    def footprint(self) -> "tuple[int, int]":
+        """HBM bytes of the stored layout and of the matrix-core copy."""
+        a, b = ctypes.c_uint64(), ctypes.c_uint64()
+        check(lib().mx4_weight_footprint(self.handle, ctypes.byref(a), ctypes.byref(b)))
+        return a.value, b.value
+
+    def release_prefill(self) -> None:
+        check(lib().mx4_weight_release_prefill(self.handle))
+
+    def drop_stored(self) -> None:
+        check(lib().mx4_weight_drop_stored(self.handle))
 
     def release(self) -> None:
         # a weight never outlives its context (release after destroy is a use-after-free)

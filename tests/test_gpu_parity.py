@@ -1412,6 +1412,41 @@ def test_prefill_8b_shapes_sampled(mx4, ctx, oracle, name, act):
     w.release()
 
 
+def test_weight_layouts_footprint_release_and_drop(mx4, ctx, oracle):
+    """Resident layouts of one weight: the stored layout and the matrix-core
+    copy are reported; the copy can be released after a prefill phase and is
+    rebuilt on the next call (same results); a weight that serves prefill only
+    can drop its stored layout (one copy left), after which prefill results are
+    unchanged and every other entry point refuses it; a wrapped weight's
+    memory is the caller's and cannot be dropped."""
+    rng = np.random.default_rng(21)
+    m, n, k = 64, 200, 2048
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(118, 130, (n, k // 32), dtype=np.uint8)
+    w = ctx.upload_weight(packed, scales, n, k)
+    stored, copy = w.footprint()
+    assert stored == n * k // 2 + n * k // 32 and copy == 0
+    x = oracle.bf16_to_f32(oracle.synth_bf16(22, 1.0, m * k)).reshape(m, k)
+    y0 = _run_prefill(mx4, ctx, x, w, "mxfp4", mx4.BF16)
+    stored, copy = w.footprint()
+    assert copy >= n * k // 2 and copy < 1.2 * stored
+    w.release_prefill()
+    assert w.footprint() == (stored, 0)
+    assert np.array_equal(_run_prefill(mx4, ctx, x, w, "mxfp4", mx4.BF16), y0)
+    w.drop_stored()
+    assert w.footprint()[0] == 0 and w.footprint()[1] == copy
+    assert np.array_equal(_run_prefill(mx4, ctx, x, w, "mxfp4", mx4.BF16), y0)
+    with pytest.raises(mx4.Mx4Error, match="stored layout was dropped"):
+        run_matmul(mx4, ctx, x, w, mx4.PATH_AUTO, mx4.BF16)
+    with pytest.raises(mx4.Mx4Error, match="only layout"):
+        w.release_prefill()
+    w.release()
+    w2 = ctx.synth_weight(23, n, k, 0.02)  # wrapped around a buffer the caller owns
+    with pytest.raises(mx4.Mx4Error, match="belongs to the caller"):
+        w2.drop_stored()
+    w2.release()
+
+
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
 def test_prefill_8b_gate_up_group(mx4, ctx, oracle, act):
     """gate|up at M = 512 through mx4_matmul_prefill_group (engine/src/lib.rs:459-467:
