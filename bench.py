@@ -632,7 +632,8 @@ def summarize(kind: str, dirs: list[str]) -> None:
     """Markdown summaries of rocprofv3 CSV output (run here, on the pulled-back
     files): `trace DIR` (kernel stats of --profile-step), `traffic FETCH_DIR
     WRITE_DIR` (FETCH_SIZE / WRITE_SIZE of --profile-traffic, calibrated by the
-    1 GiB copy), `prefill-trace DIR` and `prefill-pmc DIR` (--profile-prefill)."""
+    1 GiB copy), `step-pmc DIR` (per-launch averages of any counters of
+    --profile-traffic), `prefill-trace DIR` and `prefill-pmc DIR` (--profile-prefill)."""
     d0 = Path(dirs[0])
     st = _stamp_of(d0)
     print(f"commit: {_git_head()}")
@@ -698,18 +699,20 @@ def summarize(kind: str, dirs: list[str]) -> None:
         for r in rows:
             nm = _short(r["Kernel_Name"])
             if nm.startswith("mx4::prefill") or nm.startswith("mx4::quantize_fragments"):
-                per[(nm, r["Grid_Size"])].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+                grid = r.get("Grid_Size") or r.get("Grid_Size_X")
+                per[(nm, grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
         print("\n| kernel | grid | dispatches | median us | min us |")
         print("|---|---|---|---|---|")
         for (nm, g), ts in sorted(per.items()):
             print(f"| {nm} | {g} | {len(ts)} | {np.median(ts):.2f} | {min(ts):.2f} |")
-    elif kind == "prefill-pmc":
+    elif kind in ("prefill-pmc", "step-pmc"):
+        prefix = "mx4::prefill" if kind == "prefill-pmc" else "mx4::gemv"
         rows = _read_csv(d0, "counter_collection.csv")
         per = defaultdict(lambda: defaultdict(float))
         meta = {}
         for r in rows:
             nm = _short(r["Kernel_Name"])
-            if not nm.startswith("mx4::prefill"):
+            if not nm.startswith(prefix):
                 continue
             did = r["Dispatch_Id"]
             per[did][r["Counter_Name"]] += float(r["Counter_Value"])
@@ -751,7 +754,7 @@ def main() -> int:
     ap.add_argument("--stamp", help="profile modes: also write the stamp (library sha256, workload) to this file")
     ap.add_argument("--summarize", nargs="+", metavar=("KIND", "DIR"),
                     help="print the markdown summary of rocprofv3 CSV output: trace DIR | traffic FETCH_DIR "
-                         "WRITE_DIR | prefill-trace DIR | prefill-pmc DIR")
+                         "WRITE_DIR | step-pmc DIR | prefill-trace DIR | prefill-pmc DIR")
     args = ap.parse_args()
 
     if args.summarize:
