@@ -324,6 +324,197 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
+// Workgroup-shared operands: a workgroup of WM x WN waves owns a BM x BN
+// output tile over the whole of K. Each stage (U k-steps) of both operands'
+// fragments -- and the scale words of its quad -- is loaded once per
+// workgroup, straight into LDS by direct-to-LDS buffer loads (one 1 KiB
+// fragment per instruction), into a ring of D stages with D - 1 in flight; a
+// wave reads its TM A and TN B fragments of a k-step from LDS (16 bytes per
+// lane at 16 l, the operand order) and issues its TM x TN MFMAs. One barrier
+// per stage; no K split, so no partial tiles to reduce.
+template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D>
+struct LdsGeo {
+    static constexpr int NW = WM * WN, NT = 64 * NW;
+    static constexpr int GA = WM * TM, GB = WN * TN;  // row groups of 32 per tile
+    static constexpr int BM = 32 * GA, BN = 32 * GB;
+    static constexpr int AFK = A_FP8 ? 2 : 1;         // 1 KiB pieces per A fragment
+    static constexpr int A_BYTES = U * GA * AFK * 1024, B_BYTES = U * GB * 1024;
+    static constexpr int SA = (GA + 3) / 4, SB = (GB + 3) / 4;  // scale loads (4 groups each)
+    static constexpr int S_BYTES = NW * 1024;                     // one 1 KiB slot per wave
+    static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+    static constexpr int FRAGS = U * (GA * AFK + GB), FI = FRAGS / NW;
+    static constexpr int LPS = FI + 1;  // vector memory instructions per wave and stage
+    // stages of 2 or 4 k-steps (a scale quad in one or two stages); every wave
+    // loads the same number of fragments and one scale piece per stage; the
+    // waits fit vmcnt; the ring fits the LDS
+    static constexpr bool ok = (U == 2 || U == 4) && FRAGS % NW == 0 && SA + SB <= NW && D >= 2 && D <= 5 &&
+                               (D - 2) * LPS <= 63 && D * STAGE <= 160 * 1024;
+};
+
+template <int LPS, int MAXA>
+__device__ __forceinline__ void wait_ahead(uint32_t ahead) {
+    // outstanding loads allowed: those of the `ahead` stages issued after the one needed
+    if constexpr (MAXA >= 3) {
+        if (ahead >= 3) { wait_vm<3 * LPS>(); return; }
+    }
+    if constexpr (MAXA >= 2) {
+        if (ahead == 2) { wait_vm<2 * LPS>(); return; }
+    }
+    if constexpr (MAXA >= 1) {
+        if (ahead == 1) { wait_vm<LPS>(); return; }
+    }
+    wait_vm<0>();
+}
+
+template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D>
+__global__ __launch_bounds__(64 * WM * WN) void prefill_lds_kernel(const Segs segs, const uint8_t* __restrict__ xf,
+                                                                  const uint8_t* __restrict__ xsf, uint32_t m,
+                                                                  uint32_t k) {
+    using G = LdsGeo<A_FP8, WM, WN, TM, TN, U, D>;
+    static_assert(G::ok, "instance outside the kernel's stage, vmcnt and LDS limits");
+    constexpr uint32_t AF = A_FP8 ? 2048 : 1024;
+    constexpr int P = 4 / U;  // stages per scale quad
+    __shared__ __attribute__((aligned(16))) uint8_t lds[D * G::STAGE];
+    const uint32_t lane = threadIdx.x % 64;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t wm = wave / WN, wn = wave % WN;
+    const uint32_t bx = blockIdx.x;
+    const uint8_t* __restrict__ wf = segs.wf[0];
+    const uint8_t* __restrict__ wsf = segs.wsf[0];
+    float* __restrict__ y = segs.y[0];
+    uint32_t n = segs.n[0], t0 = 0;
+#pragma unroll
+    for (int s = 1; s < (int)kMaxPrefillGroup; ++s) {
+        const bool in = bx >= segs.tile0[s];
+        wf = in ? segs.wf[s] : wf;
+        wsf = in ? segs.wsf[s] : wsf;
+        y = in ? segs.y[s] : y;
+        n = in ? segs.n[s] : n;
+        t0 = in ? segs.tile0[s] : t0;
+    }
+    const uint32_t ga0 = blockIdx.y * G::GA, gb0 = (bx - t0) * G::GB;  // first row groups of the tile
+    const uint32_t nk_all = k / 64, nq_all = k / 256, stages = nk_all / U;
+    const uint32_t ga_n = (m + 31) / 32, gb_n = (n + 31) / 32;
+    const __amdgpu_buffer_rsrc_t xr = rsrc(xf, ga_n * nk_all * AF);
+    const __amdgpu_buffer_rsrc_t xsr = rsrc(xsf, ga_n * nq_all * 256);
+    const __amdgpu_buffer_rsrc_t wr = rsrc(wf, gb_n * nk_all * 1024);
+    const __amdgpu_buffer_rsrc_t wsr = rsrc(wsf, gb_n * nq_all * 256);
+
+    // This wave's scale load: instruction (wave mod SA + SB) -- A groups 4i..4i+3
+    // or B groups 4(i - SA).. -- into LDS slot `wave`; lane l takes 16 bytes of
+    // group 4i + l / 16 (clamped to the tile's last group: the duplicate lands
+    // in bytes nobody reads).
+    const uint32_t si = wave % (G::SA + G::SB);
+    const bool s_is_a = si < (uint32_t)G::SA;
+    const uint32_t s_grp = (s_is_a ? si : si - G::SA) * 4 + lane / 16;
+    const uint32_t s_last = s_is_a ? G::GA - 1 : G::GB - 1;
+    const uint32_t s_row = (s_is_a ? ga0 : gb0) + (s_grp < s_last ? s_grp : s_last);
+    const uint32_t s_goff = s_row * nq_all * 256 + (lane % 16) * 16;
+    const __amdgpu_buffer_rsrc_t s_r = s_is_a ? xsr : wsr;
+
+    auto issue = [&](uint32_t st, uint32_t slot) {
+        uint8_t* base = lds + slot * G::STAGE;
+#pragma unroll
+        for (int q = 0; q < G::FI; ++q) {
+            // fragment f of the stage: A pieces first, then B; uniform selects
+            // rather than a branch (the compiler waits for every load at a join)
+            const uint32_t f = q * G::NW + wave;
+            const bool is_a = f < (uint32_t)(U * G::GA * G::AFK);
+            const uint32_t fa = f, kka = fa / (G::GA * G::AFK), rem = fa % (G::GA * G::AFK);
+            const uint32_t ia = rem / G::AFK, half = rem % G::AFK;
+            const uint32_t fb = f - U * G::GA * G::AFK, kkb = fb / G::GB, jb = fb % G::GB;
+            const uint32_t lds_off = is_a ? (kka * G::GA + ia) * AF + half * 1024
+                                          : G::A_BYTES + (kkb * G::GB + jb) * 1024;
+            const uint32_t goff = is_a ? ((ga0 + ia) * nk_all + st * U + kka) * AF + half * 1024
+                                       : ((gb0 + jb) * nk_all + st * U + kkb) * 1024;
+            load_lds16(is_a ? xr : wr, (lds_ptr)(base + lds_off), goff + 16 * lane);
+        }
+        load_lds16(s_r, (lds_ptr)(base + G::A_BYTES + G::B_BYTES + wave * 1024), s_goff + (st / P) * 256);
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    // k-step kk of the stage in `slot`; the scale byte of k-step (E U + kk) of the quad
+    auto compute = [&](uint32_t slot, auto e_tag) {
+        constexpr int E = decltype(e_tag)::value;
+        const uint8_t* base = lds + slot * G::STAGE;
+        const uint8_t* sbase = base + G::A_BYTES + G::B_BYTES;
+        uint32_t sa[TM], sb[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const uint32_t g = wm * TM + i;
+            sa[i] = *reinterpret_cast<const uint32_t*>(sbase + (g / 4) * 1024 + (g % 4) * 256 + 4 * lane);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint32_t g = wn * TN + j;
+            sb[j] = *reinterpret_cast<const uint32_t*>(sbase + (G::SA + g / 4) * 1024 + (g % 4) * 256 + 4 * lane);
+        }
+#pragma unroll
+        for (int kk = 0; kk < U; ++kk) {
+            u32x4 a[TM][A_FP8 ? 2 : 1], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const uint8_t* ap = base + (kk * G::GA + wm * TM + i) * AF + 16 * lane;
+                a[i][0] = *reinterpret_cast<const u32x4*>(ap);
+                if constexpr (A_FP8) a[i][1] = *reinterpret_cast<const u32x4*>(ap + 1024);
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                b[j] = *reinterpret_cast<const u32x4*>(base + G::A_BYTES + (kk * G::GB + wn * TN + j) * 1024 + 16 * lane);
+            constexpr int o0 = E * U;
+            switch (o0 + kk) {
+                case 0: kstep<0, A_FP8, TM, TN>(a, b, sa, sb, acc); break;
+                case 1: kstep<1, A_FP8, TM, TN>(a, b, sa, sb, acc); break;
+                case 2: kstep<2, A_FP8, TM, TN>(a, b, sa, sb, acc); break;
+                default: kstep<3, A_FP8, TM, TN>(a, b, sa, sb, acc); break;
+            }
+        }
+    };
+
+#pragma unroll
+    for (int p = 0; p < D - 1; ++p)
+        if ((uint32_t)p < stages) issue(p, p);
+    for (uint32_t st0 = 0; st0 < stages; st0 += P) {
+#pragma unroll
+        for (int e = 0; e < P; ++e) {
+            const uint32_t st = st0 + e;
+            const uint32_t left = stages - 1 - st;
+            wait_ahead<G::LPS, D - 2>(left < (uint32_t)(D - 2) ? left : (uint32_t)(D - 2));
+            lds_barrier();
+            if (st + D - 1 < stages) issue(st + D - 1, (st + D - 1) % D);
+            if (e == 0) compute(st % D, std::integral_constant<int, 0>{});
+            else if constexpr (P > 1) compute(st % D, std::integral_constant<int, (P > 1 ? 1 : 0)>{});
+        }
+    }
+    mfma_drain();
+
+    // Branch-free device-scope stores through a resource over y, as in prefill_kernel.
+    constexpr int kStoreDeviceScope = 0x10;
+    const uint32_t r32 = lane % 32, h = lane / 32;
+    const uint32_t m0 = ga0 * 32 + wm * 32 * TM, n0 = gb0 * 32 + wn * 32 * TN;
+    const __amdgpu_buffer_rsrc_t yr = rsrc(y, m * n * 4);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const uint32_t col = n0 + 32 * j + r32;
+        const uint32_t cb = 4 * col + (col < n ? 0u : 0x80000000u);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t row = m0 + 32 * i + 8 * (v / 4) + 4 * h + (v % 4);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][v]), yr, row * n * 4 + cb, 0,
+                                                      kStoreDeviceScope);
+            }
+    }
+}
+
 // Row-major codes -> fragment-native order. One thread per 16-byte output
 // chunk; rows past `rows` (the padding of the last group) are zero.
 template <bool FP8>
@@ -392,6 +583,41 @@ hipError_t go(const PrefillArgs& a) {
     return hipGetLastError();
 }
 
+// The deepest ring of at most D stages that the kernel's limits allow (D when none is smaller than 3).
+template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D>
+constexpr int fit_depth() {
+    if constexpr (D <= 2 || LdsGeo<A_FP8, WM, WN, TM, TN, U, D>::ok) return D;
+    else return fit_depth<A_FP8, WM, WN, TM, TN, U, D - 1>();
+}
+
+template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D>
+hipError_t go_lds(const PrefillArgs& a) {
+    using G = LdsGeo<A_FP8, WM, WN, TM, TN, U, D>;
+    if constexpr (!G::ok) {
+        return hipErrorNotSupported;
+    } else {
+        if (a.k % 256 != 0) return hipErrorNotSupported;
+        Segs sg{};
+        uint32_t cols = 0;
+        for (uint32_t s = 0; s < kMaxPrefillGroup; ++s) {
+            if (s < a.count) {
+                sg.wf[s] = a.wf[s];
+                sg.wsf[s] = a.wsf[s];
+                sg.y[s] = a.y[s];
+                sg.n[s] = a.n[s];
+                sg.tile0[s] = cols;
+                cols += (a.n[s] + G::BN - 1) / G::BN;
+            } else {
+                sg.tile0[s] = 0xffffffffu;
+            }
+        }
+        dim3 grid(cols, (a.m + G::BM - 1) / G::BM);
+        hipLaunchKernelGGL((prefill_lds_kernel<A_FP8, WM, WN, TM, TN, U, D>), grid, dim3(G::NT), 0, a.stream, sg,
+                           a.xf, a.xsf, a.m, a.k);
+        return hipGetLastError();
+    }
+}
+
 // Wave tiles of TM x TN fragments with K in KS parts inside the workgroup,
 // four k-steps in flight per wave; unrolled for the model's K sizes. Each
 // part must start on a whole scale quad (four k-steps).
@@ -405,6 +631,35 @@ hipError_t go_parts(const PrefillArgs& a) {
 
 template <bool A_FP8>
 hipError_t dispatch(const PrefillArgs& a) {
+    if (a.tile_m != 0 && a.split_k >= 16) {
+        // workgroup-shared operands (prefill_lds_kernel): split_k = 16 U + D
+        // (stages of U k-steps, a ring of D), tile_m x tile_n workgroup tiles;
+        // a ring too deep for the LDS is cut to the deepest that fits
+        const uint32_t u = a.split_k / 16, d = a.split_k % 16;
+#define MX4_LDS(BM_, BN_, WM_, WN_, TM_, TN_)                                                           \
+        if (a.tile_m == BM_ && a.tile_n == BN_) {                                                       \
+            constexpr int WM_c = WM_, WN_c = WN_, TM_c = TM_, TN_c = TN_;                               \
+            if (u == 4 && d == 2) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 4, 2>(a);                  \
+            if (u == 4 && d == 3) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 4,                         \
+                                                fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 4, 3>()>(a);       \
+            if (u == 2 && d == 3) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 2, 3>(a);                  \
+            if (u == 2 && d == 4) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 2,                         \
+                                                fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 2, 4>()>(a);       \
+            if (u == 2 && d == 5) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 2,                         \
+                                                fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 2, 5>()>(a);       \
+            return hipErrorNotSupported;                                                                \
+        }
+        MX4_LDS(128, 192, 2, 2, 2, 3)
+        MX4_LDS(128, 128, 2, 2, 2, 2)
+        MX4_LDS(64, 128, 2, 2, 1, 2)
+        MX4_LDS(128, 64, 2, 2, 2, 1)
+        MX4_LDS(64, 256, 1, 4, 2, 2)
+        MX4_LDS(128, 96, 4, 1, 1, 3)
+        MX4_LDS(64, 192, 2, 2, 1, 3)
+        MX4_LDS(64, 64, 2, 2, 1, 1)
+#undef MX4_LDS
+        return hipErrorNotSupported;
+    }
     if (a.tile_m != 0) {
         // tuning: one explicit instance. Workgroup tiles: 128 x 192 and
         // 128 x 128 over the full K; 64 x 128 with K halves inside it; wave
@@ -431,6 +686,26 @@ hipError_t dispatch(const PrefillArgs& a) {
     }
     uint32_t ntot = 0;
     for (uint32_t s = 0; s < a.count; ++s) ntot += a.n[s];
+    // Workgroup-shared operands (prefill_lds_kernel) where they measured faster,
+    // cold weights at M = 512 (Qwen3-8B, K = 4096; split_k code 16 U + D of the
+    // tuning call):
+    //  q|k|v (6144 rows): 64 x 128 tiles; MXFP4 in stages of 2 k-steps, 4 deep
+    //  (19.4 -> 14.7 us), MX-FP8 in stages of 4, 2 deep (24.0 -> 18.2 us);
+    //  gate|up (24576 rows), MXFP4: 128 x 192 tiles in stages of 2, 3 deep, so
+    //  two workgroups share a CU (46.1 -> 43.2 us);
+    //  q / o (4096 rows), MXFP4: 128 x 64 tiles in stages of 2, 4 deep
+    //  (12.3 -> 11.3 us).
+    // gate or down alone and the other MX-FP8 shapes measured no faster there.
+    if (a.k == 4096) {
+        if (ntot > 4096 && ntot <= 8192) {
+            if constexpr (A_FP8) return go_lds<true, 2, 2, 1, 2, 4, 2>(a);
+            else return go_lds<false, 2, 2, 1, 2, 2, 4>(a);
+        }
+        if constexpr (!A_FP8) {
+            if (ntot >= 16384) return go_lds<false, 2, 2, 2, 3, 2, 3>(a);
+            if (ntot <= 4096) return go_lds<false, 2, 2, 2, 1, 2, 4>(a);
+        }
+    }
     // measured on MI355X at M = 512 (Qwen3-8B shapes): wide N takes 4 x 3 tiles
     // per wave with K in halves (gate/up: MXFP4 23.0 -> 21.9 us, MX-FP8 36.8
     // -> 27.6 us against 2 x 3 tiles over the full K); otherwise 2 x 2 tiles

@@ -1231,7 +1231,107 @@ def test_prefill_instances_match_oracle(mx4, ctx, oracle, act, k, tile):
     assert np.array_equal(outs[0], outs[1])
 
 
-GROUP_TILES = [(0, 0, 0), (128, 192, 1), (128, 128, 1), (64, 128, 2), (128, 192, 2), (128, 64, 4), (64, 128, 4)]
+# Workgroup-shared prefill instances: tile -> waves along M x N and MFMA tiles
+# per wave along M x N; split_k code 16 U + D (stages of U k-steps, ring of D).
+LDS_TILES = {(128, 192): (2, 2, 2, 3), (128, 128): (2, 2, 2, 2), (64, 128): (2, 2, 1, 2), (128, 64): (2, 2, 2, 1),
+             (64, 256): (1, 4, 2, 2), (128, 96): (4, 1, 1, 3), (64, 192): (2, 2, 1, 3), (64, 64): (2, 2, 1, 1)}
+LDS_CODES = (16 * 4 + 2, 16 * 4 + 3, 16 * 2 + 3, 16 * 2 + 4, 16 * 2 + 5)
+
+
+def lds_depth(fp8, tile, u, d):
+    """The ring depth the library compiles for (tile, U, D), or None: the
+    kernel's limits (whole fragments per wave and stage, one scale piece per
+    wave, waits within vmcnt, the ring within 160 KiB of LDS), a ring that does
+    not fit cut to the deepest that does (not below 2)."""
+    wm, wn, tm, tn = LDS_TILES[tile]
+    nw, ga, gb, afk = wm * wn, wm * tm, wn * tn, 2 if fp8 else 1
+    frags = u * (ga * afk + gb)
+    stage = u * ga * afk * 1024 + u * gb * 1024 + nw * 1024
+
+    def ok(dd):
+        return (frags % nw == 0 and (ga + 3) // 4 + (gb + 3) // 4 <= nw and 2 <= dd <= 5
+                and (dd - 2) * (frags // nw + 1) <= 63 and dd * stage <= 160 * 1024)
+    # (U, D) = (4, 2) and (2, 3) are compiled as asked; the deeper codes are cut to fit
+    if (u, d) in ((4, 2), (2, 3)):
+        return d if ok(d) else None
+    while d > 2 and not ok(d):
+        d -= 1
+    return d if ok(d) else None
+
+
+LDS_CASES = ([(4096, t, c) for t in LDS_TILES for c in LDS_CODES] +
+             [(k, t, c) for k in (256, 1280) for t in LDS_TILES for c in (16 * 4 + 2, 16 * 2 + 4)])
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+@pytest.mark.parametrize("k,tile,code", LDS_CASES, ids=[f"k{k}-{t[0]}x{t[1]}-u{c // 16}d{c % 16}" for k, t, c in LDS_CASES])
+def test_prefill_shared_instances_match_oracle(mx4, ctx, oracle, act, k, tile, code):
+    """Every workgroup-shared prefill instance reachable through
+    mx4_prefill_config is compiled exactly where the kernel's limits allow it;
+    each one, on ragged m and n (partial row groups and partial workgroup
+    tiles), and at K = 256 / 1280 (fewer stages than the ring, an odd number of
+    scale quads), matches the oracle on dequant(requant(x)), twice bitwise equal."""
+    fp8 = act == "mxfp8"
+    u, d = code // 16, code % 16
+    depth = lds_depth(fp8, tile, u, d)
+    m, n = 70, 300
+    acode = mx4.ACT_MXFP8 if fp8 else mx4.ACT_MXFP4
+    w = ctx.synth_weight(800 + k // 256, n, k, 0.02)
+    codes, sc = ctx.prefill_act_buffers(m, k, acode)
+    x = oracle.bf16_to_f32(oracle.synth_bf16(810 + k // 256, 1.0, m * k)).reshape(m, k)
+    xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+    ctx.prefill_quantize(xb, mx4.BF16, m, k, acode, codes, sc)
+    yb = ctx.buffer(m * n * 4)
+    status = ctx.prefill_config(codes, sc, acode, m, w, yb, tile[0], tile[1], code)
+    if depth is None:
+        assert status == mx4.ERR_UNSUPPORTED
+        return
+    assert status == 0, mx4.last_error()
+    say(f"shared prefill {act} k={k} tile={tile} U={u} D={depth}")
+    packed, scales = ctx.download_weight(w)
+    ref, _ = _prefill_ref(oracle, x, packed, scales, act)
+    outs = []
+    for _ in range(2):
+        yb.upload(np.full(m * n, np.nan, np.float32))
+        assert ctx.prefill_config(codes, sc, acode, m, w, yb, tile[0], tile[1], code) == 0, mx4.last_error()
+        outs.append(yb.download(np.float32).reshape(m, n))
+    assert_close(outs[0], ref, f"shared prefill {tile} U={u} D={depth} k={k} {act}")
+    assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+@pytest.mark.parametrize("tile", list(LDS_TILES), ids=[f"{t[0]}x{t[1]}" for t in LDS_TILES])
+def test_prefill_shared_identity_is_exact(mx4, ctx, oracle, act, tile):
+    """One-hot activations through each workgroup-shared tile (stages of 4 and
+    of 2 k-steps): the decoded weights bit for bit, which pins the LDS
+    placement of every fragment and scale piece, the op_sel of each k-step
+    within its quad and the output layout."""
+    rng = np.random.default_rng(37)
+    n, k, m = 200, 1024, 96
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(100, 150, (n, k // 32), dtype=np.uint8)
+    w = ctx.upload_weight(packed, scales, n, k)
+    cols = rng.choice(k, m, replace=False)
+    x = np.zeros((m, k), np.float32)
+    x[np.arange(m), cols] = 1.0
+    acode = mx4.ACT_MXFP8 if act == "mxfp8" else mx4.ACT_MXFP4
+    codes, sc = ctx.prefill_act_buffers(m, k, acode)
+    ctx.prefill_quantize(ctx.to_device(np.ascontiguousarray(x, np.float32)), mx4.F32, m, k, acode, codes, sc)
+    dec = oracle.dequantize(packed, scales)
+    yb = ctx.buffer(m * n * 4)
+    ran = 0
+    for code in (16 * 4 + 2, 16 * 2 + 3):
+        if lds_depth(act == "mxfp8", tile, code // 16, code % 16) is None:
+            continue
+        yb.upload(np.full(m * n, np.nan, np.float32))
+        assert ctx.prefill_config(codes, sc, acode, m, w, yb, tile[0], tile[1], code) == 0, mx4.last_error()
+        assert np.array_equal(yb.download(np.float32).reshape(m, n), dec[:, cols].T), (tile, code)
+        ran += 1
+    assert ran >= 1
+
+
+GROUP_TILES = [(0, 0, 0), (128, 192, 1), (128, 128, 1), (64, 128, 2), (128, 192, 2), (128, 64, 4), (64, 128, 4),
+               (64, 128, 16 * 2 + 4), (128, 192, 16 * 2 + 3), (64, 128, 16 * 4 + 2)]
 
 
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
@@ -1312,6 +1412,10 @@ def test_prefill_config_rejects_unknown_instance(mx4, ctx):
     yb = ctx.buffer(m * n * 4)
     assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 96, 256, 1) == mx4.ERR_UNSUPPORTED
     assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 64, 64, 4) == mx4.ERR_UNSUPPORTED
+    # workgroup-shared kernel: a tile it does not compile, a stage of 3 k-steps, a ring of 6
+    assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 96, 64, 16 * 4 + 2) == mx4.ERR_UNSUPPORTED
+    assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 64, 128, 16 * 3 + 3) == mx4.ERR_UNSUPPORTED
+    assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 64, 128, 16 * 2 + 6) == mx4.ERR_UNSUPPORTED
     # K quarters must start on whole scale quads (K % 1024 == 0)
     w2 = ctx.synth_weight(8, n, 1536, 0.02)
     codes2, sc2 = ctx.prefill_act_buffers(m, 1536, mx4.ACT_MXFP4)
