@@ -886,17 +886,37 @@ hipError_t launch_gemv_m1_group(const GemvGroup& g, int cus, const M1Config* for
 
 // M = 1 projection with the greedy-argmax epilogue (the lm_head of a greedy
 // decode step): y is optional (nullptr: logits are not written), *idx gets the
-// first index of the maximum. Instantiated for the lm_head configurations
-// (one-wave teams, 1-2 blocks per lane, 2 or 4 rows); others report
-// hipErrorNotSupported and the caller runs the projection and argmax_rows.
-template <bool XBF16, int BPL, int R>
+// first index of the maximum. It runs the projection's own default launch
+// shape when an epilogue instance of it is compiled -- one- and two-wave teams
+// of 1-2 blocks per lane, 2 or 4 rows, at most 8 waves per workgroup (the
+// 8B and 1.7B lm_heads) -- so the logits it writes are the projection's bit
+// for bit; other shapes fall back to the one-wave vocabulary configuration,
+// and where that does not fit either the caller gets hipErrorNotSupported and
+// runs the projection and argmax_rows.
+template <bool XBF16, int WG, int BPL, int R>
 static hipError_t go_am(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int tpw, uint32_t* idx, hipStream_t st) {
-    const size_t lds = (tpw > 1 ? (size_t)k * (XBF16 ? 2 : 4) : 0) + (size_t)tpw * 2 * R * sizeof(float);
-    hipLaunchKernelGGL((gemv_m1_one_kernel<XBF16, 1, BPL, R, true>), dim3(grid), dim3(64 * tpw), lds, st, sg.packed[0],
-                       sg.scales[0], x, sg.n[0], k, sg.rowsets, (uint32_t)tpw, grid, sg.y[0], sg.am_partial);
+    const size_t lds = (tpw > 1 ? (size_t)k * (XBF16 ? 2 : 4) : 0) + (size_t)tpw * 2 * WG * R * sizeof(float);
+    hipLaunchKernelGGL((gemv_m1_one_kernel<XBF16, WG, BPL, R, true>), dim3(grid), dim3(64 * WG * tpw), lds, st,
+                       sg.packed[0], sg.scales[0], x, sg.n[0], k, sg.rowsets, (uint32_t)tpw, grid, sg.y[0],
+                       sg.am_partial);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_argmax_reduce(sg.am_partial, 1, grid, idx, st);
+}
+
+template <bool XBF16>
+static hipError_t go_am_cfg(const Segs& sg, const void* x, uint32_t k, uint32_t grid, int wg, int bpl, int r, int tpw,
+                            uint32_t* idx, hipStream_t st) {
+#define MX4_AM_CASE(W, B, R_) \
+    if (wg == W && bpl == B && r == R_) return go_am<XBF16, W, B, R_>(sg, x, k, grid, tpw, idx, st);
+    MX4_AM_CASE(1, 1, 2) MX4_AM_CASE(1, 1, 4) MX4_AM_CASE(1, 2, 2) MX4_AM_CASE(1, 2, 4)
+    MX4_AM_CASE(2, 1, 2) MX4_AM_CASE(2, 1, 4)
+#undef MX4_AM_CASE
+    return hipErrorNotSupported;
+}
+
+static bool am_compiled(int wg, int bpl, int r) {
+    return (wg == 1 && (bpl == 1 || bpl == 2) && (r == 2 || r == 4)) || (wg == 2 && bpl == 1 && (r == 2 || r == 4));
 }
 
 hipError_t launch_gemv_m1_argmax(const GemvArgs& a, uint64_t* partial, uint32_t max_partials, uint32_t* idx,
@@ -904,14 +924,14 @@ hipError_t launch_gemv_m1_argmax(const GemvArgs& a, uint64_t* partial, uint32_t 
     if (!gemv_m1_supported(a.k) || a.n == 0) return hipErrorNotSupported;
     M1Config c;
     default_m1_config(a.k, a.n, cus, c);
-    if (c.wg != 1) {
-        // the argmax instances are one-wave teams: the vocabulary-sized
-        // one-wave configuration (4 rows, 4 teams per CU, 4 per workgroup)
-        c.wg = 1; c.r = 4; c.grid = 4 * (uint32_t)(cus > 0 ? cus : 256); c.tpw = 4;
-    }
     const uint32_t nblk = a.k / 32;
-    const int bpl = (int)(nblk / 64);
-    if ((bpl != 1 && bpl != 2) || (c.r != 2 && c.r != 4)) return hipErrorNotSupported;
+    int bpl = (int)(nblk / (64u * c.wg));
+    if (!am_compiled(c.wg, bpl, c.r) || c.tpw * c.wg > 8) {
+        // the one-wave vocabulary-sized configuration (4 rows, 4 teams per CU, 4 per workgroup)
+        c.wg = 1; c.r = 4; c.grid = 4 * (uint32_t)(cus > 0 ? cus : 256); c.tpw = 4;
+        bpl = (int)(nblk / 64);
+        if (!am_compiled(c.wg, bpl, c.r)) return hipErrorNotSupported;
+    }
     Segs sg{};
     sg.count = 1;
     sg.packed[0] = a.packed;
@@ -923,22 +943,15 @@ hipError_t launch_gemv_m1_argmax(const GemvArgs& a, uint64_t* partial, uint32_t 
     sg.rowsets = rowsets;
     sg.am_partial = partial;
     const int tpw = c.tpw < 1 ? 1 : c.tpw;
-    if (tpw > 1 && (uint64_t)a.k * (a.x_bf16 ? 2 : 4) + (uint64_t)tpw * 2 * c.r * 4 > 65536) return hipErrorNotSupported;
+    if (tpw > 1 && (uint64_t)a.k * (a.x_bf16 ? 2 : 4) + (uint64_t)tpw * 2 * c.wg * c.r * 4 > 65536)
+        return hipErrorNotSupported;
     uint32_t teams = c.grid == 0 || c.grid > rowsets ? rowsets : c.grid;
     const uint32_t per = (rowsets + teams - 1) / teams;
     teams = (rowsets + per - 1) / per;
     const uint32_t grid = (teams + tpw - 1) / tpw;
     if (grid > max_partials) return hipErrorNotSupported;
-    if (a.x_bf16) {
-        if (bpl == 1) return c.r == 2 ? go_am<true, 1, 2>(sg, a.x, a.k, grid, tpw, idx, a.stream)
-                                      : go_am<true, 1, 4>(sg, a.x, a.k, grid, tpw, idx, a.stream);
-        return c.r == 2 ? go_am<true, 2, 2>(sg, a.x, a.k, grid, tpw, idx, a.stream)
-                        : go_am<true, 2, 4>(sg, a.x, a.k, grid, tpw, idx, a.stream);
-    }
-    if (bpl == 1) return c.r == 2 ? go_am<false, 1, 2>(sg, a.x, a.k, grid, tpw, idx, a.stream)
-                                  : go_am<false, 1, 4>(sg, a.x, a.k, grid, tpw, idx, a.stream);
-    return c.r == 2 ? go_am<false, 2, 2>(sg, a.x, a.k, grid, tpw, idx, a.stream)
-                    : go_am<false, 2, 4>(sg, a.x, a.k, grid, tpw, idx, a.stream);
+    return a.x_bf16 ? go_am_cfg<true>(sg, a.x, a.k, grid, c.wg, bpl, c.r, tpw, idx, a.stream)
+                    : go_am_cfg<false>(sg, a.x, a.k, grid, c.wg, bpl, c.r, tpw, idx, a.stream);
 }
 
 hipError_t launch_gemv_m1(const GemvArgs& a, int cus) {
