@@ -25,7 +25,7 @@ then the median of 15 timed launches; per-call time = pass time / calls.
 
 extra also carries the other workloads: the Qwen3-1.7B decode step (28 layers,
 tensor j from seed 2000 + j) with its per-shape figures, the single 6144 x 2048
-GEMV of config 1 (weight seed 0, x seed 1; cold over copies, and warm on one
+GEMV that the reference runs on its CPU path (weight seed 0, x seed 1; cold over copies, and warm on one
 weight, labelled), speculative verify (8B shapes at M = 1..32), prefill at
 M = 512 (block-scaled MFMA; exact bf16-MFMA AUTO path), the per-call drop-in
 (PCIe-inclusive), and the CPU legs below.
@@ -33,8 +33,8 @@ M = 512 (block-scaled MFMA; exact bf16-MFMA AUTO path), the per-call drop-in
 cpu_baseline: the CPU oracle (a restatement of engine/src/lib.rs:240-266) on
 the box's host, one thread, over a bounded sample with the step's shape mix:
 all 7 projections of the first 9 layers plus the matching 9/36 of lm_head's
-rows. extra.cpu holds the same sample on every host thread, configs 4 and 5
-(row subsets, extrapolated to the full shapes, as stated in each entry), and
+rows. extra.cpu holds the same sample on every host thread, the verify and
+prefill shapes (row subsets, extrapolated to the full shapes, as stated in each entry), and
 the host CPU model and core counts.
 
 Profile modes (for rocprofv3; see profiles/): --profile-step, --profile-traffic,
@@ -77,6 +77,7 @@ LM_HEAD_1P7B = ("lm_head", 151936, 2048)
 LAYERS_1P7B = 28
 ROTATION_BYTES = 512 << 20   # distinct weight bytes per timed shape (2 x the Infinity Cache)
 REPS, WARM = 15, 2           # timed launches (median) and untimed ones before them
+VERIFY_REPS = 4              # enqueues of each verify block under --profile-verify
 ARENA_ALIGN = 2 << 20
 TRAFFIC_PROFILE = ROOT / "profiles" / "gemv_qwen3_8b_m1_step_traffic.md"
 
@@ -260,7 +261,7 @@ def time_lm_head_argmax(ctx, xs) -> dict:
 
 
 def time_skinny(ctx, ms=(1, 2, 4, 8, 16, 32)) -> dict:
-    """Speculative-verify shapes (config 4): each 8B projection at M token rows
+    """Speculative-verify shapes: each 8B projection at M token rows
     through AUTO (GEMV at M = 1, few-token GEMV or skinny bf16-MFMA kernel
     above), over >= 512 MiB of cold copies per shape; per-call latency and
     effective GB/s (bytes with M*K*2 + M*N*4)."""
@@ -282,7 +283,7 @@ def time_skinny(ctx, ms=(1, 2, 4, 8, 16, 32)) -> dict:
 
 
 def time_prefill(ctx, m: int = 512) -> dict:
-    """Prefill (config 5) on block-scaled MFMA: each 8B q/o/gate/up/down shape
+    """Prefill at M = 512 on block-scaled MFMA: each 8B q/o/gate/up/down shape
     at M = 512, activations bf16 N(0, 1) requantized per 32 along K (MXFP4 and
     MX-FP8), over >= 512 MiB of cold weight copies. The GEMM kernel alone
     (activations requantized beforehand, as when q|k|v or gate|up share them)
@@ -525,7 +526,7 @@ def _rows_for(work_macs: float, per_row_macs: int, n: int) -> int:
 
 
 def cpu_verify(ctx, weights, threads: int) -> dict:
-    """Config 4 on the host: each 8B shape at M = 2, 4, 8, 16 (bf16 N(0, 1) rows,
+    """Speculative verify on the host: each 8B shape at M = 2, 4, 8, 16 (bf16 N(0, 1) rows,
     seed 2), the oracle over the first R weight rows (about 5e6 multiply-adds
     per thread), extrapolated to all N rows: us per call = t * N / R."""
     oracle = _oracle()
@@ -549,7 +550,7 @@ def cpu_verify(ctx, weights, threads: int) -> dict:
 
 
 def cpu_prefill(ctx, weights, threads: int) -> dict:
-    """Config 5 on the host: each 8B q/o/gate/up/down shape at M = 512, the
+    """Prefill at M = 512 on the host: each 8B q/o/gate/up/down shape at M = 512, the
     oracle (no requantization: engine/src/lib.rs:240-266 on the bf16 rows) over
     8 of the 512 token rows and the first R weight rows (about 5e6
     multiply-adds per thread), extrapolated: seconds per call = t * (512 / 8)
@@ -633,7 +634,8 @@ def summarize(kind: str, dirs: list[str]) -> None:
     files): `trace DIR` (kernel stats of --profile-step), `traffic FETCH_DIR
     WRITE_DIR` (FETCH_SIZE / WRITE_SIZE of --profile-traffic, calibrated by the
     1 GiB copy), `step-pmc DIR` (per-launch averages of any counters of
-    --profile-traffic), `prefill-trace DIR` and `prefill-pmc DIR` (--profile-prefill)."""
+    --profile-traffic), `verify-trace DIR` (--profile-verify), `prefill-trace DIR`
+    and `prefill-pmc DIR` (--profile-prefill)."""
     d0 = Path(dirs[0])
     st = _stamp_of(d0)
     print(f"commit: {_git_head()}")
@@ -693,6 +695,33 @@ def summarize(kind: str, dirs: list[str]) -> None:
         print(f"\nper step: HBM fetch {tf:.6g} B, write {tw:.6g} B, total {tf + tw:.6g} B; algorithmic {alg} B; "
               f"ratio {(tf + tw) / alg if alg else 0:.4f}\n")
         print(f"hbm_bytes_per_step: {int(round(tf + tw))}")
+    elif kind == "verify-trace":
+        rows = _read_csv(d0, "kernel_trace.csv")
+        rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+        blocks = []
+        for r in rows:
+            nm = _short(r["Kernel_Name"])
+            if nm == "mx4::synth_bf16_kernel":
+                blocks.append([])
+            elif blocks and (nm.startswith("mx4::gemv") or nm.startswith("mx4::skinny")):
+                blocks[-1].append(r)
+        plan = st["plan"]
+        if len(blocks) != len(plan):
+            raise SystemExit(f"{len(blocks)} blocks in the trace, {len(plan)} in the stamp")
+        print("\n| projection | M | kernels per call: instance, workgroups x threads | us per call | GB/s |")
+        print("|---|---|---|---|---|")
+        for (name, m, n, k, copies, reps), blk in zip(plan, blocks):
+            calls = copies * reps
+            if len(blk) % calls:
+                raise SystemExit(f"{name} M={m}: {len(blk)} kernels for {calls} calls")
+            per = len(blk) // calls
+            kinds = []
+            for r in blk[:per]:
+                g = int(r.get("Grid_Size_X") or r.get("Grid_Size"))
+                wg = int(r.get("Workgroup_Size_X") or r.get("Workgroup_Size"))
+                kinds.append(f"{_short(r['Kernel_Name'])[5:]}, {g // wg} x {wg}")
+            us = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in blk) / calls / 1e3
+            print(f"| {name} | {m} | {' + '.join(kinds)} | {us:.2f} | {gemv_bytes(m, n, k) / (us * 1e-6) / 1e9:.0f} |")
     elif kind == "prefill-trace":
         rows = _read_csv(d0, "kernel_trace.csv")
         per = defaultdict(list)
@@ -743,7 +772,7 @@ def main() -> int:
     ap.add_argument("--no-shapes", action="store_true")
     ap.add_argument("--no-skinny", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--no-1p7b", action="store_true", help="skip the Qwen3-1.7B step and the single config-1 GEMV")
+    ap.add_argument("--no-1p7b", action="store_true", help="skip the Qwen3-1.7B step and the single 6144 x 2048 GEMV")
     ap.add_argument("--profile-step", action="store_true",
                     help="for kernel traces: only the recorded decode step (warmup + steps replays)")
     ap.add_argument("--profile-traffic", action="store_true",
@@ -751,10 +780,13 @@ def main() -> int:
     ap.add_argument("--profile-prefill", action="store_true",
                     help="for profiler runs: only the M=512 prefill (q, o, gate, up, down; MXFP4 and MX-FP8 "
                          "activations): 5 GEMMs on requantized activations, then 5 requantize + GEMM calls")
+    ap.add_argument("--profile-verify", action="store_true",
+                    help="for kernel traces: only the speculative-verify shapes (each 8B projection and the lm_head "
+                         "at M = 1..32 through AUTO over cold copies, enqueued 4 times)")
     ap.add_argument("--stamp", help="profile modes: also write the stamp (library sha256, workload) to this file")
     ap.add_argument("--summarize", nargs="+", metavar=("KIND", "DIR"),
                     help="print the markdown summary of rocprofv3 CSV output: trace DIR | traffic FETCH_DIR "
-                         "WRITE_DIR | step-pmc DIR | prefill-trace DIR | prefill-pmc DIR")
+                         "WRITE_DIR | step-pmc DIR | verify-trace DIR | prefill-trace DIR | prefill-pmc DIR")
     args = ap.parse_args()
 
     if args.summarize:
@@ -772,6 +804,28 @@ def main() -> int:
         return 1
 
     ctx = mx4hip.Context(0)
+    if args.profile_verify:
+        # Each 8B projection and the lm_head at M = 1..32 token rows through
+        # AUTO over the cold copies time_skinny uses, enqueued eagerly
+        # VERIFY_REPS times (kernel durations do not depend on how the launch
+        # was enqueued). A synth_bf16 launch (the block's input) opens every
+        # (projection, M) block, so the summary can split the trace.
+        plan = []
+        for i, (name, n, k) in enumerate(LAYER + [LM_HEAD]):
+            arena, copies = rotation(ctx, [(n, k)], 40000 + 1000 * i)
+            for m in (1, 2, 4, 8, 16, 32):
+                xb = ctx.buffer(m * k * 2)
+                ctx.synth_bf16(2, 1.0, m * k, xb)
+                yb = ctx.buffer(m * n * 4)
+                for _ in range(VERIFY_REPS):
+                    for ws in copies:
+                        ctx.matmul_ptr(xb.ptr, mx4hip.BF16, m, ws[0], yb.ptr)
+                ctx.synchronize()
+                plan.append([name, m, n, k, len(copies), VERIFY_REPS])
+            arena.release()
+        write_stamp(args.stamp, {"profile_verify": True, "plan": plan})
+        ctx.close()
+        return 0
     log("synthesizing 253 resident MXFP4 weights (4.03 GB, one arena) on the GPU")
     weights, arena = build_step(ctx)
 
@@ -894,7 +948,7 @@ def main() -> int:
         extra["prefill_exact_auto"] = time_prefill_exact(ctx)
 
     if not args.no_1p7b:
-        log("qwen3-1.7b decode step and the config-1 GEMV")
+        log("qwen3-1.7b decode step and the single 6144 x 2048 GEMV")
         extra["qwen3_1p7b"] = time_model_1p7b(ctx, max(5, args.steps // 2))
         extra["single_gemv_6144x2048"] = time_config1(ctx)
         log("per-call drop-in (host buffers)")
@@ -909,7 +963,7 @@ def main() -> int:
         if nt > 1:
             log(f"cpu baseline (oracle, {nt} threads)")
             cpu_extra["step_sample_all_threads"] = cpu_baseline(ctx, weights, x_host, threads=nt)
-        log("cpu legs: verify (config 4) and prefill (config 5)")
+        log("cpu legs: verify (M = 2..16) and prefill (M = 512)")
         cpu_extra["verify_1_thread"] = cpu_verify(ctx, weights, 1)
         cpu_extra["prefill_1_thread"] = cpu_prefill(ctx, weights, 1)
         if nt > 1:

@@ -60,7 +60,7 @@ typedef enum mx4_path {
     MX4_PATH_GEMM = 5      /* exact tiled GEMM on bf16 MFMA, any M, K % 128 == 0 */
 } mx4_path;
 
-/* Activation format on the block-scaled MFMA path (north-star prefill). */
+/* Activation format on the block-scaled MFMA path (M = 512 prefill). */
 typedef enum mx4_act_format {
     MX4_ACT_MXFP4 = 1,  /* requantized per 32 along K by the MXFP4 rule */
     MX4_ACT_MXFP8 = 2   /* requantized per 32 along K to MX E4M3 */

@@ -33,7 +33,7 @@ def test_every_kernel_launch_stub_is_defined(mx4):
     """Every kernel the host code launches has its launch stub in the library.
     (A device-only builtin that the host pass rejects makes clang drop the
     stubs of the kernels that use it without an error; the library then fails
-    to load on the GPU box.)"""
+    to load on a machine with the GPU.)"""
     import shutil
     import subprocess
 
