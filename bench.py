@@ -436,12 +436,19 @@ def time_model_1p7b(ctx, steps: int) -> dict:
     p = ctx.record(lambda: enqueue_grouped_step(ctx, weights, xs, yq, LAYER_1P7B, LAYERS_1P7B))
     ms = time_step(ctx, p, steps)
     p.release()
+    ys = {n: ctx.buffer(n * 4) for n in sorted({n for (_, n, _, _) in weights})}
+    ops = ctx.make_ops([(xs[k].ptr, mx4hip.BF16, 1, w, ys[n].ptr) for (_, n, k, w) in weights])
+    p = ctx.record(lambda: ctx.matmul_batch(ops))
+    ms_sep = time_step(ctx, p, steps)
+    p.release()
     arena.release()
     gbps = step_bytes / (ms * 1e-3) / 1e9
     return {"workload": "qwen3-1.7b decode step, M=1: 28 layers x 7 projections + lm_head (197 GEMVs, "
                         f"{LAYERS_1P7B * 4 + 1} launches)",
             "bytes_per_step": step_bytes, "ms_per_step": round(ms, 4), "GBps": round(gbps, 1),
             "frac": round(gbps / HBM_PEAK_GBS, 4),
+            "one_launch_per_projection": {"launches": len(weights), "ms_per_step": round(ms_sep, 4),
+                                          "GBps": round(step_bytes / (ms_sep * 1e-3) / 1e9, 1)},
             "shapes": time_shapes(ctx, xs, LAYER_1P7B, LM_HEAD_1P7B, seed0=70000)}
 
 
@@ -930,6 +937,14 @@ def main() -> int:
     if pss is not None:
         extra["gpu_ms_per_step_median"] = round(time_step(ctx, pss, max(5, args.steps // 2)), 4)
         extra["gpu_ms_per_step_median_protocol"] = f"median of {REPS} runs of {max(5, args.steps // 2)} replays"
+    if not args.separate:
+        # the same step with one launch per projection (253), as the reference
+        # dispatches it: what grouping q|k|v and gate|up saves
+        p_sep = ctx.record(lambda: ctx.matmul_batch(ops))
+        ms_sep = time_step(ctx, p_sep, max(5, args.steps // 2))
+        p_sep.release()
+        extra["one_launch_per_projection"] = {"launches": len(weights), "gpu_ms_per_step": round(ms_sep, 4),
+                                              "GBps": round(step_bytes / (ms_sep * 1e-3) / 1e9, 1)}
     if not args.no_shapes:
         log("per-shape timing (>= 512 MiB of cold copies per shape)")
         extra["shapes"] = time_shapes(ctx, xs)
