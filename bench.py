@@ -734,7 +734,7 @@ def summarize(kind: str, dirs: list[str]) -> None:
         per = defaultdict(list)
         for r in rows:
             nm = _short(r["Kernel_Name"])
-            if nm.startswith("mx4::prefill") or nm.startswith("mx4::quantize_fragments"):
+            if nm.startswith(("mx4::prefill", "mx4::quantize_fragments", "mx4::gemm_exact")):
                 grid = r.get("Grid_Size") or r.get("Grid_Size_X")
                 per[(nm, grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
         print("\n| kernel | grid | dispatches | median us | min us |")
@@ -742,7 +742,7 @@ def summarize(kind: str, dirs: list[str]) -> None:
         for (nm, g), ts in sorted(per.items()):
             print(f"| {nm} | {g} | {len(ts)} | {np.median(ts):.2f} | {min(ts):.2f} |")
     elif kind in ("prefill-pmc", "step-pmc"):
-        prefix = "mx4::prefill" if kind == "prefill-pmc" else "mx4::gemv"
+        prefix = ("mx4::prefill", "mx4::gemm_exact") if kind == "prefill-pmc" else ("mx4::gemv",)
         rows = _read_csv(d0, "counter_collection.csv")
         per = defaultdict(lambda: defaultdict(float))
         meta = {}
@@ -786,7 +786,8 @@ def main() -> int:
                     help="for counter runs: 2 eager grouped steps, then a 1 GiB device copy as the byte calibration")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="for profiler runs: only the M=512 prefill (q, o, gate, up, down; MXFP4 and MX-FP8 "
-                         "activations): 5 GEMMs on requantized activations, then 5 requantize + GEMM calls")
+                         "activations): 5 GEMMs on requantized activations, then 5 requantize + GEMM calls; "
+                         "and 5 exact GEMMs (AUTO, bf16 x) for q, gate and down")
     ap.add_argument("--profile-verify", action="store_true",
                     help="for kernel traces: only the speculative-verify shapes (each 8B projection and the lm_head "
                          "at M = 1..32 through AUTO over cold copies, enqueued 4 times)")
@@ -880,9 +881,14 @@ def main() -> int:
                     ctx.prefill_matmul(xq, xsc, code, m, w, yb)
                 for _ in range(5):
                     ctx.matmul_prefill(xb, mx4hip.BF16, m, w, code, yb)
+            # the exact matrix-core GEMM that AUTO runs above 32 token rows (bf16 x)
+            if name in ("q", "gate", "down"):
+                for _ in range(5):
+                    ctx.matmul_ptr(xb.ptr, mx4hip.BF16, m, w, yb.ptr)
             ctx.synchronize()
         write_stamp(args.stamp, {"profile_prefill": True, "m": m, "gemm_launches_per_shape_and_format": 10,
-                                 "requant_launches_per_shape_and_format": 6})
+                                 "requant_launches_per_shape_and_format": 6,
+                                 "exact_gemm_launches_per_shape": 5})
         ctx.close()
         return 0
 
