@@ -642,7 +642,8 @@ def summarize(kind: str, dirs: list[str]) -> None:
     WRITE_DIR` (FETCH_SIZE / WRITE_SIZE of --profile-traffic, calibrated by the
     1 GiB copy), `step-pmc DIR` (per-launch averages of any counters of
     --profile-traffic), `verify-trace DIR` (--profile-verify), `prefill-trace DIR`
-    and `prefill-pmc DIR` (--profile-prefill)."""
+    and `prefill-pmc DIR` (--profile-prefill), `prefill-compare DIR`
+    (--profile-prefill-compare)."""
     d0 = Path(dirs[0])
     st = _stamp_of(d0)
     print(f"commit: {_git_head()}")
@@ -729,6 +730,23 @@ def summarize(kind: str, dirs: list[str]) -> None:
                 kinds.append(f"{_short(r['Kernel_Name'])[5:]}, {g // wg} x {wg}")
             us = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in blk) / calls / 1e3
             print(f"| {name} | {m} | {' + '.join(kinds)} | {us:.2f} | {gemv_bytes(m, n, k) / (us * 1e-6) / 1e9:.0f} |")
+    elif kind == "prefill-compare":
+        rows = _read_csv(d0, "counter_collection.csv")
+        per = defaultdict(lambda: defaultdict(float))
+        for r in rows:
+            if _short(r["Kernel_Name"]).startswith("mx4::prefill"):
+                per[int(r["Dispatch_Id"])][r["Counter_Name"]] += float(r["Counter_Value"])
+        ids = sorted(per)
+        plan, calls = st["plan"], st["calls_per_instance"]
+        if len(ids) != len(plan) * calls:
+            raise SystemExit(f"{len(ids)} prefill dispatches, {len(plan) * calls} expected")
+        names = sorted({cn for c in per.values() for cn in c})
+        print("\n| shape | kernel | " + " | ".join(names) + " |")
+        print("|---|---|" + "---|" * len(names))
+        for i, (shape, desc, _) in enumerate(plan):
+            grp = [per[d] for d in ids[i * calls:(i + 1) * calls]]
+            avg = [sum(c.get(cn, 0.0) for c in grp) / calls for cn in names]
+            print(f"| {shape} | {desc} | " + " | ".join(f"{v:.4g}" for v in avg) + " |")
     elif kind == "prefill-trace":
         rows = _read_csv(d0, "kernel_trace.csv")
         per = defaultdict(list)
@@ -788,13 +806,17 @@ def main() -> int:
                     help="for profiler runs: only the M=512 prefill (q, o, gate, up, down; MXFP4 and MX-FP8 "
                          "activations): 5 GEMMs on requantized activations, then 5 requantize + GEMM calls; "
                          "and 5 exact GEMMs (AUTO, bf16 x) for q, gate and down")
+    ap.add_argument("--profile-prefill-compare", action="store_true",
+                    help="for counter runs: gate and q at M=512 (MXFP4), 5 calls each of the register-direct and "
+                         "the workgroup-shared prefill kernel")
     ap.add_argument("--profile-verify", action="store_true",
                     help="for kernel traces: only the speculative-verify shapes (each 8B projection and the lm_head "
                          "at M = 1..32 through AUTO over cold copies, enqueued 4 times)")
     ap.add_argument("--stamp", help="profile modes: also write the stamp (library sha256, workload) to this file")
     ap.add_argument("--summarize", nargs="+", metavar=("KIND", "DIR"),
                     help="print the markdown summary of rocprofv3 CSV output: trace DIR | traffic FETCH_DIR "
-                         "WRITE_DIR | step-pmc DIR | verify-trace DIR | prefill-trace DIR | prefill-pmc DIR")
+                         "WRITE_DIR | step-pmc DIR | verify-trace DIR | prefill-trace DIR | prefill-pmc DIR | "
+                         "prefill-compare DIR")
     args = ap.parse_args()
 
     if args.summarize:
@@ -889,6 +911,34 @@ def main() -> int:
         write_stamp(args.stamp, {"profile_prefill": True, "m": m, "gemm_launches_per_shape_and_format": 10,
                                  "requant_launches_per_shape_and_format": 6,
                                  "exact_gemm_launches_per_shape": 5})
+        ctx.close()
+        return 0
+
+    if args.profile_prefill_compare:
+        # counters of the two prefill kernels on the same shapes (MXFP4, M = 512,
+        # warm weights): 5 eager calls of each instance, in this order
+        m = 512
+        by = {}
+        for (nm, n, k, w) in weights:
+            by.setdefault(nm, (n, k, w))
+        ctx.reserve_prefill(m, 12288)
+        plan = [("gate", "register-direct 4x3 tiles, K halves (default)", (0, 0, 0)),
+                ("gate", "workgroup-shared 128x192, U=4, D=2", (128, 192, 16 * 4 + 2)),
+                ("q", "register-direct 2x2 tiles, K halves", (64, 128, 2)),
+                ("q", "workgroup-shared 128x64, U=2, D=4 (default)", (128, 64, 16 * 2 + 4))]
+        for name, _, inst in plan:
+            n, k, w = by[name]
+            w.prepare_prefill()
+            xb = ctx.buffer(m * k * 2)
+            ctx.synth_bf16(3, 1.0, m * k, xb)
+            yb = ctx.buffer(m * n * 4)
+            xq, xsc = ctx.prefill_act_buffers(m, k, mx4hip.ACT_MXFP4)
+            ctx.prefill_quantize(xb, mx4hip.BF16, m, k, mx4hip.ACT_MXFP4, xq, xsc)
+            for _ in range(5):
+                mx4hip.check(ctx.prefill_config(xq, xsc, mx4hip.ACT_MXFP4, m, w, yb, *inst))
+            ctx.synchronize()
+        write_stamp(args.stamp, {"profile_prefill_compare": True, "m": m, "calls_per_instance": 5,
+                                 "plan": [[nm, desc, list(inst)] for nm, desc, inst in plan]})
         ctx.close()
         return 0
 
