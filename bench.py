@@ -408,6 +408,33 @@ def time_dropin(ctx, weights, x_host: dict, reps: int = 5) -> dict:
                       f"median of {reps}"}
 
 
+def time_bf16_weights(ctx, ms=(1, 4)) -> dict:
+    """bf16 (non-quantized) weights, the scales == NULL arm of the drop-in
+    (engine/src/lib.rs:255, metal.rs:45-50): 8B q, gate and down at M = 1 and
+    4 (bf16 x), over >= 512 MiB of distinct device copies per shape (the same
+    N(0, 0.02) bf16 values uploaded to each). Bytes: N*K*2 + M*K*2 + M*N*4."""
+    out = {}
+    rng = np.random.default_rng(5)
+    for name, n, k in (LAYER[0], LAYER[4], LAYER[6]):
+        vals = (rng.standard_normal(n * k, dtype=np.float32) * 0.02).view(np.uint32)
+        bits = ((vals + 0x7FFF + ((vals >> 16) & 1)) >> 16).astype(np.uint16).reshape(n, k)
+        copies = [ctx.upload_weight_bf16(bits, n, k) for _ in range(max(2, -(-ROTATION_BYTES // (n * k * 2))))]
+        row = {"n": n, "k": k, "copies": len(copies)}
+        for m in ms:
+            xb = ctx.buffer(m * k * 2)
+            ctx.synth_bf16(2, 1.0, m * k, xb)
+            yb = ctx.buffer(m * n * 4)
+            t = time_pass(ctx, lambda: [ctx.matmul_ptr(xb.ptr, mx4hip.BF16, m, w, yb.ptr) for w in copies],
+                          len(copies))
+            b = n * k * 2 + m * k * 2 + m * n * 4
+            row[f"M{m}"] = {"us": t["us"], "GBps": round(b / (t["us"] * 1e-6) / 1e9, 1),
+                            "frac": round(b / (t["us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        for w in copies:
+            w.release()
+        out[name] = row
+    return out
+
+
 def time_step(ctx, p, steps: int, reps: int = REPS, warm: int = WARM) -> float:
     """Median GPU milliseconds per step over `reps` runs of `steps` replays."""
     for _ in range(warm):
@@ -1024,6 +1051,8 @@ def main() -> int:
         extra["single_gemv_6144x2048"] = time_config1(ctx)
         log("per-call drop-in (host buffers)")
         extra["dropin_per_call"] = time_dropin(ctx, weights, x_host)
+        log("bf16 weights (the unquantized arm)")
+        extra["bf16_weights"] = time_bf16_weights(ctx)
 
     cpu = None
     if not args.no_cpu_baseline:
