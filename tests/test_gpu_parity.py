@@ -1079,7 +1079,8 @@ def test_prefill_identity_is_exact(mx4, ctx, oracle, act):
 
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
 @pytest.mark.parametrize("m,n,k", [(1, 32, 256), (7, 200, 512), (64, 128, 1024), (130, 96, 256), (256, 256, 4096),
-                                   (70, 8256, 512), (33, 64, 12288)])
+                                   (70, 8256, 512), (33, 64, 12288), (1, 300, 4096), (33, 4100, 4096),
+                                   (5, 16400, 4096)])
 def test_prefill_matches_oracle_on_requantized_x(mx4, ctx, oracle, act, m, n, k):
     rng = np.random.default_rng(m * 7 + n)
     w = ctx.synth_weight(50 + m, n, k, 0.02)
