@@ -155,14 +155,17 @@ mx4_status mx4_weight_info(const mx4_weight *w, uint32_t *rows, uint32_t *cols,
  * reference (its GPU path reads the stored layout only). */
 mx4_status mx4_weight_footprint(const mx4_weight *w, uint64_t *stored_bytes, uint64_t *matrix_core_bytes);
 /* Free the matrix-core copy (after a prefill phase); a later prefill call
- * builds it again, which allocates. Refused when it is the only layout left. */
+ * builds it again, which allocates. Refused when it is the only layout left,
+ * and while any recorded pass of the context is alive (a pass keeps the raw
+ * pointers of the layouts it read). */
 mx4_status mx4_weight_release_prefill(mx4_weight *w);
 /* Keep one resident copy of a weight that serves prefill only: build the
  * matrix-core copy if needed, then free the stored layout. Afterwards only
  * the prefill entry points (mx4_matmul_prefill*, mx4_prefill_matmul*,
  * mx4_matmul_mx, mx4_matmul_prefill_noalloc) take the weight; the others fail
  * with MX4_ERR_UNSUPPORTED, and mx4_weight_info reports null packed/scales.
- * Only for weights whose memory the library owns (not mx4_weight_wrap). */
+ * Only for weights whose memory the library owns (not mx4_weight_wrap), and
+ * refused while any recorded pass of the context is alive. */
 mx4_status mx4_weight_drop_stored(mx4_weight *w);
 
 /* GpuModel::matmul (engine/src/gpu.rs:469-515): y_dev[m][rows] =

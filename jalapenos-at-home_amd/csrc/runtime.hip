@@ -669,6 +669,8 @@ mx4_status mx4_weight_release_prefill(mx4_weight* w) {
     if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
     if (!w->frag) return MX4_OK;
     if (!w->stored) return fail(MX4_ERR_UNSUPPORTED, "the matrix-core copy is the weight's only layout");
+    if (!w->ctx->passes.empty())
+        return fail(MX4_ERR_UNSUPPORTED, "a recorded pass of the context may read this layout; release the passes first");
     DeviceGuard g(w->ctx->device);
     HIP_TRY(hipStreamSynchronize(w->ctx->stream));
     HIP_TRY(hipFree(w->frag));
@@ -682,6 +684,8 @@ mx4_status mx4_weight_drop_stored(mx4_weight* w) {
     if (!w->stored) return MX4_OK;
     if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "a bf16 weight has no matrix-core copy");
     if (!w->allocation) return fail(MX4_ERR_UNSUPPORTED, "a wrapped weight's memory belongs to the caller");
+    if (!w->ctx->passes.empty())
+        return fail(MX4_ERR_UNSUPPORTED, "a recorded pass of the context may read this layout; release the passes first");
     DeviceGuard g(w->ctx->device);
     mx4_status st = prepare_fragments(w->ctx, w);
     if (st != MX4_OK) return st;

@@ -1524,8 +1524,9 @@ def test_weight_layouts_footprint_release_and_drop(mx4, ctx, oracle):
     copy are reported; the copy can be released after a prefill phase and is
     rebuilt on the next call (same results); a weight that serves prefill only
     can drop its stored layout (one copy left), after which prefill results are
-    unchanged and every other entry point refuses it; a wrapped weight's
-    memory is the caller's and cannot be dropped."""
+    unchanged and every other entry point refuses it; neither layout is freed
+    while a recorded pass of the context is alive; a wrapped weight's memory is
+    the caller's and cannot be dropped."""
     rng = np.random.default_rng(21)
     m, n, k = 64, 200, 2048
     packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
@@ -1537,6 +1538,17 @@ def test_weight_layouts_footprint_release_and_drop(mx4, ctx, oracle):
     y0 = _run_prefill(mx4, ctx, x, w, "mxfp4", mx4.BF16)
     stored, copy = w.footprint()
     assert copy >= n * k // 2 and copy < 1.2 * stored
+    # a live recorded pass may read either layout: both frees are refused until it is released
+    xb1 = ctx.to_device((f32_bits(x[:1]) >> 16).astype(np.uint16))
+    yb1 = ctx.buffer(n * 4)
+    p = ctx.record(lambda: ctx.matmul(xb1, mx4.BF16, 1, w, yb1))
+    with pytest.raises(mx4.Mx4Error, match="release the passes first"):
+        w.release_prefill()
+    with pytest.raises(mx4.Mx4Error, match="release the passes first"):
+        w.drop_stored()
+    p.launch()
+    p.release()
+    assert w.footprint() == (stored, copy)
     w.release_prefill()
     assert w.footprint() == (stored, 0)
     assert np.array_equal(_run_prefill(mx4, ctx, x, w, "mxfp4", mx4.BF16), y0)
