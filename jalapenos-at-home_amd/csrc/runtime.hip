@@ -108,6 +108,13 @@ struct mx4_context {
     uint64_t x_cap = 0;
     void* y_stage = nullptr;
     uint64_t y_cap = 0;
+    // pinned host bounce buffers of the drop-in (hipHostMalloc): the caller's
+    // pageable x and y are copied through them with host memcpy, and the
+    // device transfers run from and to page-locked memory
+    void* x_pin = nullptr;
+    uint64_t x_pin_cap = 0;
+    void* y_pin = nullptr;
+    uint64_t y_pin_cap = 0;
     // prefill workspace: requantized activations + their scales
     void* work = nullptr;
     uint64_t work_cap = 0;
@@ -214,6 +221,24 @@ mx4_status ensure_buffer(mx4_context* ctx, void** buf, uint64_t* cap, uint64_t n
     if (hipMalloc(buf, size) != hipSuccess) {
         *buf = nullptr;
         return fail(MX4_ERR_NO_MEMORY, "could not allocate %llu bytes of device memory",
+                    (unsigned long long)size);
+    }
+    *cap = size;
+    return MX4_OK;
+}
+
+// Grow a pinned host buffer of the drop-in (the previous transfer through it
+// has completed: every drop-in call synchronizes before returning).
+mx4_status ensure_pinned(mx4_context* ctx, void** buf, uint64_t* cap, uint64_t need) {
+    (void)ctx;
+    if (need <= *cap) return MX4_OK;
+    if (*buf) HIP_TRY(hipHostFree(*buf));
+    *buf = nullptr;
+    *cap = 0;
+    uint64_t size = need < (1u << 20) ? (1u << 20) : need;
+    if (hipHostMalloc(buf, size, hipHostMallocDefault) != hipSuccess) {
+        *buf = nullptr;
+        return fail(MX4_ERR_NO_MEMORY, "could not allocate %llu bytes of pinned host memory",
                     (unsigned long long)size);
     }
     *cap = size;
@@ -458,6 +483,8 @@ void mx4_destroy(mx4_context* ctx) {
     for (void* b : ctx->retired) (void)hipFree(b);
     if (ctx->x_stage) (void)hipFree(ctx->x_stage);
     if (ctx->y_stage) (void)hipFree(ctx->y_stage);
+    if (ctx->x_pin) (void)hipHostFree(ctx->x_pin);
+    if (ctx->y_pin) (void)hipHostFree(ctx->y_pin);
     if (ctx->work) (void)hipFree(ctx->work);
     if (ctx->flags) (void)hipFree(ctx->flags);
     if (ctx->am_partial) (void)hipFree(ctx->am_partial);
@@ -1314,18 +1341,22 @@ bool qwen_hip_matmul(void* context, const float* x, const void* w, const uint8_t
     const uint64_t xbytes = (uint64_t)rows * inner * 4, ybytes = (uint64_t)rows * cols * 4;
     if (ensure_buffer(ctx, &ctx->x_stage, &ctx->x_cap, xbytes) != MX4_OK) return false;
     if (ensure_buffer(ctx, &ctx->y_stage, &ctx->y_cap, ybytes) != MX4_OK) return false;
-    if (hipMemcpyAsync(ctx->x_stage, x, xbytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess) {
+    if (ensure_pinned(ctx, &ctx->x_pin, &ctx->x_pin_cap, xbytes) != MX4_OK) return false;
+    if (ensure_pinned(ctx, &ctx->y_pin, &ctx->y_pin_cap, ybytes) != MX4_OK) return false;
+    std::memcpy(ctx->x_pin, x, xbytes);
+    if (hipMemcpyAsync(ctx->x_stage, ctx->x_pin, xbytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess) {
         fail(MX4_ERR_DEVICE, "input upload failed");
         return false;
     }
     if (run_matmul(ctx, ctx->x_stage, MX4_F32, rows, weight, static_cast<float*>(ctx->y_stage), MX4_PATH_AUTO) !=
         MX4_OK)
         return false;
-    if (hipMemcpyAsync(y, ctx->y_stage, ybytes, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess ||
+    if (hipMemcpyAsync(ctx->y_pin, ctx->y_stage, ybytes, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess ||
         hipStreamSynchronize(ctx->stream) != hipSuccess) {
         fail(MX4_ERR_DEVICE, "matmul or copy-back failed");
         return false;
     }
+    std::memcpy(y, ctx->y_pin, ybytes);
     // evict only after the call completed, never the weight just used
     if (ctx->cache_bytes > ctx->cache_limit) {
         CacheKey keep = key;
