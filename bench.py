@@ -435,6 +435,44 @@ def time_bf16_weights(ctx, ms=(1, 4)) -> dict:
     return out
 
 
+def time_embed_quantize(ctx, weights) -> dict:
+    """The data formats either side of the projection. Embedding
+    (engine/src/lib.rs:213-234): 512 and 1 token ids into the 8B table (the tied
+    lm_head weight, 151936 x 4096), decoded to bf16 rows; bytes = the rows'
+    packed + scale bytes read and their bf16 written. Quantization
+    (python/quantize_mxfp4.py:18-39 on device, the checkpoint converter's rule):
+    a bf16 12288 x 4096 matrix to packed + scales, synchronous calls on the
+    host clock; bytes = input + output."""
+    out = {}
+    _, n, k, table = weights[-1]
+    rng = np.random.default_rng(9)
+    for count in (1, 512):
+        ids = ctx.to_device(rng.integers(0, n, count, dtype=np.uint32))
+        ob = ctx.buffer(count * k * 2)
+        # ten calls per pass: a pass of one small launch times the pass's own launch
+        t = time_pass(ctx, lambda: [ctx.embed(table, ids, count, ob) for _ in range(10)], 10)
+        b = count * (k // 2 + k // 32) + count * k * 2
+        out[f"embed_{count}_ids"] = {"us": t["us"], "GBps": round(b / (t["us"] * 1e-6) / 1e9, 1)}
+    rows, cols = 12288, 4096
+    xb = ctx.buffer(rows * cols * 2)
+    ctx.synth_bf16(7, 0.02, rows * cols, xb)
+    packed, scales = ctx.buffer(rows * cols // 2), ctx.buffer(rows * cols // 32)
+    # mx4_quantize is synchronous (it reads back the non-finite flag and fails
+    # on one), so it is timed per call on the host clock, the read-back included
+    ts = []
+    for i in range(WARM + REPS):
+        t0 = time.perf_counter()
+        ctx.quantize(xb, mx4hip.BF16, rows, cols, packed, scales)
+        if i >= WARM:
+            ts.append((time.perf_counter() - t0) * 1e6)
+    us = float(np.median(ts))
+    b = rows * cols * 2 + rows * cols // 2 + rows * cols // 32
+    out["quantize_bf16_12288x4096"] = {"us_per_synchronous_call": round(us, 2),
+                                       "GBps": round(b / (us * 1e-6) / 1e9, 1),
+                                       "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def time_step(ctx, p, steps: int, reps: int = REPS, warm: int = WARM) -> float:
     """Median GPU milliseconds per step over `reps` runs of `steps` replays."""
     for _ in range(warm):
@@ -1053,6 +1091,8 @@ def main() -> int:
         extra["dropin_per_call"] = time_dropin(ctx, weights, x_host)
         log("bf16 weights (the unquantized arm)")
         extra["bf16_weights"] = time_bf16_weights(ctx)
+        log("embedding and quantization")
+        extra["embed_quantize"] = time_embed_quantize(ctx, weights)
 
     cpu = None
     if not args.no_cpu_baseline:
