@@ -78,6 +78,7 @@ LAYERS_1P7B = 28
 ROTATION_BYTES = 512 << 20   # distinct weight bytes per timed shape (2 x the Infinity Cache)
 REPS, WARM = 15, 2           # timed launches (median) and untimed ones before them
 VERIFY_REPS = 4              # enqueues of each verify block under --profile-verify
+MIN_COPIES = 8               # launches per timed pass at least (weights rotated)
 ARENA_ALIGN = 2 << 20
 TRAFFIC_PROFILE = ROOT / "profiles" / "gemv_qwen3_8b_m1_step_traffic.md"
 
@@ -178,7 +179,9 @@ def rotation(ctx, members, seed0: int, min_bytes: int = ROTATION_BYTES) -> tuple
     weights. members: [(rows, cols)]. Returns the arena and the copies, each a
     list of weights (one per member)."""
     per = sum(weight_bytes(n, k) for n, k in members)
-    copies = max(2, -(-min_bytes // per))
+    # at least MIN_COPIES launches per pass: the pass's own start-up (tens of
+    # microseconds for a pass of one launch) is then a small share of each call
+    copies = max(MIN_COPIES, -(-min_bytes // per))
     specs = [(n, k, seed0 + c * len(members) + i) for c in range(copies) for i, (n, k) in enumerate(members)]
     arena = Arena(ctx, specs)
     ws = arena.weights
@@ -418,7 +421,7 @@ def time_bf16_weights(ctx, ms=(1, 4)) -> dict:
     for name, n, k in (LAYER[0], LAYER[4], LAYER[6]):
         vals = (rng.standard_normal(n * k, dtype=np.float32) * 0.02).view(np.uint32)
         bits = ((vals + 0x7FFF + ((vals >> 16) & 1)) >> 16).astype(np.uint16).reshape(n, k)
-        copies = [ctx.upload_weight_bf16(bits, n, k) for _ in range(max(2, -(-ROTATION_BYTES // (n * k * 2))))]
+        copies = [ctx.upload_weight_bf16(bits, n, k) for _ in range(max(MIN_COPIES, -(-ROTATION_BYTES // (n * k * 2))))]
         row = {"n": n, "k": k, "copies": len(copies)}
         for m in ms:
             xb = ctx.buffer(m * k * 2)
