@@ -1061,6 +1061,18 @@ def main() -> int:
     if pss is not None:
         extra["gpu_ms_per_step_median"] = round(time_step(ctx, pss, max(5, args.steps // 2)), 4)
         extra["gpu_ms_per_step_median_protocol"] = f"median of {REPS} runs of {max(5, args.steps // 2)} replays"
+    if pss is not None:
+        # the same grouped step enqueued from the host launch by launch
+        for _ in range(2):
+            enqueue()
+        ctx.synchronize()
+        te = []
+        for _ in range(REPS):
+            ctx.timer_begin()
+            for _ in range(max(5, args.steps // 2)):
+                enqueue()
+            te.append(ctx.timer_end() / max(5, args.steps // 2))
+        extra["gpu_ms_per_step_eager_median"] = round(float(np.median(te)), 4)
     if not args.separate:
         # the same step with one launch per projection (253), as the reference
         # dispatches it: what grouping q|k|v and gate|up saves
