@@ -520,7 +520,7 @@ def time_model_1p7b(ctx, steps: int) -> dict:
             "shapes": time_shapes(ctx, xs, LAYER_1P7B, LM_HEAD_1P7B, seed0=70000)}
 
 
-def time_config1(ctx) -> dict:
+def time_single_gemv(ctx) -> dict:
     """The single GEMV of the CPU reference case: W 6144 x 2048 (seed 0; the
     cold figure also uses copies of the same recipe), x bf16 [1, 2048] from
     seed 1, y f32 [1, 6144]. Cold: over >= 512 MiB of distinct copies. Warm:
@@ -1101,7 +1101,7 @@ def main() -> int:
     if not args.no_1p7b:
         log("qwen3-1.7b decode step and the single 6144 x 2048 GEMV")
         extra["qwen3_1p7b"] = time_model_1p7b(ctx, max(5, args.steps // 2))
-        extra["single_gemv_6144x2048"] = time_config1(ctx)
+        extra["single_gemv_6144x2048"] = time_single_gemv(ctx)
         log("per-call drop-in (host buffers)")
         extra["dropin_per_call"] = time_dropin(ctx, weights, x_host)
         log("bf16 weights (the unquantized arm)")

@@ -366,7 +366,7 @@ def test_gemv_model_shapes(mx4, ctx, oracle, model):
         w.release()
 
 
-def test_gemv_config1_against_fixture(mx4, ctx, oracle):
+def test_gemv_6144x2048_against_fixture(mx4, ctx, oracle):
     import hashlib
 
     fx = json.loads((GOLDEN / "synth_fixtures.json").read_text())["gemv_2048x6144"]
