@@ -17,7 +17,9 @@
  * is packed u8 [rows][cols/2], element 2j in the low nibble of byte j, and
  * scales u8 [rows][cols/32], E8M0 with bias 127. Activations x are row-major
  * [m][cols] f32 (what engine/src/metal.rs:11 passes) or bf16; outputs y are
- * row-major f32 [m][rows].
+ * row-major f32 [m][rows]. Device pointers given to the resident API are
+ * expected to be 16-byte aligned, as hipMalloc returns them: kernels access
+ * activations, outputs and packed codes 16 bytes at a time.
  *
  * Threading: a context is not thread-safe (the reference's Metal context is
  * neither Send nor Sync). Errors: every mx4_* call returns an mx4_status;
