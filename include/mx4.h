@@ -334,13 +334,16 @@ mx4_status mx4_prefill_matmul_group(mx4_context *ctx, const uint8_t *codes_dev, 
  * inside the workgroup (split_k, summed through LDS) of one compiled
  * instance: 128 x 192 x 1 (K % 512 == 0), 128 x 128 x 1, 64 x 128 x 2 and
  * 128 x 192 x 2 (K % 512 == 0), 128 x 64 x 4, 64 x 128 x 4, 128 x 96 x 4 and
- * 128 x 128 x 4 (K % 1024 == 0). split_k = 16 U + D (U = 2 or 4, D = 2..5)
+ * 128 x 128 x 4 (K % 1024 == 0). split_k = 128 (H - 1) + 16 U + D (H = 1
+ * or 2; (U, D) = (4, 2), (4, 3), (4, 5), (2, 3), (2, 4), (2, 5) or (2, 8))
  * selects instead the kernel whose workgroup loads each operand fragment
  * once into LDS for all its waves: stages of U k-steps (64 K each) in a ring
  * of D, workgroup tiles 128 x 192, 128 x 128, 64 x 128, 128 x 64, 64 x 256,
- * 128 x 96, 64 x 192 and 64 x 64 (K % 256 == 0; a ring that does not fit the
- * LDS is cut to the deepest that fits, and a stage the waves cannot share
- * evenly is not compiled).
+ * 128 x 96, 64 x 192 and 64 x 64 (K % 256 == 0); with H = 2 the workgroup
+ * has two sets of four waves, each over one half of K with its own ring,
+ * whose tiles are summed in LDS at the end (K % 512 == 0). A ring that does
+ * not fit the LDS is cut to the deepest that fits (except (4, 2)), and a
+ * stage the waves cannot share evenly is not compiled.
  * MX4_ERR_UNSUPPORTED when no compiled instance matches. tile_m == 0 keeps
  * the default choice. */
 mx4_status mx4_prefill_config(mx4_context *ctx, const uint8_t *codes_dev, const uint8_t *scales_dev,

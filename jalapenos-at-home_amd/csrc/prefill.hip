@@ -324,17 +324,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
-// Workgroup-shared operands: a workgroup of WM x WN waves owns a BM x BN
-// output tile over the whole of K. Each stage (U k-steps) of both operands'
-// fragments -- and the scale words of its quad -- is loaded once per
-// workgroup, straight into LDS by direct-to-LDS buffer loads (one 1 KiB
-// fragment per instruction), into a ring of D stages with D - 1 in flight; a
-// wave reads its TM A and TN B fragments of a k-step from LDS (16 bytes per
-// lane at 16 l, the operand order) and issues its TM x TN MFMAs. One barrier
-// per stage; no K split, so no partial tiles to reduce.
-template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D>
+// Workgroup-shared operands: a workgroup of KH x WM x WN waves owns a BM x BN
+// output tile. Each stage (U k-steps) of both operands' fragments -- and the
+// scale words of its quad -- is loaded once per workgroup, straight into LDS
+// by direct-to-LDS buffer loads (one 1 KiB fragment per instruction), into a
+// ring of D stages with D - 1 in flight; a wave reads its TM A and TN B
+// fragments of a k-step from LDS (16 bytes per lane at 16 l, the operand
+// order) and issues its TM x TN MFMAs. One barrier per stage.
+// KH = 1: the WM x WN waves cover the whole of K. KH = 2: two sets of WM x WN
+// waves take one half of K each, every set with its own ring, so each SIMD
+// runs two waves whose loads and MFMAs interleave; at the end the second
+// half's tile crosses LDS and the first half adds it (a fixed order, so
+// repeated calls agree bit for bit).
+template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D, int KH = 1>
 struct LdsGeo {
-    static constexpr int NW = WM * WN, NT = 64 * NW;
+    static constexpr int NW = WM * WN, NT = 64 * NW * KH;  // waves per K part; threads
     static constexpr int GA = WM * TM, GB = WN * TN;  // row groups of 32 per tile
     static constexpr int BM = 32 * GA, BN = 32 * GB;
     static constexpr int AFK = A_FP8 ? 2 : 1;         // 1 KiB pieces per A fragment
@@ -342,41 +346,44 @@ struct LdsGeo {
     static constexpr int SA = (GA + 3) / 4, SB = (GB + 3) / 4;  // scale loads (4 groups each)
     static constexpr int S_BYTES = NW * 1024;                     // one 1 KiB slot per wave
     static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+    static constexpr int RING = D * STAGE;
     static constexpr int FRAGS = U * (GA * AFK + GB), FI = FRAGS / NW;
     static constexpr int LPS = FI + 1;  // vector memory instructions per wave and stage
+    static constexpr int RED = KH > 1 ? NW * TM * TN * 16 * 64 * 4 : 0;  // bytes of the K-half hand-over
+    static constexpr int LDS = KH * RING > RED ? KH * RING : RED;
     // stages of 2 or 4 k-steps (a scale quad in one or two stages); every wave
     // loads the same number of fragments and one scale piece per stage; the
-    // waits fit vmcnt; the ring fits the LDS
-    static constexpr bool ok = (U == 2 || U == 4) && FRAGS % NW == 0 && SA + SB <= NW && D >= 2 && D <= 5 &&
-                               (D - 2) * LPS <= 63 && D * STAGE <= 160 * 1024;
+    // waits fit vmcnt; the rings fit the LDS; two K parts need two waves per
+    // SIMD to fit in the register file
+    static constexpr bool ok = (U == 2 || U == 4) && FRAGS % NW == 0 && SA + SB <= NW && D >= 2 && D <= 8 &&
+                               (D - 2) * LPS <= 63 && LDS <= 160 * 1024 && (KH == 1 || (KH == 2 && NW == 4));
 };
 
 template <int LPS, int MAXA>
 __device__ __forceinline__ void wait_ahead(uint32_t ahead) {
-    // outstanding loads allowed: those of the `ahead` stages issued after the one needed
-    if constexpr (MAXA >= 3) {
-        if (ahead >= 3) { wait_vm<3 * LPS>(); return; }
-    }
-    if constexpr (MAXA >= 2) {
-        if (ahead == 2) { wait_vm<2 * LPS>(); return; }
-    }
+    // outstanding loads allowed: those of the `ahead` stages issued after the
+    // one needed (ahead <= MAXA)
     if constexpr (MAXA >= 1) {
-        if (ahead == 1) { wait_vm<LPS>(); return; }
+        if (ahead >= (uint32_t)MAXA) { wait_vm<MAXA * LPS>(); return; }
+        wait_ahead<LPS, MAXA - 1>(ahead);
+    } else {
+        wait_vm<0>();
     }
-    wait_vm<0>();
 }
 
-template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D>
-__global__ __launch_bounds__(64 * WM * WN) void prefill_lds_kernel(const Segs segs, const uint8_t* __restrict__ xf,
-                                                                  const uint8_t* __restrict__ xsf, uint32_t m,
-                                                                  uint32_t k) {
-    using G = LdsGeo<A_FP8, WM, WN, TM, TN, U, D>;
+template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D, int KH>
+__global__ __launch_bounds__(64 * WM * WN * KH) void prefill_lds_kernel(const Segs segs, const uint8_t* __restrict__ xf,
+                                                                       const uint8_t* __restrict__ xsf, uint32_t m,
+                                                                       uint32_t k) {
+    using G = LdsGeo<A_FP8, WM, WN, TM, TN, U, D, KH>;
     static_assert(G::ok, "instance outside the kernel's stage, vmcnt and LDS limits");
     constexpr uint32_t AF = A_FP8 ? 2048 : 1024;
     constexpr int P = 4 / U;  // stages per scale quad
-    __shared__ __attribute__((aligned(16))) uint8_t lds[D * G::STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_all[G::LDS];
     const uint32_t lane = threadIdx.x % 64;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t kh = wave_all / G::NW, wave = wave_all % G::NW;  // K part; wave within it
+    uint8_t* const lds = lds_all + kh * G::RING;
     const uint32_t wm = wave / WN, wn = wave % WN;
     const uint32_t bx = blockIdx.x;
     const uint8_t* __restrict__ wf = segs.wf[0];
@@ -393,7 +400,8 @@ __global__ __launch_bounds__(64 * WM * WN) void prefill_lds_kernel(const Segs se
         t0 = in ? segs.tile0[s] : t0;
     }
     const uint32_t ga0 = blockIdx.y * G::GA, gb0 = (bx - t0) * G::GB;  // first row groups of the tile
-    const uint32_t nk_all = k / 64, nq_all = k / 256, stages = nk_all / U;
+    const uint32_t nk_all = k / 64, nq_all = k / 256, stages = nk_all / U / KH;
+    const uint32_t kk0 = kh * (nk_all / KH);  // first k-step of this K part (a whole scale quad)
     const uint32_t ga_n = (m + 31) / 32, gb_n = (n + 31) / 32;
     const __amdgpu_buffer_rsrc_t xr = rsrc(xf, ga_n * nk_all * AF);
     const __amdgpu_buffer_rsrc_t xsr = rsrc(xsf, ga_n * nq_all * 256);
@@ -409,7 +417,7 @@ __global__ __launch_bounds__(64 * WM * WN) void prefill_lds_kernel(const Segs se
     const uint32_t s_grp = (s_is_a ? si : si - G::SA) * 4 + lane / 16;
     const uint32_t s_last = s_is_a ? G::GA - 1 : G::GB - 1;
     const uint32_t s_row = (s_is_a ? ga0 : gb0) + (s_grp < s_last ? s_grp : s_last);
-    const uint32_t s_goff = s_row * nq_all * 256 + (lane % 16) * 16;
+    const uint32_t s_goff = s_row * nq_all * 256 + (kk0 / 4) * 256 + (lane % 16) * 16;
     const __amdgpu_buffer_rsrc_t s_r = s_is_a ? xsr : wsr;
 
     auto issue = [&](uint32_t st, uint32_t slot) {
@@ -425,8 +433,8 @@ __global__ __launch_bounds__(64 * WM * WN) void prefill_lds_kernel(const Segs se
             const uint32_t fb = f - U * G::GA * G::AFK, kkb = fb / G::GB, jb = fb % G::GB;
             const uint32_t lds_off = is_a ? (kka * G::GA + ia) * AF + half * 1024
                                           : G::A_BYTES + (kkb * G::GB + jb) * 1024;
-            const uint32_t goff = is_a ? ((ga0 + ia) * nk_all + st * U + kka) * AF + half * 1024
-                                       : ((gb0 + jb) * nk_all + st * U + kkb) * 1024;
+            const uint32_t goff = is_a ? ((ga0 + ia) * nk_all + kk0 + st * U + kka) * AF + half * 1024
+                                       : ((gb0 + jb) * nk_all + kk0 + st * U + kkb) * 1024;
             load_lds16(is_a ? xr : wr, (lds_ptr)(base + lds_off), goff + 16 * lane);
         }
         load_lds16(s_r, (lds_ptr)(base + G::A_BYTES + G::B_BYTES + wave * 1024), s_goff + (st / P) * 256);
@@ -494,6 +502,38 @@ __global__ __launch_bounds__(64 * WM * WN) void prefill_lds_kernel(const Segs se
         }
     }
     mfma_drain();
+
+    if constexpr (KH > 1) {
+        // the second K half hands its tile to the first through LDS (the rings
+        // are done: every wave has passed its last stage's barrier and read
+        // its operands before this barrier), as 16-byte vectors at
+        // [wave][tile][q][lane]
+        f32x4* red = reinterpret_cast<f32x4*>(lds_all);
+        auto red_at = [&](int tile, int q) -> f32x4& { return red[((wave * TM * TN + tile) * 4 + q) * 64 + lane]; };
+        __syncthreads();
+        if (kh == 1) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        red_at(i * TN + j, q) =
+                            f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        }
+        __syncthreads();
+        if (kh == 1) return;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4 o = red_at(i * TN + j, q);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += o[e];
+                }
+    }
 
     // Branch-free device-scope stores through a resource over y, as in prefill_kernel.
     constexpr int kStoreDeviceScope = 0x10;
@@ -584,19 +624,20 @@ hipError_t go(const PrefillArgs& a) {
 }
 
 // The deepest ring of at most D stages that the kernel's limits allow (D when none is smaller than 3).
-template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D>
+template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D, int KH = 1>
 constexpr int fit_depth() {
-    if constexpr (D <= 2 || LdsGeo<A_FP8, WM, WN, TM, TN, U, D>::ok) return D;
-    else return fit_depth<A_FP8, WM, WN, TM, TN, U, D - 1>();
+    if constexpr (D <= 2 || LdsGeo<A_FP8, WM, WN, TM, TN, U, D, KH>::ok) return D;
+    else return fit_depth<A_FP8, WM, WN, TM, TN, U, D - 1, KH>();
 }
 
-template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D>
+template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D, int KH = 1>
 hipError_t go_lds(const PrefillArgs& a) {
-    using G = LdsGeo<A_FP8, WM, WN, TM, TN, U, D>;
+    using G = LdsGeo<A_FP8, WM, WN, TM, TN, U, D, KH>;
     if constexpr (!G::ok) {
         return hipErrorNotSupported;
     } else {
-        if (a.k % 256 != 0) return hipErrorNotSupported;
+        // each K part starts on a whole scale quad
+        if (a.k % (256 * KH) != 0) return hipErrorNotSupported;
         Segs sg{};
         uint32_t cols = 0;
         for (uint32_t s = 0; s < kMaxPrefillGroup; ++s) {
@@ -612,8 +653,8 @@ hipError_t go_lds(const PrefillArgs& a) {
             }
         }
         dim3 grid(cols, (a.m + G::BM - 1) / G::BM);
-        hipLaunchKernelGGL((prefill_lds_kernel<A_FP8, WM, WN, TM, TN, U, D>), grid, dim3(G::NT), 0, a.stream, sg,
-                           a.xf, a.xsf, a.m, a.k);
+        hipLaunchKernelGGL((prefill_lds_kernel<A_FP8, WM, WN, TM, TN, U, D, KH>), grid, dim3(G::NT), 0, a.stream,
+                           sg, a.xf, a.xsf, a.m, a.k);
         return hipGetLastError();
     }
 }
@@ -632,21 +673,39 @@ hipError_t go_parts(const PrefillArgs& a) {
 template <bool A_FP8>
 hipError_t dispatch(const PrefillArgs& a) {
     if (a.tile_m != 0 && a.split_k >= 16) {
-        // workgroup-shared operands (prefill_lds_kernel): split_k = 16 U + D
-        // (stages of U k-steps, a ring of D), tile_m x tile_n workgroup tiles;
-        // a ring too deep for the LDS is cut to the deepest that fits
-        const uint32_t u = a.split_k / 16, d = a.split_k % 16;
+        // workgroup-shared operands (prefill_lds_kernel): split_k = 128 (KH - 1)
+        // + 16 U + D (K in KH parts of their own waves, stages of U k-steps, a
+        // ring of D), tile_m x tile_n workgroup tiles; a ring too deep for the
+        // LDS is cut to the deepest that fits
+        const uint32_t kh = a.split_k >= 128 ? 2 : 1, code = a.split_k % 128;
+        const uint32_t u = code / 16, d = code % 16;
+#define MX4_LDS_KH(KH_)                                                                                  \
+            if (kh == KH_) {                                                                             \
+                if (u == 4 && d == 2) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 4, 2, KH_>(a);          \
+                if (u == 4 && d == 3)                                                                    \
+                    return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 4,                                      \
+                                  fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 4, 3, KH_>(), KH_>(a);         \
+                if (u == 2 && d == 3)                                                                    \
+                    return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 2,                                      \
+                                  fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 2, 3, KH_>(), KH_>(a);         \
+                if (u == 2 && d == 4)                                                                    \
+                    return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 2,                                      \
+                                  fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 2, 4, KH_>(), KH_>(a);         \
+                if (u == 2 && d == 5)                                                                    \
+                    return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 2,                                      \
+                                  fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 2, 5, KH_>(), KH_>(a);         \
+                if (u == 2 && d == 8)                                                                    \
+                    return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 2,                                      \
+                                  fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 2, 8, KH_>(), KH_>(a);         \
+                if (u == 4 && d == 5)                                                                    \
+                    return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 4,                                      \
+                                  fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 4, 5, KH_>(), KH_>(a);         \
+            }
 #define MX4_LDS(BM_, BN_, WM_, WN_, TM_, TN_)                                                           \
         if (a.tile_m == BM_ && a.tile_n == BN_) {                                                       \
             constexpr int WM_c = WM_, WN_c = WN_, TM_c = TM_, TN_c = TN_;                               \
-            if (u == 4 && d == 2) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 4, 2>(a);                  \
-            if (u == 4 && d == 3) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 4,                         \
-                                                fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 4, 3>()>(a);       \
-            if (u == 2 && d == 3) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 2, 3>(a);                  \
-            if (u == 2 && d == 4) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 2,                         \
-                                                fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 2, 4>()>(a);       \
-            if (u == 2 && d == 5) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 2,                         \
-                                                fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 2, 5>()>(a);       \
+            MX4_LDS_KH(1)                                                                               \
+            MX4_LDS_KH(2)                                                                               \
             return hipErrorNotSupported;                                                                \
         }
         MX4_LDS(128, 192, 2, 2, 2, 3)
@@ -658,6 +717,7 @@ hipError_t dispatch(const PrefillArgs& a) {
         MX4_LDS(64, 192, 2, 2, 1, 3)
         MX4_LDS(64, 64, 2, 2, 1, 1)
 #undef MX4_LDS
+#undef MX4_LDS_KH
         return hipErrorNotSupported;
     }
     if (a.tile_m != 0) {
@@ -687,15 +747,24 @@ hipError_t dispatch(const PrefillArgs& a) {
     uint32_t ntot = 0;
     for (uint32_t s = 0; s < a.count; ++s) ntot += a.n[s];
     // Workgroup-shared operands (prefill_lds_kernel) where they measured faster,
-    // cold weights at M = 512 (Qwen3-8B, K = 4096; split_k code 16 U + D of the
-    // tuning call):
-    //  q|k|v (6144 rows): 64 x 128 tiles; MXFP4 in stages of 2 k-steps, 4 deep
-    //  (19.4 -> 14.7 us), MX-FP8 in stages of 4, 2 deep (24.0 -> 18.2 us);
+    // cold weights at M = 512 (Qwen3-8B; split_k code 128 (KH - 1) + 16 U + D
+    // of the tuning call):
+    //  q|k|v (6144 rows, K = 4096): 64 x 128 tiles; MXFP4 in stages of 2
+    //  k-steps, 4 deep (19.4 -> 14.7 us), MX-FP8 in stages of 4, 2 deep
+    //  (24.0 -> 18.2 us);
     //  gate|up (24576 rows), MXFP4: 128 x 192 tiles in stages of 2, 3 deep, so
     //  two workgroups share a CU (46.1 -> 43.2 us);
-    //  q / o (4096 rows), MXFP4: 128 x 64 tiles in stages of 2, 4 deep
-    //  (12.3 -> 11.3 us).
-    // gate or down alone and the other MX-FP8 shapes measured no faster there.
+    //  q / o (4096 rows, K = 4096) and down (4096 rows, K = 12288): K in two
+    //  halves of their own four waves (two waves per SIMD), stages of 2, 4
+    //  deep; MXFP4 on 128 x 64 tiles (q 11.4 -> 10.7 us against the one-ring
+    //  tile, down 27.7 -> 25.7 us against 4 x 2 wave tiles in K quarters),
+    //  MX-FP8 on 64 x 128 tiles (q 14.7 -> 13.5 us, down 34.1 -> 33.3 us
+    //  against 2 x 4 wave tiles in K quarters).
+    // gate alone and the other MX-FP8 shapes measured no faster there.
+    if ((a.k == 4096 || a.k == 12288) && ntot <= 4096) {
+        if constexpr (A_FP8) return go_lds<true, 2, 2, 1, 2, 2, 4, 2>(a);
+        else return go_lds<false, 2, 2, 2, 1, 2, 4, 2>(a);
+    }
     if (a.k == 4096) {
         if (ntot > 4096 && ntot <= 8192) {
             if constexpr (A_FP8) return go_lds<true, 2, 2, 1, 2, 4, 2>(a);
@@ -703,7 +772,6 @@ hipError_t dispatch(const PrefillArgs& a) {
         }
         if constexpr (!A_FP8) {
             if (ntot >= 16384) return go_lds<false, 2, 2, 2, 3, 2, 3>(a);
-            if (ntot <= 4096) return go_lds<false, 2, 2, 2, 1, 2, 4>(a);
         }
     }
     // measured on MI355X at M = 512 (Qwen3-8B shapes): wide N takes 4 x 3 tiles
@@ -716,17 +784,6 @@ hipError_t dispatch(const PrefillArgs& a) {
     // workgroup tiles over the full K, 192 workgroups (MXFP4 17.3 -> 15.9 us,
     // MX-FP8 22.4 -> 20.6 us against 2 x 2 tiles in K halves)
     if (ntot > 4096 && a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 1, 2, 0>(a);
-    // K = 12288 (down) in K quarters: MX-FP8 on 2 x 4 wave tiles (29.5 -> 27.1 us
-    // warm), MXFP4 on 4 x 2 wave tiles (cold weights: 30.9 -> 26.4 us)
-    if (a.k == 12288 && ntot <= 4096) {
-        if constexpr (A_FP8) return go_parts<true, 2, 4, 4>(a);
-        else return go_parts<false, 4, 2, 4>(a);
-    }
-    // MX-FP8 at K = 4096 up to 4096 rows (q/o): 2 x 4 wave tiles in K quarters
-    // (cold weights: 16.0 -> 14.5 us)
-    if constexpr (A_FP8) {
-        if (a.k == 4096 && ntot <= 4096) return go_parts<true, 2, 4, 4>(a);
-    }
     if (a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 2, 2, 32>(a);
     if (a.k == 12288) return go<A_FP8, 2, 2, 2, 4, 2, 2, 96>(a);
     if (a.k % 512 == 0) return go<A_FP8, 2, 2, 2, 4, 2, 2, 0>(a);

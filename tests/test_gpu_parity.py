@@ -1232,27 +1232,35 @@ def test_prefill_instances_match_oracle(mx4, ctx, oracle, act, k, tile):
 
 
 # Workgroup-shared prefill instances: tile -> waves along M x N and MFMA tiles
-# per wave along M x N; split_k code 16 U + D (stages of U k-steps, ring of D).
+# per wave along M x N; split_k code 128 (H - 1) + 16 U + D (K in H halves of
+# their own waves, stages of U k-steps, ring of D).
 LDS_TILES = {(128, 192): (2, 2, 2, 3), (128, 128): (2, 2, 2, 2), (64, 128): (2, 2, 1, 2), (128, 64): (2, 2, 2, 1),
              (64, 256): (1, 4, 2, 2), (128, 96): (4, 1, 1, 3), (64, 192): (2, 2, 1, 3), (64, 64): (2, 2, 1, 1)}
-LDS_CODES = (16 * 4 + 2, 16 * 4 + 3, 16 * 2 + 3, 16 * 2 + 4, 16 * 2 + 5)
+LDS_CODES = (16 * 4 + 2, 16 * 4 + 3, 16 * 2 + 3, 16 * 2 + 4, 16 * 2 + 5, 16 * 2 + 8, 16 * 4 + 5,
+             128 + 16 * 4 + 2, 128 + 16 * 2 + 3, 128 + 16 * 2 + 4, 128 + 16 * 2 + 8)
 
 
-def lds_depth(fp8, tile, u, d):
-    """The ring depth the library compiles for (tile, U, D), or None: the
-    kernel's limits (whole fragments per wave and stage, one scale piece per
-    wave, waits within vmcnt, the ring within 160 KiB of LDS), a ring that does
-    not fit cut to the deepest that does (not below 2)."""
+def lds_depth(fp8, tile, code, k):
+    """The ring depth the library compiles for (tile, split_k code) at K, or
+    None: the kernel's limits (whole fragments per wave and stage, one scale
+    piece per wave, waits within vmcnt, the rings -- and with two K halves the
+    hand-over of the second half's tile -- within 160 KiB of LDS, each K half
+    on whole scale quads), a ring that does not fit cut to the deepest that
+    does (not below 2)."""
+    h, u, d = (2 if code >= 128 else 1), (code % 128) // 16, code % 16
+    if k % (256 * h) != 0:
+        return None
     wm, wn, tm, tn = LDS_TILES[tile]
     nw, ga, gb, afk = wm * wn, wm * tm, wn * tn, 2 if fp8 else 1
     frags = u * (ga * afk + gb)
     stage = u * ga * afk * 1024 + u * gb * 1024 + nw * 1024
+    red = nw * tm * tn * 16 * 64 * 4 if h == 2 else 0
 
     def ok(dd):
-        return (frags % nw == 0 and (ga + 3) // 4 + (gb + 3) // 4 <= nw and 2 <= dd <= 5
-                and (dd - 2) * (frags // nw + 1) <= 63 and dd * stage <= 160 * 1024)
-    # (U, D) = (4, 2) and (2, 3) are compiled as asked; the deeper codes are cut to fit
-    if (u, d) in ((4, 2), (2, 3)):
+        return (frags % nw == 0 and (ga + 3) // 4 + (gb + 3) // 4 <= nw and 2 <= dd <= 8
+                and (dd - 2) * (frags // nw + 1) <= 63 and max(h * dd * stage, red) <= 160 * 1024)
+    # (U, D) = (4, 2) is compiled as asked; the other codes are cut to fit
+    if (u, d) == (4, 2):
         return d if ok(d) else None
     while d > 2 and not ok(d):
         d -= 1
@@ -1260,20 +1268,24 @@ def lds_depth(fp8, tile, u, d):
 
 
 LDS_CASES = ([(4096, t, c) for t in LDS_TILES for c in LDS_CODES] +
-             [(k, t, c) for k in (256, 1280) for t in LDS_TILES for c in (16 * 4 + 2, 16 * 2 + 4)])
+             [(k, t, c) for k in (256, 1280) for t in LDS_TILES for c in (16 * 4 + 2, 16 * 2 + 4)] +
+             [(k, t, c) for k in (1536, 1280) for t in LDS_TILES for c in (128 + 16 * 4 + 2, 128 + 16 * 2 + 4)])
 
 
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
-@pytest.mark.parametrize("k,tile,code", LDS_CASES, ids=[f"k{k}-{t[0]}x{t[1]}-u{c // 16}d{c % 16}" for k, t, c in LDS_CASES])
+@pytest.mark.parametrize("k,tile,code", LDS_CASES,
+                         ids=[f"k{k}-{t[0]}x{t[1]}-h{1 + c // 128}u{c % 128 // 16}d{c % 16}" for k, t, c in LDS_CASES])
 def test_prefill_shared_instances_match_oracle(mx4, ctx, oracle, act, k, tile, code):
     """Every workgroup-shared prefill instance reachable through
     mx4_prefill_config is compiled exactly where the kernel's limits allow it;
     each one, on ragged m and n (partial row groups and partial workgroup
     tiles), and at K = 256 / 1280 (fewer stages than the ring, an odd number of
-    scale quads), matches the oracle on dequant(requant(x)), twice bitwise equal."""
+    scale quads; with two K halves K = 1536 / 1280: three quads per half, or
+    halves off the quad grid, which the library refuses), matches the oracle on
+    dequant(requant(x)), twice bitwise equal."""
     fp8 = act == "mxfp8"
-    u, d = code // 16, code % 16
-    depth = lds_depth(fp8, tile, u, d)
+    h, u = 1 + code // 128, code % 128 // 16
+    depth = lds_depth(fp8, tile, code, k)
     m, n = 70, 300
     acode = mx4.ACT_MXFP8 if fp8 else mx4.ACT_MXFP4
     w = ctx.synth_weight(800 + k // 256, n, k, 0.02)
@@ -1287,7 +1299,7 @@ def test_prefill_shared_instances_match_oracle(mx4, ctx, oracle, act, k, tile, c
         assert status == mx4.ERR_UNSUPPORTED
         return
     assert status == 0, mx4.last_error()
-    say(f"shared prefill {act} k={k} tile={tile} U={u} D={depth}")
+    say(f"shared prefill {act} k={k} tile={tile} H={h} U={u} D={depth}")
     packed, scales = ctx.download_weight(w)
     ref, _ = _prefill_ref(oracle, x, packed, scales, act)
     outs = []
@@ -1295,7 +1307,7 @@ def test_prefill_shared_instances_match_oracle(mx4, ctx, oracle, act, k, tile, c
         yb.upload(np.full(m * n, np.nan, np.float32))
         assert ctx.prefill_config(codes, sc, acode, m, w, yb, tile[0], tile[1], code) == 0, mx4.last_error()
         outs.append(yb.download(np.float32).reshape(m, n))
-    assert_close(outs[0], ref, f"shared prefill {tile} U={u} D={depth} k={k} {act}")
+    assert_close(outs[0], ref, f"shared prefill {tile} H={h} U={u} D={depth} k={k} {act}")
     assert np.array_equal(outs[0], outs[1])
 
 
@@ -1303,9 +1315,10 @@ def test_prefill_shared_instances_match_oracle(mx4, ctx, oracle, act, k, tile, c
 @pytest.mark.parametrize("tile", list(LDS_TILES), ids=[f"{t[0]}x{t[1]}" for t in LDS_TILES])
 def test_prefill_shared_identity_is_exact(mx4, ctx, oracle, act, tile):
     """One-hot activations through each workgroup-shared tile (stages of 4 and
-    of 2 k-steps): the decoded weights bit for bit, which pins the LDS
-    placement of every fragment and scale piece, the op_sel of each k-step
-    within its quad and the output layout."""
+    of 2 k-steps, one ring or two K halves): the decoded weights bit for bit,
+    which pins the LDS placement of every fragment and scale piece, the op_sel
+    of each k-step within its quad, each half's K range and the output
+    layout."""
     rng = np.random.default_rng(37)
     n, k, m = 200, 1024, 96
     packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
@@ -1320,8 +1333,8 @@ def test_prefill_shared_identity_is_exact(mx4, ctx, oracle, act, tile):
     dec = oracle.dequantize(packed, scales)
     yb = ctx.buffer(m * n * 4)
     ran = 0
-    for code in (16 * 4 + 2, 16 * 2 + 3):
-        if lds_depth(act == "mxfp8", tile, code // 16, code % 16) is None:
+    for code in (16 * 4 + 2, 16 * 2 + 3, 128 + 16 * 4 + 2, 128 + 16 * 2 + 3):
+        if lds_depth(act == "mxfp8", tile, code, k) is None:
             continue
         yb.upload(np.full(m * n, np.nan, np.float32))
         assert ctx.prefill_config(codes, sc, acode, m, w, yb, tile[0], tile[1], code) == 0, mx4.last_error()
