@@ -400,6 +400,16 @@ mx4_status mx4_synth_weight(mx4_context *ctx, uint64_t seed, double sigma, uint3
 mx4_status mx4_timer_begin(mx4_context *ctx);
 mx4_status mx4_timer_end(mx4_context *ctx, double *ms);
 
+/* Measurement aid, no counterpart in the reference: the rate the matrix
+ * cores sustain on the prefill GEMM's instruction and the shader clock they
+ * hold meanwhile. Scaled FP4 MFMAs (shape 0: 32x32x64, 1: 16x16x128) back to
+ * back on every SIMD of every CU for about 0.3 ms (after one warm-up run), on
+ * random E2M1 codes (random_codes != 0) or on constant codes; *pflops is the
+ * achieved dense rate, *clock_ghz the median over waves of the shader clock
+ * (s_memtime against the constant-rate s_memrealtime). Synchronous; allocates
+ * and frees its own small buffers. */
+mx4_status mx4_mfma_ceiling(mx4_context *ctx, int shape, int random_codes, double *pflops, double *clock_ghz);
+
 /* Decode table of the hardware E2M1 converter as the kernels use it,
  * out_dev[s*16 + c] for scale byte s and code c (mode 0: bit construction,
  * 1: converter at scale 1 times 2^(s-127), 2: converter with the scale

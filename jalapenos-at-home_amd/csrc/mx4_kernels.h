@@ -149,5 +149,13 @@ hipError_t launch_min_max_scale(const uint8_t* scales, uint64_t count, uint32_t*
                                 hipStream_t s);
 // Hardware-converter table for the exhaustive decode check: out[s*16 + c]
 hipError_t launch_decode_table(int mode, float* out, hipStream_t s);
+// Matrix-core ceiling probe (probe.hip): back-to-back scaled FP4 MFMAs
+// (shape 0: 32x32x64, 1: 16x16x128) on `grid` workgroups of eight waves;
+// clocks[4 w ..] = shader clock and wall clock at the start and end of wave
+// w's loop; sink[grid * 512] keeps the results.
+uint32_t mfma_ceiling_waves(uint32_t grid);
+double mfma_ceiling_flops(int shape, uint32_t iters, uint32_t grid);
+hipError_t launch_mfma_ceiling(int shape, uint32_t iters, bool random, uint32_t grid, uint64_t* clocks, float* sink,
+                               hipStream_t s);
 
 }  // namespace mx4

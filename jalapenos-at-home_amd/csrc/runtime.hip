@@ -7,6 +7,7 @@
 //    (resident weights, one stream, GPU-timed passes, M-based dispatch).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -1285,6 +1286,54 @@ mx4_status mx4_decode_table(mx4_context* ctx, int mode, float* out) {
     DeviceGuard g(ctx->device);
     hipError_t e = mx4::launch_decode_table(mode, out, ctx->stream);
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "decode table launch failed: %s", hipGetErrorString(e));
+    return MX4_OK;
+}
+
+mx4_status mx4_mfma_ceiling(mx4_context* ctx, int shape, int random_codes, double* pflops, double* clock_ghz) {
+    if (!ctx || !pflops || !clock_ghz) return fail(MX4_ERR_ARGUMENT, "null argument");
+    if (shape != 0 && shape != 1) return fail(MX4_ERR_ARGUMENT, "shape must be 0 (32x32x64) or 1 (16x16x128)");
+    DeviceGuard g(ctx->device);
+    int wall_khz = 0;
+    HIP_TRY(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, ctx->device));
+    if (wall_khz <= 0) return fail(MX4_ERR_DEVICE, "no constant-rate clock");
+    // one workgroup of eight waves per CU; 8192 (32x32x64) or 16384
+    // (16x16x128) MFMAs per wave, about 0.3 ms at the full rate
+    const uint32_t grid = (uint32_t)ctx->cus, iters = 1024;
+    const uint32_t waves = mx4::mfma_ceiling_waves(grid);
+    uint64_t* clocks = nullptr;
+    float* sink = nullptr;
+    HIP_TRY(hipMalloc(&clocks, (size_t)waves * 4 * sizeof(uint64_t)));
+    if (hipMalloc(&sink, (size_t)grid * 512 * sizeof(float)) != hipSuccess) {
+        (void)hipFree(clocks);
+        return fail(MX4_ERR_DEVICE, "out of device memory");
+    }
+    mx4_status st = MX4_OK;
+    std::vector<uint64_t> h((size_t)waves * 4);
+    float ms = 0.0f;
+    // a warm-up launch (the clock settles under the load), then the timed one
+    for (int rep = 0; rep < 2 && st == MX4_OK; ++rep) {
+        hipError_t e = hipEventRecord(ctx->ev0, ctx->stream);
+        if (e == hipSuccess) e = mx4::launch_mfma_ceiling(shape, iters, random_codes != 0, grid, clocks, sink, ctx->stream);
+        if (e == hipSuccess) e = hipEventRecord(ctx->ev1, ctx->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(ctx->ev1);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1);
+        if (e != hipSuccess) st = fail(MX4_ERR_DEVICE, "mfma ceiling probe: %s", hipGetErrorString(e));
+    }
+    if (st == MX4_OK && hipMemcpy(h.data(), clocks, h.size() * sizeof(uint64_t), hipMemcpyDeviceToHost) != hipSuccess)
+        st = fail(MX4_ERR_DEVICE, "mfma ceiling probe: copy of the clocks failed");
+    (void)hipFree(clocks);
+    (void)hipFree(sink);
+    if (st != MX4_OK) return st;
+    std::vector<double> ghz;
+    ghz.reserve(waves);
+    for (uint32_t w = 0; w < waves; ++w) {
+        const double dc = (double)(h[4 * w + 1] - h[4 * w]), dw = (double)(h[4 * w + 3] - h[4 * w + 2]);
+        if (dw > 0) ghz.push_back(dc / dw * wall_khz * 1e-6);
+    }
+    if (ghz.empty() || ms <= 0.0f) return fail(MX4_ERR_DEVICE, "mfma ceiling probe: no timing");
+    std::sort(ghz.begin(), ghz.end());
+    *clock_ghz = ghz[ghz.size() / 2];
+    *pflops = mx4::mfma_ceiling_flops(shape, iters, grid) / (ms * 1e-3) / 1e15;
     return MX4_OK;
 }
 

@@ -99,6 +99,7 @@ SIGNATURES = {
     "mx4_timer_begin": (_int, [_vp]),
     "mx4_timer_end": (_int, [_vp, ctypes.POINTER(ctypes.c_double)]),
     "mx4_decode_table": (_int, [_vp, _int, _vp]),
+    "mx4_mfma_ceiling": (_int, [_vp, _int, _int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
 }
 
 
@@ -464,6 +465,13 @@ class Context:
         out = self.buffer(256 * 16 * 4)
         check(lib().mx4_decode_table(self.handle, mode, out.ptr))
         return out.download(np.float32).reshape(256, 16)
+
+    def mfma_ceiling(self, shape: int, random_codes: bool) -> "tuple[float, float]":
+        """Matrix-core ceiling probe: (PFLOP/s, median shader clock in GHz) of
+        back-to-back scaled FP4 MFMAs (shape 0: 32x32x64, 1: 16x16x128)."""
+        pf, ghz = ctypes.c_double(), ctypes.c_double()
+        check(lib().mx4_mfma_ceiling(self.handle, shape, int(random_codes), ctypes.byref(pf), ctypes.byref(ghz)))
+        return pf.value, ghz.value
 
     def timer_begin(self) -> None:
         check(lib().mx4_timer_begin(self.handle))

@@ -1,0 +1,48 @@
+"""The matrix-core ceiling probe (mx4_mfma_ceiling) that the prefill figures
+are read against. These check the measurement, not numerics: the rate it
+reports cannot exceed one MFMA per nominal issue time at the clock the waves
+held, the probe keeps the matrix cores nearly fully issued, and the clock is
+a plausible shader clock for this part (at most its 2.4 GHz peak)."""
+import sys
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+# MI355X: 256 CUs x 4 SIMDs; one scaled FP4 32x32x64 MFMA (131072 flops) per
+# 32 cycles per SIMD, one 16x16x128 (65536 flops) per 16: 4096 flops per
+# cycle per SIMD either way.
+FLOPS_PER_CYCLE_PER_SIMD = 4096
+PEAK_CLOCK_GHZ = 2.4
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    import mx4hip
+
+    if mx4hip.device_count() < 1:
+        pytest.fail("no gfx950 device visible to the HIP library")
+    c = mx4hip.Context(0)
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("shape", [0, 1], ids=["32x32x64", "16x16x128"])
+@pytest.mark.parametrize("random_codes", [True, False], ids=["random", "constant"])
+def test_mfma_ceiling_is_a_physical_rate(ctx, shape, random_codes):
+    pf, ghz = ctx.mfma_ceiling(shape, random_codes)
+    simds = 256 * 4
+    at_clock = FLOPS_PER_CYCLE_PER_SIMD * simds * ghz * 1e9 / 1e15
+    print(f"mfma ceiling shape {shape} random {random_codes}: {pf:.2f} PF at {ghz:.3f} GHz "
+          f"(issue-limited rate at that clock {at_clock:.2f} PF)", flush=True)
+    sys.stdout.flush()
+    assert 0.3 < ghz <= PEAK_CLOCK_GHZ * 1.02
+    assert pf <= at_clock * 1.02
+    assert pf >= 0.7 * at_clock
+
+
+def test_mfma_ceiling_rejects_bad_shape(ctx):
+    import mx4hip
+
+    with pytest.raises(mx4hip.Mx4Error, match="shape"):
+        ctx.mfma_ceiling(2, True)
