@@ -1310,17 +1310,23 @@ mx4_status mx4_mfma_ceiling(mx4_context* ctx, int shape, int random_codes, doubl
     mx4_status st = MX4_OK;
     std::vector<uint64_t> h((size_t)waves * 4);
     float ms = 0.0f;
+    // events of its own: the context's pair may be inside a caller's mx4_timer_begin/end
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+        st = fail(MX4_ERR_DEVICE, "mfma ceiling probe: event creation failed");
     // a warm-up launch (the clock settles under the load), then the timed one
     for (int rep = 0; rep < 2 && st == MX4_OK; ++rep) {
-        hipError_t e = hipEventRecord(ctx->ev0, ctx->stream);
+        hipError_t e = hipEventRecord(e0, ctx->stream);
         if (e == hipSuccess) e = mx4::launch_mfma_ceiling(shape, iters, random_codes != 0, grid, clocks, sink, ctx->stream);
-        if (e == hipSuccess) e = hipEventRecord(ctx->ev1, ctx->stream);
-        if (e == hipSuccess) e = hipEventSynchronize(ctx->ev1);
-        if (e == hipSuccess) e = hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1);
+        if (e == hipSuccess) e = hipEventRecord(e1, ctx->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
         if (e != hipSuccess) st = fail(MX4_ERR_DEVICE, "mfma ceiling probe: %s", hipGetErrorString(e));
     }
     if (st == MX4_OK && hipMemcpy(h.data(), clocks, h.size() * sizeof(uint64_t), hipMemcpyDeviceToHost) != hipSuccess)
         st = fail(MX4_ERR_DEVICE, "mfma ceiling probe: copy of the clocks failed");
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
     (void)hipFree(clocks);
     (void)hipFree(sink);
     if (st != MX4_OK) return st;

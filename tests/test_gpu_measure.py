@@ -46,3 +46,13 @@ def test_mfma_ceiling_rejects_bad_shape(ctx):
 
     with pytest.raises(mx4hip.Mx4Error, match="shape"):
         ctx.mfma_ceiling(2, True)
+
+
+def test_mfma_ceiling_leaves_the_context_timer_alone(ctx):
+    """The probe times itself with events of its own: a caller's
+    mx4_timer_begin/end around it still measures from its own begin (the
+    probe's two runs, about 0.3 ms each, fall inside)."""
+    ctx.timer_begin()
+    ctx.mfma_ceiling(0, True)
+    ms = ctx.timer_end()
+    assert ms > 0.4
