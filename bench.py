@@ -294,16 +294,19 @@ def time_mfma_ceiling(ctx) -> dict:
     published 10.1 PFLOP/s assumes 2.4 GHz; under this load the part lowers
     its clock, further with random codes, so the random-code 32x32x64 rate
     (the prefill kernels' instruction and operand statistics) is the
-    clock-derived ceiling the MXFP4 prefill figures are also read against."""
+    clock-derived ceiling the MXFP4 prefill figures are also read against;
+    likewise the FP8 x FP4 instruction for the MX-FP8 prefill and the bf16
+    32x32x16 for the exact GEMM."""
     out = {}
-    for shape, label in ((0, "32x32x64"), (1, "16x16x128")):
+    for shape, label, peak in ((0, "32x32x64", "mxfp4"), (1, "16x16x128", "mxfp4"), (2, "fp8xfp4_32x32x64", "mxfp8"),
+                               (3, "bf16_32x32x16", "bf16")):
         row = {}
         for codes, rnd in (("random", True), ("constant", False)):
             runs = [ctx.mfma_ceiling(shape, rnd) for _ in range(3)]
             pf = float(np.median([r[0] for r in runs]))
             ghz = float(np.median([r[1] for r in runs]))
             row[codes] = {"TFLOPs": round(pf * 1000, 1), "clock_GHz": round(ghz, 3),
-                          "frac_of_published": round(pf * 1000 / PEAK_TFLOPS["mxfp4"], 4)}
+                          "frac_of_published": round(pf * 1000 / PEAK_TFLOPS[peak], 4)}
         out[label] = row
     out["method"] = ("two waves per SIMD, one workgroup of eight per CU, independent accumulators, about 0.3 ms per "
                      "run after a warm-up; median of 3 runs; clock = shader clock counter over the constant-rate "
@@ -311,13 +314,14 @@ def time_mfma_ceiling(ctx) -> dict:
     return out
 
 
-def time_prefill(ctx, m: int = 512, ceiling: float | None = None) -> dict:
+def time_prefill(ctx, m: int = 512, ceiling: dict | None = None) -> dict:
     """Prefill at M = 512 on block-scaled MFMA: each 8B q/o/gate/up/down shape
     at M = 512, activations bf16 N(0, 1) requantized per 32 along K (MXFP4 and
     MX-FP8), over >= 512 MiB of cold weight copies. The GEMM kernel alone
     (activations requantized beforehand, as when q|k|v or gate|up share them)
-    and requant + GEMM, as TFLOP/s of 2*M*N*K; MXFP4 also as a fraction of the
-    measured matrix-core ceiling (`ceiling`, TFLOP/s) when given."""
+    and requant + GEMM, as TFLOP/s of 2*M*N*K; also as a fraction of the
+    measured matrix-core ceiling of each activation format (`ceiling`,
+    TFLOP/s by format) when given."""
     out = {}
     dims = {name: (n, k) for name, n, k in LAYER}
     ctx.reserve_prefill(m, 12288)
@@ -340,8 +344,8 @@ def time_prefill(ctx, m: int = 512, ceiling: float | None = None) -> dict:
                 t = time_pass(ctx, lambda: [fn(ws[0]) for ws in copies], len(copies))
                 tf = flops / (t["us"] * 1e-6) / 1e12
                 res[label] = {"us": t["us"], "TFLOPs": round(tf, 1), "frac": round(tf / PEAK_TFLOPS[act], 4)}
-                if ceiling and act == "mxfp4":
-                    res[label]["frac_of_measured_ceiling"] = round(tf / ceiling, 4)
+                if ceiling and act in ceiling:
+                    res[label]["frac_of_measured_ceiling"] = round(tf / ceiling[act], 4)
             row[act] = res
         out[name] = row
         arena.release()
@@ -391,11 +395,11 @@ def time_prefill_layer(ctx, weights, m: int = 512) -> dict:
     return out
 
 
-def time_prefill_exact(ctx, ms=(33, 128, 512)) -> dict:
+def time_prefill_exact(ctx, ms=(33, 128, 512), ceiling: float | None = None) -> dict:
     """The exact path a drop-in call takes for M > 32 (AUTO: bf16 x, no
     requantization, f32 accumulation of exact products) on the 8B q/gate/down
     shapes, over >= 512 MiB of cold copies; TFLOP/s against the dense bf16 MFMA
-    peak (2.5 PFLOP/s)."""
+    peak (2.5 PFLOP/s) and, when given, the measured bf16 ceiling (TFLOP/s)."""
     out = {}
     dims = {name: (n, k) for name, n, k in LAYER}
     for i, name in enumerate(("q", "gate", "down")):
@@ -410,6 +414,8 @@ def time_prefill_exact(ctx, ms=(33, 128, 512)) -> dict:
                           len(copies))
             tf = 2.0 * m * n * k / (t["us"] * 1e-6) / 1e12
             row[f"M{m}"] = {"us": t["us"], "TFLOPs": round(tf, 1), "frac_bf16": round(tf / PEAK_TFLOPS["bf16"], 4)}
+            if ceiling:
+                row[f"M{m}"]["frac_of_measured_ceiling"] = round(tf / ceiling, 4)
         out[name] = row
         arena.release()
     return out
@@ -1123,10 +1129,12 @@ def main() -> int:
     if not args.no_prefill:
         log("matrix-core ceiling (scaled FP4 MFMAs back to back) and prefill (M=512, block-scaled MFMA) timing")
         extra["mfma_ceiling"] = time_mfma_ceiling(ctx)
-        extra["prefill"] = time_prefill(ctx, ceiling=extra["mfma_ceiling"]["32x32x64"]["random"]["TFLOPs"])
+        ceil = {act: extra["mfma_ceiling"][key]["random"]["TFLOPs"]
+                for act, key in (("mxfp4", "32x32x64"), ("mxfp8", "fp8xfp4_32x32x64"), ("bf16", "bf16_32x32x16"))}
+        extra["prefill"] = time_prefill(ctx, ceiling=ceil)
         extra["prefill_layer"] = time_prefill_layer(ctx, weights)
         log("exact matrix-core path for M > 32 (AUTO)")
-        extra["prefill_exact_auto"] = time_prefill_exact(ctx)
+        extra["prefill_exact_auto"] = time_prefill_exact(ctx, ceiling=ceil["bf16"])
 
     if not args.no_1p7b:
         log("qwen3-1.7b decode step and the single 6144 x 2048 GEMV")

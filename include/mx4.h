@@ -401,13 +401,15 @@ mx4_status mx4_timer_begin(mx4_context *ctx);
 mx4_status mx4_timer_end(mx4_context *ctx, double *ms);
 
 /* Measurement aid, no counterpart in the reference: the rate the matrix
- * cores sustain on the prefill GEMM's instruction and the shader clock they
- * hold meanwhile. Scaled FP4 MFMAs (shape 0: 32x32x64, 1: 16x16x128) back to
- * back on every SIMD of every CU for about 0.3 ms (after one warm-up run), on
- * random E2M1 codes (random_codes != 0) or on constant codes; *pflops is the
- * achieved dense rate, *clock_ghz the median over waves of the shader clock
- * (s_memtime against the constant-rate s_memrealtime). Synchronous; allocates
- * and frees its own small buffers. */
+ * cores sustain on the matrix-core kernels' instructions and the shader clock
+ * they hold meanwhile. MFMAs of one shape -- 0: block-scaled FP4 x FP4
+ * 32x32x64 (MXFP4 prefill), 1: its 16x16x128 form, 2: block-scaled FP8 x FP4
+ * 32x32x64 (MX-FP8 prefill), 3: bf16 32x32x16 (exact GEMM) -- back to back on
+ * every SIMD of every CU for about 0.3 ms (after one warm-up run), on random
+ * codes (random_codes != 0) or on constant codes; *pflops is the achieved
+ * dense rate, *clock_ghz the median over waves of the shader clock (s_memtime
+ * against the constant-rate s_memrealtime). Synchronous; allocates and frees
+ * its own small buffers. */
 mx4_status mx4_mfma_ceiling(mx4_context *ctx, int shape, int random_codes, double *pflops, double *clock_ghz);
 
 /* Decode table of the hardware E2M1 converter as the kernels use it,

@@ -1291,14 +1291,16 @@ mx4_status mx4_decode_table(mx4_context* ctx, int mode, float* out) {
 
 mx4_status mx4_mfma_ceiling(mx4_context* ctx, int shape, int random_codes, double* pflops, double* clock_ghz) {
     if (!ctx || !pflops || !clock_ghz) return fail(MX4_ERR_ARGUMENT, "null argument");
-    if (shape != 0 && shape != 1) return fail(MX4_ERR_ARGUMENT, "shape must be 0 (32x32x64) or 1 (16x16x128)");
+    if (shape < 0 || shape > 3)
+        return fail(MX4_ERR_ARGUMENT, "shape must be 0 (FP4 32x32x64), 1 (FP4 16x16x128), 2 (FP8 x FP4 32x32x64) "
+                                      "or 3 (bf16 32x32x16)");
     DeviceGuard g(ctx->device);
     int wall_khz = 0;
     HIP_TRY(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, ctx->device));
     if (wall_khz <= 0) return fail(MX4_ERR_DEVICE, "no constant-rate clock");
-    // one workgroup of eight waves per CU; 8192 (32x32x64) or 16384
-    // (16x16x128) MFMAs per wave, about 0.3 ms at the full rate
-    const uint32_t grid = (uint32_t)ctx->cus, iters = 1024;
+    // one workgroup of eight waves per CU; 8192 (16384 for 16x16x128; 4096 for
+    // the half-rate FP8 x FP4) MFMAs per wave, about 0.3 ms at the full rate
+    const uint32_t grid = (uint32_t)ctx->cus, iters = shape == 2 ? 512 : 1024;
     const uint32_t waves = mx4::mfma_ceiling_waves(grid);
     uint64_t* clocks = nullptr;
     float* sink = nullptr;

@@ -468,7 +468,8 @@ class Context:
 
     def mfma_ceiling(self, shape: int, random_codes: bool) -> "tuple[float, float]":
         """Matrix-core ceiling probe: (PFLOP/s, median shader clock in GHz) of
-        back-to-back scaled FP4 MFMAs (shape 0: 32x32x64, 1: 16x16x128)."""
+        back-to-back MFMAs (shape 0: scaled FP4 32x32x64, 1: scaled FP4
+        16x16x128, 2: scaled FP8 x FP4 32x32x64, 3: bf16 32x32x16)."""
         pf, ghz = ctypes.c_double(), ctypes.c_double()
         check(lib().mx4_mfma_ceiling(self.handle, shape, int(random_codes), ctypes.byref(pf), ctypes.byref(ghz)))
         return pf.value, ghz.value

@@ -9,10 +9,12 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-# MI355X: 256 CUs x 4 SIMDs; one scaled FP4 32x32x64 MFMA (131072 flops) per
-# 32 cycles per SIMD, one 16x16x128 (65536 flops) per 16: 4096 flops per
-# cycle per SIMD either way.
-FLOPS_PER_CYCLE_PER_SIMD = 4096
+# MI355X: 256 CUs x 4 SIMDs. Issue rates per SIMD (the published dense peaks
+# at 2.4 GHz): a block-scaled FP4 x FP4 32x32x64 MFMA (131072 flops) every 32
+# cycles and its 16x16x128 form (65536 flops) every 16, 4096 flops per cycle;
+# FP8 x FP4 32x32x64 at half that; bf16 32x32x16 (32768 flops) every 32
+# cycles, 1024 flops per cycle.
+FLOPS_PER_CYCLE_PER_SIMD = {0: 4096, 1: 4096, 2: 2048, 3: 1024}
 PEAK_CLOCK_GHZ = 2.4
 
 
@@ -27,12 +29,13 @@ def ctx():
     c.close()
 
 
-@pytest.mark.parametrize("shape", [0, 1], ids=["32x32x64", "16x16x128"])
+@pytest.mark.parametrize("shape", [0, 1, 2, 3], ids=["fp4-32x32x64", "fp4-16x16x128", "fp8xfp4-32x32x64",
+                                                    "bf16-32x32x16"])
 @pytest.mark.parametrize("random_codes", [True, False], ids=["random", "constant"])
 def test_mfma_ceiling_is_a_physical_rate(ctx, shape, random_codes):
     pf, ghz = ctx.mfma_ceiling(shape, random_codes)
     simds = 256 * 4
-    at_clock = FLOPS_PER_CYCLE_PER_SIMD * simds * ghz * 1e9 / 1e15
+    at_clock = FLOPS_PER_CYCLE_PER_SIMD[shape] * simds * ghz * 1e9 / 1e15
     print(f"mfma ceiling shape {shape} random {random_codes}: {pf:.2f} PF at {ghz:.3f} GHz "
           f"(issue-limited rate at that clock {at_clock:.2f} PF)", flush=True)
     sys.stdout.flush()
@@ -45,7 +48,7 @@ def test_mfma_ceiling_rejects_bad_shape(ctx):
     import mx4hip
 
     with pytest.raises(mx4hip.Mx4Error, match="shape"):
-        ctx.mfma_ceiling(2, True)
+        ctx.mfma_ceiling(4, True)
 
 
 def test_mfma_ceiling_leaves_the_context_timer_alone(ctx):
