@@ -754,14 +754,15 @@ hipError_t dispatch(const PrefillArgs& a) {
     //  (24.0 -> 18.2 us);
     //  gate|up (24576 rows), MXFP4: 128 x 192 tiles in stages of 2, 3 deep, so
     //  two workgroups share a CU (46.1 -> 43.2 us);
-    //  q / o (4096 rows, K = 4096) and down (4096 rows, K = 12288): K in two
-    //  halves of their own four waves (two waves per SIMD), stages of 2, 4
-    //  deep; MXFP4 on 128 x 64 tiles (q 11.4 -> 10.7 us against the one-ring
-    //  tile, down 27.7 -> 25.7 us against 4 x 2 wave tiles in K quarters),
-    //  MX-FP8 on 64 x 128 tiles (q 14.7 -> 13.5 us, down 34.1 -> 33.3 us
+    //  q / o (4096 rows, K = 4096): K in two halves of their own four waves
+    //  (two waves per SIMD), stages of 2, 4 deep; MXFP4 on 128 x 64 tiles
+    //  (11.4 -> 10.7 us against the one-ring tile in two sweeps, even in a
+    //  third), MX-FP8 on 64 x 128 tiles (14.7 -> 13.5 and 14.8 -> 14.2 us
     //  against 2 x 4 wave tiles in K quarters).
-    // gate alone and the other MX-FP8 shapes measured no faster there.
-    if ((a.k == 4096 || a.k == 12288) && ntot <= 4096) {
+    // gate or down alone and the other MX-FP8 shapes measured no faster there
+    // (down with K halves of their own waves: ahead in one sweep, 2-10% behind
+    // in three repetitions on another machine).
+    if (a.k == 4096 && ntot <= 4096) {
         if constexpr (A_FP8) return go_lds<true, 2, 2, 1, 2, 2, 4, 2>(a);
         else return go_lds<false, 2, 2, 2, 1, 2, 4, 2>(a);
     }
@@ -784,6 +785,12 @@ hipError_t dispatch(const PrefillArgs& a) {
     // workgroup tiles over the full K, 192 workgroups (MXFP4 17.3 -> 15.9 us,
     // MX-FP8 22.4 -> 20.6 us against 2 x 2 tiles in K halves)
     if (ntot > 4096 && a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 1, 2, 0>(a);
+    // K = 12288 (down) in K quarters: MX-FP8 on 2 x 4 wave tiles (29.5 -> 27.1 us
+    // warm), MXFP4 on 4 x 2 wave tiles (cold weights: 30.9 -> 26.4 us)
+    if (a.k == 12288 && ntot <= 4096) {
+        if constexpr (A_FP8) return go_parts<true, 2, 4, 4>(a);
+        else return go_parts<false, 4, 2, 4>(a);
+    }
     if (a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 2, 2, 32>(a);
     if (a.k == 12288) return go<A_FP8, 2, 2, 2, 4, 2, 2, 96>(a);
     if (a.k % 512 == 0) return go<A_FP8, 2, 2, 2, 4, 2, 2, 0>(a);
