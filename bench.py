@@ -745,8 +745,10 @@ def summarize(kind: str, dirs: list[str]) -> None:
     WRITE_DIR` (FETCH_SIZE / WRITE_SIZE of --profile-traffic, calibrated by the
     1 GiB copy), `step-pmc DIR` (per-launch averages of any counters of
     --profile-traffic), `verify-trace DIR` (--profile-verify), `prefill-trace DIR`
-    and `prefill-pmc DIR` (--profile-prefill), `prefill-compare DIR`
-    (--profile-prefill-compare)."""
+    and `prefill-pmc DIR` (--profile-prefill), `prefill-shapes TRACE_DIR
+    PMC_DIR` (--profile-prefill: each shape's GEMM dispatches, in the order the
+    mode issues them, with their traced durations and MFMA counters),
+    `prefill-compare DIR` (--profile-prefill-compare)."""
     d0 = Path(dirs[0])
     st = _stamp_of(d0)
     print(f"commit: {_git_head()}")
@@ -850,6 +852,52 @@ def summarize(kind: str, dirs: list[str]) -> None:
             grp = [per[d] for d in ids[i * calls:(i + 1) * calls]]
             avg = [sum(c.get(cn, 0.0) for c in grp) / calls for cn in names]
             print(f"| {shape} | {desc} | " + " | ".join(f"{v:.4g}" for v in avg) + " |")
+    elif kind == "prefill-shapes":
+        # --profile-prefill issues, per shape (q, o, gate, up, down) and
+        # activation format (MXFP4, MX-FP8), 5 GEMMs on requantized activations
+        # and 5 requantize + GEMM calls, then, for q, gate and down, 5 exact
+        # GEMMs: the GEMM dispatches of the trace and of the counter run follow
+        # that order
+        m = int(st.get("m", 512))
+        calls = int(st.get("gemm_launches_per_shape_and_format", 10))
+        exact = int(st.get("exact_gemm_launches_per_shape", 5))
+        dims = {name: (n, k) for name, n, k in LAYER}
+        seq = []
+        for name in ("q", "o", "gate", "up", "down"):
+            seq += [(name, "mxfp4")] * calls + [(name, "mxfp8")] * calls
+            if name in ("q", "gate", "down"):
+                seq += [(name, "exact bf16")] * exact
+        gemm = ("mx4::prefill_kernel", "mx4::prefill_lds_kernel", "mx4::gemm_exact")
+        trace = sorted((r for r in _read_csv(d0, "kernel_trace.csv") if _short(r["Kernel_Name"]).startswith(gemm)),
+                       key=lambda r: int(r["Dispatch_Id"]))
+        pmc = defaultdict(lambda: defaultdict(float))
+        for r in _read_csv(Path(dirs[1]), "counter_collection.csv"):
+            if _short(r["Kernel_Name"]).startswith(gemm):
+                pmc[int(r["Dispatch_Id"])][r["Counter_Name"]] += float(r["Counter_Value"])
+        pids = sorted(pmc)
+        if len(trace) != len(seq) or len(pids) != len(seq):
+            raise SystemExit(f"{len(trace)} traced / {len(pids)} counted GEMM dispatches, {len(seq)} expected")
+        peak = {"mxfp4": PEAK_TFLOPS["mxfp4"], "mxfp8": PEAK_TFLOPS["mxfp8"], "exact bf16": PEAK_TFLOPS["bf16"]}
+        print("\n| shape | act | kernel instance | dispatches | us | TFLOP/s | of peak | MOPS x 512 | MFMA busy |")
+        print("|---|---|---|---|---|---|---|---|---|")
+        i = 0
+        while i < len(seq):
+            j = i
+            while j < len(seq) and seq[j] == seq[i]:
+                j += 1
+            name, act = seq[i]
+            n, k = dims[name]
+            us = float(np.median([(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in trace[i:j]]))
+            grp = [pmc[d] for d in pids[i:j]]
+            mops = float(np.mean([c.get("SQ_INSTS_VALU_MFMA_MOPS_F6F4", 0) + c.get("SQ_INSTS_VALU_MFMA_MOPS_F8", 0) +
+                                  c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0) for c in grp])) * 512
+            busy = float(np.mean([c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) for c in grp])) / (us * 1e-6 * 2.4e9 * 1024)
+            flops = 2.0 * m * n * k
+            tf = flops / (us * 1e-6) / 1e12
+            inst = _short(trace[i]["Kernel_Name"]).replace("mx4::", "")
+            print(f"| {name} {m}x{k}->{n} | {act} | {inst} | {j - i} | {us:.2f} | {tf:.0f} | "
+                  f"{tf / peak[act]:.1%} | {mops:.4g} ({mops / flops:.3f} x 2MNK) | {busy:.1%} |")
+            i = j
     elif kind == "prefill-trace":
         rows = _read_csv(d0, "kernel_trace.csv")
         per = defaultdict(list)
@@ -911,7 +959,7 @@ def main() -> int:
                          "and 5 exact GEMMs (AUTO, bf16 x) for q, gate and down")
     ap.add_argument("--profile-prefill-compare", action="store_true",
                     help="for counter runs: gate and q at M=512 (MXFP4), 5 calls each of the register-direct and "
-                         "the workgroup-shared prefill kernel")
+                         "the workgroup-shared prefill kernel (for q also with K in halves of their own waves)")
     ap.add_argument("--profile-verify", action="store_true",
                     help="for kernel traces: only the speculative-verify shapes (each 8B projection and the lm_head "
                          "at M = 1..32 through AUTO over cold copies, enqueued 4 times)")
@@ -919,7 +967,7 @@ def main() -> int:
     ap.add_argument("--summarize", nargs="+", metavar=("KIND", "DIR"),
                     help="print the markdown summary of rocprofv3 CSV output: trace DIR | traffic FETCH_DIR "
                          "WRITE_DIR | step-pmc DIR | verify-trace DIR | prefill-trace DIR | prefill-pmc DIR | "
-                         "prefill-compare DIR")
+                         "prefill-shapes TRACE_DIR PMC_DIR | prefill-compare DIR")
     args = ap.parse_args()
 
     if args.summarize:
@@ -1028,7 +1076,9 @@ def main() -> int:
         plan = [("gate", "register-direct 4x3 tiles, K halves (default)", (0, 0, 0)),
                 ("gate", "workgroup-shared 128x192, U=4, D=2", (128, 192, 16 * 4 + 2)),
                 ("q", "register-direct 2x2 tiles, K halves", (64, 128, 2)),
-                ("q", "workgroup-shared 128x64, U=2, D=4 (default)", (128, 64, 16 * 2 + 4))]
+                ("q", "workgroup-shared 128x64, U=2, D=4, one ring", (128, 64, 16 * 2 + 4)),
+                ("q", "workgroup-shared 128x64, U=2, D=4, K halves of their own waves (default)",
+                 (128, 64, 128 + 16 * 2 + 4))]
         for name, _, inst in plan:
             n, k, w = by[name]
             w.prepare_prefill()
