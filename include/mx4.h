@@ -211,7 +211,7 @@ mx4_status mx4_gemv_tokens_config(mx4_context *ctx, const void *x_dev, uint32_t 
 
 /* Tuning hook for the exact tiled GEMM (MX4_PATH_GEMM): waves per workgroup
  * along M and N and 32x32 MFMA tiles per wave along M and N, one of the
- * compiled instances (2x2 waves of 2x2, 2x1, 1x2 or 1x1 tiles; 1x4 waves of
+ * compiled instances (2x2 waves of 2x3, 2x2, 2x1, 1x2 or 1x1 tiles; 1x4 waves of
  * 2x2, 2x1, 1x2 or 1x1; 2x4 waves of 2x2 (bf16 x only) or 1x2; 4x1 waves of
  * 1x2), and K slices across workgroups (0 or 1: none; a split needs K a
  * multiple of 128 * k_slices and k_slices * m * rows * 4 bytes within the

@@ -280,6 +280,7 @@ template <bool XBF16>
 hipError_t dispatch(const GemvArgs& a, const GemmConfig& c, float* part) {
     // instances: (waves along M x along N, MFMA tiles per wave along M x N)
     const uint32_t ks = c.ks < 1 ? 1u : (uint32_t)c.ks;
+    if (c.wm == 2 && c.wn == 2 && c.tm == 2 && c.tn == 3) return go<XBF16, 2, 2, 2, 3>(a, ks, part);
     if (c.wm == 2 && c.wn == 2 && c.tm == 2 && c.tn == 2) return go<XBF16, 2, 2, 2, 2>(a, ks, part);
     if (c.wm == 2 && c.wn == 2 && c.tm == 2 && c.tn == 1) return go<XBF16, 2, 2, 2, 1>(a, ks, part);
     if (c.wm == 2 && c.wn == 2 && c.tm == 1 && c.tn == 2) return go<XBF16, 2, 2, 1, 2>(a, ks, part);
@@ -315,26 +316,35 @@ hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* force
                          (uint64_t)c.ks * a.m * a.n * 4 > part_bytes))
             return hipErrorNotSupported;
     } else {
-        // The largest tile whose grid still reaches three quarters of the CUs
-        // (larger tiles re-read fewer operand bytes; a grid below that leaves
-        // CUs idle), else the smallest. From a sweep of every instance on the
-        // Qwen3-8B q/gate/down weights at M = 33..512 (bf16 x, cold weights):
-        // gate at M = 512 128 x 256 (8 waves) 51 us, at 256 64 x 256 34 us, at
-        // 128 64 x 128 23 us; q and down at 512 64 x 128 (24 / 64 us); 64 x 64
-        // below (q 16-17 us, down 42-46 us, latency-bound: too few tiles).
-        struct Cand { int wm, wn, tm, tn, bm, bn; };
-        const Cand cands[] = {{2, 4, 2, 2, 128, 256}, {1, 4, 2, 2, 64, 256}, {1, 4, 2, 1, 64, 128},
-                              {2, 2, 1, 1, 64, 64}};
-        const uint64_t want = (uint64_t)(cus > 0 ? cus : 256) * 3 / 4;
-        Cand pick = cands[3];
+        // The tile with the least estimated time: whole rounds of workgroups
+        // (one per CU) times the time one round of that tile takes. The round
+        // times (µs at K = 4096, bf16 x) are from a sweep of every instance on
+        // the Qwen3-8B q, gate and down weights at M = 64..2048 on MI355X
+        // (cold weights); with them the pick was the fastest instance, or
+        // within 2% of it, at every M of the sweep: gate at M = 384 / 768 /
+        // 1536 128 x 192 (47 / 90 / 145 us, where the largest tile whose grid
+        // reaches three quarters of the CUs takes 64 / 102 / 157 us), at 2048
+        // 128 x 256 (176 us); q and down at M = 512 64 x 128 (23 / 64 us).
+        // The larger tiles re-read fewer operand bytes per flop, the smaller
+        // ones leave fewer CUs idle in the last round.
+        struct Cand { int wm, wn, tm, tn, bm, bn; double round_us; };
+        const Cand cands[] = {{2, 4, 2, 2, 128, 256, 50.0}, {2, 2, 2, 3, 128, 192, 46.0},
+                              {1, 4, 2, 2, 64, 256, 33.5},  {2, 2, 2, 2, 128, 128, 34.5},
+                              {1, 4, 2, 1, 64, 128, 22.0},  {2, 2, 1, 1, 64, 64, 16.5}};
+        const uint64_t nc = (uint64_t)(cus > 0 ? cus : 256);
+        const uint64_t want = nc * 3 / 4;
+        const Cand* best = nullptr;
+        double best_t = 0.0;
         for (const Cand& cd : cands) {
             if (!a.x_bf16 && cd.wn == 4 && cd.wm == 2) continue;  // no f32 instance of 128 x 256
             const uint64_t tiles = (uint64_t)((a.m + cd.bm - 1) / cd.bm) * ((a.n + cd.bn - 1) / cd.bn);
-            if (tiles >= want) {
-                pick = cd;
-                break;
+            const double t = (double)((tiles + nc - 1) / nc) * cd.round_us;
+            if (!best || t < best_t) {
+                best = &cd;
+                best_t = t;
             }
         }
+        const Cand pick = *best;
         c.wm = pick.wm; c.wn = pick.wn; c.tm = pick.tm; c.tn = pick.tn;
         // A grid still short of the CUs (few token rows): split K across up to
         // four workgroups per tile, each slice whole stages, when the partials

@@ -926,8 +926,8 @@ def test_skinny_ragged_rows_and_identity(mx4, ctx, oracle):
 
 # ------------------------------------------------------------------ exact GEMM (M > 32)
 
-GEMM_INSTANCES = [(2, 2, 2, 2), (2, 2, 2, 1), (2, 2, 1, 2), (4, 1, 1, 2), (2, 2, 1, 1), (1, 4, 2, 2), (1, 4, 2, 1),
-                  (1, 4, 1, 2), (1, 4, 1, 1), (2, 4, 2, 2), (2, 4, 1, 2)]
+GEMM_INSTANCES = [(2, 2, 2, 3), (2, 2, 2, 2), (2, 2, 2, 1), (2, 2, 1, 2), (4, 1, 1, 2), (2, 2, 1, 1), (1, 4, 2, 2),
+                  (1, 4, 2, 1), (1, 4, 1, 2), (1, 4, 1, 1), (2, 4, 2, 2), (2, 4, 1, 2)]
 GEMM_BF16_ONLY = {(2, 4, 2, 2)}  # its f32 tile would leave LDS room for one stage only
 
 
@@ -978,16 +978,18 @@ def test_gemm_identity_and_oracle_every_instance(mx4, ctx, oracle, inst, ks):
 
 @pytest.mark.parametrize("name", ["q", "gate", "down"])
 def test_gemm_auto_8b_shapes(mx4, ctx, oracle, name):
-    """AUTO at M = 33, 128 and 512 token rows on the Qwen3-8B q, gate and down
-    weights (the drop-in's path for a prompt; engine/src/gpu.rs:510-514) takes
-    the exact tiled GEMM: sampled token rows x weight rows against the oracle,
-    bf16 and f32 activations."""
+    """AUTO at M = 33, 128, 384, 512 and 768 token rows on the Qwen3-8B q,
+    gate and down weights (the drop-in's path for a prompt;
+    engine/src/gpu.rs:510-514) takes the exact tiled GEMM, with the tile the
+    round-time estimate picks (64x64 with K split, 64x128, 64x256 and 128x192
+    among these): sampled token rows x weight rows against the oracle, bf16
+    and f32 activations."""
     n, k = QWEN8[name]
     rng = np.random.default_rng(91)
     w = ctx.synth_weight(500 + list(QWEN8).index(name), n, k, 0.02)
     packed, scales = ctx.download_weight(w)
     cols = _sample_rows(n, 64, rng)
-    for m in (33, 128, 512):
+    for m in (33, 128, 384, 512, 768):
         say(f"gemm AUTO 8B {name} m={m}")
         x = oracle.bf16_to_f32(oracle.synth_bf16(510 + m, 1.0, m * k)).reshape(m, k)
         rows = np.unique(np.concatenate([[0, m - 1], rng.choice(m, 14, replace=False)]))
