@@ -480,7 +480,7 @@ hipError_t go_k(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
         // they need 16 or 12 waves per workgroup and measured slower (down)
         case 8192: return go<XBF16, MT, U, 8 / U, TW, false>(a, cus);
         case 12288:
-            // bf16 x from 8 tokens on: four workgroups per tile, each over a
+            // bf16 x from 12 tokens on: four workgroups per tile, each over a
             // 3072-wide K slice with its activations resident and the
             // three-tile ring, so that every workgroup reads a quarter of x
             // instead of all of it. 8B down at 8 / 12 / 16 / 24 / 32 tokens:
