@@ -613,7 +613,9 @@ __device__ __forceinline__ void rows_dot_mt(const LaneX<true, BPL> (&xr)[MT], co
     }
 }
 
-template <int WG, int BPL, int R, int MT>
+// SHARED: several teams per workgroup share one LDS copy of the token rows
+// (tpw > 1); otherwise each team loads its own into registers (tpw == 1).
+template <int WG, int BPL, int R, int MT, bool SHARED>
 __global__ __launch_bounds__(512) void gemv_mt_kernel(const uint8_t* __restrict__ packed,
                                                       const uint8_t* __restrict__ scales,
                                                       const void* __restrict__ x, uint32_t m, uint32_t n,
@@ -644,15 +646,36 @@ __global__ __launch_bounds__(512) void gemv_mt_kernel(const uint8_t* __restrict_
     const uint32_t first = blockIdx.x * tpw;  // the workgroup's first team visits the most row-sets
     uint32_t rs = first + team;
     RowSet<true, BPL, R> a, b;
-    load_rowset<true, WG, BPL, R>(sg, rs, rowsets, t, row_bytes, nblk, a);
     // Dynamic LDS: the MT token rows of x when several teams share the
     // workgroup (loaded once, then each lane copies its blocks to registers),
     // then the cross-wave partial sums [tpw][2][WG][RM].
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    if constexpr (SHARED) {
+        // The token rows' direct-to-LDS loads go out before the first
+        // row-set's, so that waiting for them (loads return in order) does not
+        // also wait for the weights: the second row-set is issued once x is
+        // in (8B down / gate at 2 tokens 8.5 / 7.8 -> 7.0 / 7.2 us). Token
+        // rows >= m lie past the resource and read as zeros; xbytes / 16 is a
+        // multiple of 64, so every turn of the loop is whole waves.
+        const uint32_t live = (m < (uint32_t)MT ? m : (uint32_t)MT) * k * 2;
+        const __amdgpu_buffer_rsrc_t xres = rsrc(x, live);
+        const uint32_t wave0 = threadIdx.x - threadIdx.x % 64;
+        for (uint32_t c0 = wave0; c0 < xbytes / 16; c0 += tpw * T)
+            load_lds16(xres, (lds_ptr)(smem + 16 * c0), 16 * (c0 + lane));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    load_rowset<true, WG, BPL, R>(sg, rs, rowsets, t, row_bytes, nblk, a);
     float(*red)[WG][RM] = reinterpret_cast<float(*)[WG][RM]>(smem + (tpw > 1 ? xbytes : 0)) + 2 * team;
     LaneX<true, BPL> xr[MT];
     const uint8_t* xb = static_cast<const uint8_t*>(x);
-    if (tpw > 1) {
+    if constexpr (SHARED) {
+        // the first row-set's 2 R BPL loads were issued after x's
+        wait_vm<2 * R * BPL>();
+        __syncthreads();
+#pragma unroll
+        for (int tok = 0; tok < MT; ++tok) xr[tok].load_lds(smem + (size_t)tok * k * 2, t, T);
+    } else if (tpw > 1) {
+        // (the launcher sends shared copies to the SHARED instances)
         const uint32_t live = (m < (uint32_t)MT ? m : (uint32_t)MT) * k * 2;
         for (uint32_t c = threadIdx.x; c < xbytes / 16; c += tpw * T)
             *reinterpret_cast<u32x4*>(smem + 16 * c) = 16 * c < live ? load_u32x4(xb + 16 * c) : u32x4{0u, 0u, 0u, 0u};
@@ -660,6 +683,7 @@ __global__ __launch_bounds__(512) void gemv_mt_kernel(const uint8_t* __restrict_
 #pragma unroll
         for (int tok = 0; tok < MT; ++tok) xr[tok].load_lds(smem + (size_t)tok * k * 2, t, T);
     } else {
+        // each team's own copy, behind the first row-set
 #pragma unroll
         for (int tok = 0; tok < MT; ++tok) {
             if ((uint32_t)tok < m) {
@@ -1018,8 +1042,12 @@ static hipError_t go_mt(const GemvArgs& a, int cus, uint32_t teams, uint32_t tpw
     if (teams > rowsets) teams = rowsets;
     const uint32_t grid = (teams + tpw - 1) / tpw;
     const size_t lds = (tpw > 1 ? xbytes : 0) + (size_t)tpw * 2 * WG * R * MT * sizeof(float);
-    hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT>), dim3(grid), dim3(64 * WG * tpw), lds, a.stream, a.packed,
-                       a.scales, a.x, a.m, a.n, rowsets, tpw, grid, a.y);
+    if (tpw > 1)
+        hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, true>), dim3(grid), dim3(64 * WG * tpw), lds, a.stream,
+                           a.packed, a.scales, a.x, a.m, a.n, rowsets, tpw, grid, a.y);
+    else
+        hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, false>), dim3(grid), dim3(64 * WG * tpw), lds, a.stream,
+                           a.packed, a.scales, a.x, a.m, a.n, rowsets, tpw, grid, a.y);
     return hipGetLastError();
 }
 
