@@ -389,14 +389,16 @@ __device__ __forceinline__ void gemv_m1_body(const Segs& early, const void* __re
     RowSet<XBF16, BPL, R> a, b;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t xbytes = k * (XBF16 ? 2 : 4);
-    // K = 64 WG BPL blocks of 32. From K = 6144 on (12 KiB of bf16 x per
-    // workgroup) x is fetched first when several teams share one LDS copy of
-    // it: its direct-to-LDS loads go out before the first row-set's, so that
-    // waiting for them (loads return in order) does not also wait for the
-    // weights, and the second row-set is issued once x is in, not once the
-    // first one is (8B down 7.10 -> 6.43 us). With 8 KiB of x (K = 4096) the
-    // same order measured 0.05-0.13 us slower, so there x follows the weights.
-    constexpr bool XFIRST = WG * BPL >= 3;
+    // K = 64 WG BPL blocks of 32. When several teams share one LDS copy of x,
+    // x is fetched first from K = 6144 on (12 KiB of bf16 x per workgroup)
+    // and for one-row teams: its direct-to-LDS loads go out before the first
+    // row-set's, so that waiting for them (loads return in order) does not
+    // also wait for the weights, and the second row-set is issued once x is
+    // in, not once the first one is (8B down 7.10 -> 6.43 us; q, o 3.62 ->
+    // 3.52 us and k, v 2.54 -> 2.29 us with four one-row teams sharing x).
+    // With two-row teams at K = 4096 (gate, gate|up, lm_head) the same order
+    // measured 0.05-0.13 us slower, so there x follows the weights.
+    constexpr bool XFIRST = WG * BPL >= 3 || R == 1;
     if (XFIRST && tpw > 1) {
         const __amdgpu_buffer_rsrc_t xres = rsrc(x, xbytes);
         const uint32_t lane = threadIdx.x % 64, wave0 = threadIdx.x - lane;
@@ -871,6 +873,9 @@ static void default_m1_config(uint32_t k, uint32_t rows, int cus, M1Config& c) {
             break;
         case 128:  // K = 4096
             c.wg = 1; c.r = 2; c.grid = (rows <= 8192 ? 4 : 16) * scale;
+            // up to 8192 rows (q, o, k, v, q|k|v): four one-row teams per
+            // workgroup sharing x, fetched ahead of the weights
+            if (rows <= 8192) { c.r = 1; c.grid = 8 * scale; c.tpw = 4; }
             if (rows > 8192) c.tpw = 8;
             if (rows > 65536) { c.wg = 2; c.grid = 8 * scale; c.tpw = 4; }  // vocabulary-sized
             break;
