@@ -867,6 +867,9 @@ static void default_m1_config(uint32_t k, uint32_t rows, int cus, M1Config& c) {
     switch (nblk) {
         case 64:  // K = 2048 (Qwen3-1.7B sweep: q|k|v 3.33 -> 3.14 us, gate|up 4.86 -> 4.71 us)
             c.wg = 1; c.r = 2; c.grid = (rows > 2048 && rows <= 4096 ? 4 : 12) * scale;
+            // up to 2048 rows (o): eight one-row teams per workgroup sharing x,
+            // fetched ahead of the weights (2.42 -> 2.22 us)
+            if (rows <= 2048) { c.r = 1; c.grid = 8 * scale; c.tpw = 8; }
             if (rows > 4096 && rows <= 8192) c.r = 4;
             if (rows > 8192) c.grid = 16 * scale;
             if (rows > 65536) { c.r = 4; c.tpw = 8; c.grid = 8 * scale; }  // vocabulary-sized
