@@ -83,6 +83,7 @@ VERIFY_REPS = 4              # enqueues of each verify block under --profile-ver
 MIN_COPIES = 8               # launches per timed pass at least (weights rotated)
 ARENA_ALIGN = 2 << 20
 TRAFFIC_PROFILE = ROOT / "profiles" / "gemv_qwen3_8b_m1_step_traffic.md"
+PREFILL_PROFILE = ROOT / "profiles" / "prefill_qwen3_8b_m512.md"
 
 
 def gemv_bytes(m: int, n: int, k: int, x_bytes: int = 2) -> int:
@@ -314,6 +315,50 @@ def time_mfma_ceiling(ctx) -> dict:
     return out
 
 
+def _err(y: np.ndarray, r: np.ndarray) -> dict:
+    """max_i |y - r| / max_i |r| and ||y - r||_2 / ||r||_2
+    (python/src/jalapenos_reference/compare.py:19-22, engine/tests/mxfp4.rs:76-84)."""
+    y, r = y.astype(np.float64), r.astype(np.float64)
+    d = y - r
+    return {"max_rel": float(f"{np.max(np.abs(d)) / max(np.max(np.abs(r)), 1e-300):.3e}"),
+            "rel_l2": float(f"{np.sqrt(np.sum(d * d)) / max(np.sqrt(np.sum(r * r)), 1e-300):.3e}")}
+
+
+def prefill_error(ctx, w, xb, x_host: np.ndarray, m: int, rng) -> dict:
+    """What requantizing the activations costs (information, not a parity
+    gate): the M = 512 outputs of requant + block-scaled MFMA (MXFP4 and
+    MX-FP8 activations) and of the exact AUTO path (bf16 MFMA, no
+    requantization) on sampled token rows x weight rows, against the oracle on
+    the unquantized bf16 x (engine/src/lib.rs:240-266); and, for the
+    requantized paths, against the oracle on dequant(requant(x)), the parity
+    bar of the tests."""
+    oracle = _oracle()
+    n, k = w.rows, w.cols
+    packed, scales = ctx.download_weight(w)
+    rows = np.unique(np.concatenate([[0, m - 1], rng.choice(m, 14, replace=False)]))
+    cols = np.unique(np.concatenate([[0, n - 1], rng.choice(n, 62, replace=False)]))
+
+    def ref(xs):
+        return np.concatenate([oracle.matmul_rows(xs, packed.reshape(-1), scales.reshape(-1), int(c), int(c) + 1)
+                               for c in cols], axis=1)
+
+    exact = ref(x_host[rows])
+    yb = ctx.buffer(m * n * 4)
+    out = {}
+    for act, code in (("mxfp4", mx4hip.ACT_MXFP4), ("mxfp8", mx4hip.ACT_MXFP8)):
+        ctx.matmul_prefill(xb, mx4hip.BF16, m, w, code, yb)
+        y = yb.download(np.float32).reshape(m, n)[np.ix_(rows, cols)]
+        xd = oracle.dequantize(*oracle.quantize(x_host[rows])) if act == "mxfp4" else \
+            oracle.dequantize_fp8(*oracle.quantize_fp8(x_host[rows]))
+        e = _err(y, exact)
+        e["vs_requantized_oracle"] = _err(y, ref(xd))
+        out[act] = e
+    ctx.matmul_ptr(xb.ptr, mx4hip.BF16, m, w, yb.ptr)
+    out["exact_auto"] = _err(yb.download(np.float32).reshape(m, n)[np.ix_(rows, cols)], exact)
+    out["sample"] = f"{len(rows)} token rows x {len(cols)} weight rows"
+    return out
+
+
 def time_prefill(ctx, m: int = 512, ceiling: dict | None = None) -> dict:
     """Prefill at M = 512 on block-scaled MFMA: each 8B q/o/gate/up/down shape
     at M = 512, activations bf16 N(0, 1) requantized per 32 along K (MXFP4 and
@@ -325,6 +370,7 @@ def time_prefill(ctx, m: int = 512, ceiling: dict | None = None) -> dict:
     out = {}
     dims = {name: (n, k) for name, n, k in LAYER}
     ctx.reserve_prefill(m, 12288)
+    rng = np.random.default_rng(512)
     for i, name in enumerate(("q", "o", "gate", "up", "down")):
         n, k = dims[name]
         arena, copies = rotation(ctx, [(n, k)], 50000 + 1000 * i)
@@ -332,6 +378,7 @@ def time_prefill(ctx, m: int = 512, ceiling: dict | None = None) -> dict:
             ws[0].prepare_prefill()  # the matrix-core copy of each weight, outside the timed passes
         xb = ctx.buffer(m * k * 2)
         ctx.synth_bf16(3, 1.0, m * k, xb)
+        x_host = (xb.download(np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(m, k)
         yb = ctx.buffer(m * n * 4)
         flops = 2.0 * m * n * k
         row = {"m": m, "n": n, "k": k, "copies": len(copies)}
@@ -347,8 +394,62 @@ def time_prefill(ctx, m: int = 512, ceiling: dict | None = None) -> dict:
                 if ceiling and act in ceiling:
                     res[label]["frac_of_measured_ceiling"] = round(tf / ceiling[act], 4)
             row[act] = res
+        row["requant_error"] = prefill_error(ctx, copies[0][0], xb, x_host, m, rng)
         out[name] = row
         arena.release()
+    return out
+
+
+def prefill_counters() -> dict:
+    """MFMA operation and busy counters of the M = 512 prefill dispatches
+    from the committed profile summary, when its stamp names the library this
+    process loaded (otherwise only the reason)."""
+    f = PREFILL_PROFILE
+    if not f.exists():
+        return {"note": "no prefill profile"}
+    sha = library_sha256()
+    text = f.read_text().splitlines()
+    stamp = next((ln.split(":", 1)[1].strip() for ln in text if ln.startswith("library_sha256:")), "missing")
+    if stamp != sha:
+        return {"note": f"profile stamp {stamp[:12]} != loaded library {sha[:12]}"}
+    out = {}
+    for ln in text:
+        cells = [c.strip() for c in ln.strip().strip("|").split("|")]
+        if len(cells) != 9 or not cells[0]:
+            continue
+        key = f"{cells[0].split()[0]} {cells[1]}"
+        if key not in ("gate mxfp4", "down mxfp4", "gate mxfp8"):
+            continue
+        out[key] = [cells[2].replace(" ", ""), float(cells[4]), float(cells[7].split("(")[1].split()[0]),
+                    round(float(cells[8].rstrip("%")) / 100, 3)]
+    out["cols"] = ["instance", "warm_us", "MOPSx512/2MNK", "busy@2.4GHz"]
+    out["stamp"] = sha[:12]
+    return out
+
+
+def prefill_summary(pf: dict, layer: dict, ceiling: dict) -> dict:
+    """The M = 512 half of the headline metric, compact: per 8B shape and
+    activation format [GEMM us, TFLOP/s, of peak, of the measured ceiling,
+    requant + GEMM us, TFLOP/s, of peak]; the grouped layer; the largest
+    requantization error against the unquantized oracle; counters of the
+    dominant instances from the stamped profile."""
+    out = {"m": 512, "peak_TFLOPs": {"mxfp4": PEAK_TFLOPS["mxfp4"], "mxfp8": PEAK_TFLOPS["mxfp8"]},
+           "measured_ceiling_TFLOPs": {a: round(ceiling[a], 1) for a in ("mxfp4", "mxfp8")},
+           "cols": ["gemm_us", "gemm_TF", "gemm_of_peak", "gemm_of_ceiling", "rq_gemm_us", "rq_gemm_TF",
+                    "rq_gemm_of_peak"], "rq": "requantization of the bf16 activations included"}
+    for act in ("mxfp4", "mxfp8"):
+        out[act] = {}
+        for name, row in pf.items():
+            g, r = row[act]["gemm"], row[act]["requant+gemm"]
+            out[act][name] = [g["us"], round(g["TFLOPs"]), g["frac"], g.get("frac_of_measured_ceiling"),
+                              r["us"], round(r["TFLOPs"]), r["frac"]]
+    out["layer_grouped"] = {a: [layer[a]["grouped"]["us"], layer[a]["grouped"]["frac"]] for a in ("mxfp4", "mxfp8")}
+    out["layer_cols"] = ["us, 7 projections with rq", "of_peak"]
+    out["requant_error_vs_unquantized"] = {
+        a: {"max_rel": max(row["requant_error"][a]["max_rel"] for row in pf.values()),
+            "rel_l2": max(row["requant_error"][a]["rel_l2"] for row in pf.values())}
+        for a in ("mxfp4", "mxfp8", "exact_auto")}
+    out["counters"] = prefill_counters()
     return out
 
 
@@ -631,6 +732,51 @@ def cpu_baseline(ctx, weights, x_host: dict, layers: int = 9, threads: int = 1) 
                       "engine/src/lib.rs:240-266"}
 
 
+def _time_full(fn, reps: int = 3) -> float:
+    """Median seconds of `reps` timed calls after one untimed one
+    (engine/src/model.rs:259-264: warm-ups dropped, median kept)."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_full_shapes(ctx, thread_counts) -> dict:
+    """Whole shapes on the host, no sampling: the single 6144 x 2048 GEMV of
+    the CPU reference case (weight seed 0, x seed 1, y f32 [1, 6144]) and
+    every Qwen3-1.7B projection at M = 1 (the 1.7B step's first-layer weights,
+    seeds 2000..2006, and its lm_head, seed 2196; x bf16 N(0, 1) from seed 1),
+    each timed in full, 1 thread and every thread of the lease; the 1.7B step
+    is 28 x the layer's seven projections + lm_head. us per call and GB/s of
+    algorithmic bytes (bf16 x as the GPU reads it; the oracle takes it as f32,
+    as the reference's CPU path does)."""
+    oracle = _oracle()
+    jobs = [("config1_6144x2048", 6144, 2048, 0)]
+    jobs += [(f"1p7b_{name}", n, k, 2000 + j) for j, (name, n, k) in enumerate(LAYER_1P7B)]
+    jobs.append(("1p7b_lm_head", LM_HEAD_1P7B[1], LM_HEAD_1P7B[2], 2000 + LAYERS_1P7B * len(LAYER_1P7B)))
+    xs = {k: oracle.bf16_to_f32(oracle.synth_bf16(1, 1.0, k)).reshape(1, k) for k in {k for _, _, k, _ in jobs}}
+    out = {f"threads_{t}": {} for t in thread_counts}
+    for label, n, k, seed in jobs:
+        w = ctx.synth_weight(seed, n, k, 0.02)
+        packed, scales = ctx.download_weight(w)
+        w.release()
+        p, sc = packed.reshape(-1), scales.reshape(-1)
+        for t in thread_counts:
+            sec = _time_full(lambda: oracle.matmul_rows(xs[k], p, sc, 0, n, threads=t))
+            out[f"threads_{t}"][label] = [round(sec * 1e6, 1), round(gemv_bytes(1, n, k) / sec / 1e9, 3)]
+    step_bytes = LAYERS_1P7B * sum(gemv_bytes(1, n, k) for _, n, k in LAYER_1P7B) + \
+        gemv_bytes(1, LM_HEAD_1P7B[1], LM_HEAD_1P7B[2])
+    for t in thread_counts:
+        row = out[f"threads_{t}"]
+        us = LAYERS_1P7B * sum(row[f"1p7b_{name}"][0] for name, _, _ in LAYER_1P7B) + row["1p7b_lm_head"][0]
+        row["1p7b_step_28_layers"] = [round(us, 1), round(step_bytes / (us * 1e-6) / 1e9, 3)]
+    out["cols"] = ["us per call (median of 3 after 1 untimed)", "GB/s"]
+    return out
+
+
 def _rows_for(work_macs: float, per_row_macs: int, n: int) -> int:
     return int(min(n, max(16, -(-int(work_macs) // per_row_macs))))
 
@@ -652,10 +798,9 @@ def cpu_verify(ctx, weights, threads: int) -> dict:
             oracle.matmul_rows(x, packed.reshape(-1), scales.reshape(-1), 0, r, threads=threads)
             t = time.perf_counter() - t0
             us = t * n / r * 1e6
-            row[f"M{m}"] = {"rows": r, "us_per_call": round(us, 1),
-                            "GBps": round(gemv_bytes(m, n, k) / (us * 1e-6) / 1e9, 4)}
+            row[f"M{m}"] = [r, round(us, 1), round(gemv_bytes(m, n, k) / (us * 1e-6) / 1e9, 4)]
         out[name] = row
-    return {"threads": threads, "shapes": out,
+    return {"threads": threads, "shapes": out, "cols": ["rows R", "us_per_call", "GBps"],
             "method": "oracle over the first R of N weight rows (all M token rows), us_per_call = time * N / R"}
 
 
@@ -1176,6 +1321,7 @@ def main() -> int:
         log("skinny (speculative verify) timing")
         extra["skinny"] = time_skinny(ctx)
 
+    prefill_top = None
     if not args.no_prefill:
         log("matrix-core ceiling (scaled FP4 MFMAs back to back) and prefill (M=512, block-scaled MFMA) timing")
         extra["mfma_ceiling"] = time_mfma_ceiling(ctx)
@@ -1183,6 +1329,7 @@ def main() -> int:
                 for act, key in (("mxfp4", "32x32x64"), ("mxfp8", "fp8xfp4_32x32x64"), ("bf16", "bf16_32x32x16"))}
         extra["prefill"] = time_prefill(ctx, ceiling=ceil)
         extra["prefill_layer"] = time_prefill_layer(ctx, weights)
+        prefill_top = prefill_summary(extra["prefill"], extra["prefill_layer"], ceil)
         log("exact matrix-core path for M > 32 (AUTO)")
         extra["prefill_exact_auto"] = time_prefill_exact(ctx, ceiling=ceil["bf16"])
 
@@ -1212,6 +1359,9 @@ def main() -> int:
         if nt > 1:
             cpu_extra["verify_all_threads"] = cpu_verify(ctx, weights, nt)
             cpu_extra["prefill_all_threads"] = cpu_prefill(ctx, weights, nt)
+        log("cpu legs: whole shapes (the single 6144 x 2048 GEMV, every Qwen3-1.7B M = 1 projection)")
+        # last in the line, so that the end of the printed line carries it whole
+        cpu_extra["full_shapes"] = cpu_full_shapes(ctx, [1] + ([nt] if nt > 1 else []))
         extra["cpu"] = cpu_extra
 
     traffic, traffic_note = (None, "--separate launches differ from the profiled step") if args.separate \
@@ -1239,6 +1389,7 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,
                      "basis": "algorithmic bytes of one decode step / GPU event time of one step"},
         "cpu_baseline": cpu,
+        "prefill": prefill_top,
         "extra": extra,
     }
     print(json.dumps(out), flush=True)

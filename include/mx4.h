@@ -108,10 +108,21 @@ void qwen_hip_set_cache_limit(void *context, uint64_t bytes);
  * must stay ordered: after mx4_set_stream, work still queued on the previous
  * stream must finish before the new stream runs more. */
 mx4_status mx4_create(int device, mx4_context **out);
+/* Waits for the context's stream, then frees everything it holds. Weight
+ * handles made on it (mx4_weight_upload*, mx4_weight_wrap) stay valid as
+ * handles but are detached: their device memory is freed here, every entry
+ * point given one fails with MX4_ERR_ARGUMENT ("the weight's context was
+ * destroyed"), and mx4_weight_release then only deletes the handle. Passes
+ * are detached the same way (mx4_pass_release). Either order of releasing
+ * weights and destroying their context is therefore safe. */
 void mx4_destroy(mx4_context *ctx);
 const char *mx4_last_error(void);
 /* Number of gfx950 devices visible (0 without a GPU; never fails). */
 int mx4_device_count(void);
+/* Compute units of the context's device (the launch shapes are sized by it;
+ * 256 on a full MI355X, fewer on a partitioned one). No counterpart in the
+ * reference (Metal sizes its grids by the matrix alone). */
+mx4_status mx4_compute_units(const mx4_context *ctx, int *cus);
 
 /* Enqueue on a caller stream (a hipStream_t) instead of the context's own;
  * NULL restores the context stream. */
@@ -147,6 +158,8 @@ mx4_status mx4_weight_upload_bf16(mx4_context *ctx, const uint16_t *data, uint32
  * scale bytes are scanned on device; a 255 byte fails with MX4_ERR_NAN_SCALE. */
 mx4_status mx4_weight_wrap(mx4_context *ctx, const uint8_t *packed_dev, const uint8_t *scales_dev,
                            uint32_t rows, uint32_t cols, mx4_weight **out);
+/* Frees the weight's device memory (the library's, not a wrapped caller's)
+ * and its handle; after mx4_destroy of its context, only the handle. */
 void mx4_weight_release(mx4_weight *w);
 mx4_status mx4_weight_info(const mx4_weight *w, uint32_t *rows, uint32_t *cols,
                            const uint8_t **packed_dev, const uint8_t **scales_dev);

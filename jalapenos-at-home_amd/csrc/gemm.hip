@@ -35,18 +35,17 @@ namespace mx4 {
 
 namespace {
 
-// Three bf16 terms of eight f32 values, hi + mid + lo = x exactly.
+// Three bf16 terms of eight f32 values, hi + mid + lo = x exactly
+// (split3_bf16: non-finite values stay in hi).
 __device__ __forceinline__ void split3x8(const f32x4 a, const f32x4 b, bf16x8& hi, bf16x8& mid, bf16x8& lo) {
     const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const __bf16 h = (__bf16)v[e];
-        const float r1 = v[e] - (float)h;
-        const __bf16 md = (__bf16)r1;
-        const float r2 = r1 - (float)md;
+        __bf16 h, md, l;
+        split3_bf16(v[e], h, md, l);
         hi[e] = h;
         mid[e] = md;
-        lo[e] = (__bf16)r2;
+        lo[e] = l;
     }
 }
 

@@ -43,6 +43,27 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t row) {
 
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+// An f32 activation as three bf16 terms, hi + mid + lo == x, for exact
+// products on the bf16 matrix cores. Each term is cut from the bits
+// (truncation, never rounding up): hi keeps the top 8 significant bits of x,
+// mid the top 8 of the remainder, lo what is left (at most 8 bits, exact),
+// so no finite x yields an infinite term (rounding to nearest would turn
+// |x| >= 0x7F7F8000 into a bf16 inf and the remainder into inf - inf = NaN).
+// A non-finite x stays in hi (a NaN keeps its quiet bit in the upper half)
+// with mid = lo = 0, so its products are the f32 products of the reference's
+// loop: +-inf, or NaN against a zero weight.
+__device__ __forceinline__ void split3_bf16(float v, __bf16& hi, __bf16& mid, __bf16& lo) {
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t hb = (u & 0xFFFF0000u) | (v != v ? 0x00400000u : 0u);
+    float r1 = v - __uint_as_float(hb);  // NaN exactly when x is not finite
+    r1 = r1 == r1 ? r1 : 0.0f;
+    const uint32_t mb = __float_as_uint(r1) & 0xFFFF0000u;
+    const float r2 = r1 - __uint_as_float(mb);
+    hi = __builtin_bit_cast(__bf16, (uint16_t)(hb >> 16));
+    mid = __builtin_bit_cast(__bf16, (uint16_t)(mb >> 16));
+    lo = (__bf16)r2;
+}
+
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t m) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {

@@ -134,6 +134,10 @@ struct mx4_context {
     // is retired (freed when the last pass is released) instead of freed
     std::unordered_set<mx4_pass*> passes;
     std::vector<void*> retired;
+    // every weight handle made on this context and not yet released: the
+    // handles belong to the caller, so mx4_destroy frees their device memory
+    // and detaches them (ctx = null) instead of leaving them pointing here
+    std::unordered_set<mx4_weight*> weights;
 };
 
 // Workspace of mx4_matmul_prefill_noalloc: the requantized activations in
@@ -304,6 +308,7 @@ mx4_status check_matmul_args(mx4_context* ctx, const void* x, mx4_dtype xt, uint
     if (m == 0) return fail(MX4_ERR_ARGUMENT, "m must be at least 1");
     if (((uintptr_t)x & 15) != 0) return fail(MX4_ERR_ARGUMENT, "x must be 16-byte aligned");
     if (((uintptr_t)y & 3) != 0) return fail(MX4_ERR_ARGUMENT, "y must be 4-byte aligned");
+    if (!w->ctx) return fail(MX4_ERR_ARGUMENT, "the weight's context was destroyed");
     if (w->ctx != ctx) return fail(MX4_ERR_ARGUMENT, "weight belongs to another context");
     return MX4_OK;
 }
@@ -389,6 +394,10 @@ mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
 mx4_status new_weight(mx4_context* ctx, uint32_t rows, uint32_t cols, mx4_weight** out) {
     mx4_weight* w = new (std::nothrow) mx4_weight{};
     if (!w) return fail(MX4_ERR_NO_MEMORY, "out of host memory");
+    if (!ctx->weights.insert(w).second) {
+        delete w;
+        return fail(MX4_ERR_NO_MEMORY, "out of host memory");
+    }
     w->ctx = ctx;
     w->rows = rows;
     w->cols = cols;
@@ -422,6 +431,12 @@ int mx4_device_count(void) {
     int c = 0;
     for (int i = 0; i < n; ++i) c += is_gfx950(i) ? 1 : 0;
     return c;
+}
+
+mx4_status mx4_compute_units(const mx4_context* ctx, int* cus) {
+    if (!ctx || !cus) return fail(MX4_ERR_ARGUMENT, "null argument");
+    *cus = ctx->cus;
+    return MX4_OK;
 }
 
 mx4_status mx4_validate(uint64_t rows, uint64_t cols, uint64_t packed_len, const uint8_t* scales,
@@ -480,6 +495,19 @@ void mx4_destroy(mx4_context* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (auto& kv : ctx->cache) mx4_weight_release(kv.second.w);
     ctx->cache.clear();
+    // the caller's weights outlive the context as empty handles: their device
+    // memory goes now, and a later mx4_weight_release only deletes the handle
+    for (mx4_weight* w : ctx->weights) {
+        if (w->allocation) (void)hipFree(w->allocation);
+        if (w->frag) (void)hipFree(w->frag);
+        w->ctx = nullptr;
+        w->allocation = nullptr;
+        w->frag = w->frag_scales = nullptr;
+        w->packed = w->scales = nullptr;
+        w->bf16 = nullptr;
+        w->stored = false;
+    }
+    ctx->weights.clear();
     for (mx4_pass* p : ctx->passes) p->ctx = nullptr;
     for (void* b : ctx->retired) (void)hipFree(b);
     if (ctx->x_stage) (void)hipFree(ctx->x_stage);
@@ -630,17 +658,22 @@ mx4_status mx4_weight_wrap(mx4_context* ctx, const uint8_t* packed_dev, const ui
 
 void mx4_weight_release(mx4_weight* w) {
     if (!w) return;
-    if (w->allocation || w->frag) {
-        DeviceGuard g(w->ctx->device);
-        (void)hipStreamSynchronize(w->ctx->stream);
-        if (w->allocation) (void)hipFree(w->allocation);
-        if (w->frag) (void)hipFree(w->frag);
+    // a weight whose context was destroyed holds no device memory any more
+    if (w->ctx) {
+        if (w->allocation || w->frag) {
+            DeviceGuard g(w->ctx->device);
+            (void)hipStreamSynchronize(w->ctx->stream);
+            if (w->allocation) (void)hipFree(w->allocation);
+            if (w->frag) (void)hipFree(w->frag);
+        }
+        w->ctx->weights.erase(w);
     }
     delete w;
 }
 
 mx4_status mx4_weight_prepare_prefill(mx4_weight* w) {
     if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
+    if (!w->ctx) return fail(MX4_ERR_ARGUMENT, "the weight's context was destroyed");
     DeviceGuard g(w->ctx->device);
     return prepare_fragments(w->ctx, w);
 }
@@ -675,6 +708,7 @@ mx4_status mx4_weight_upload_bf16(mx4_context* ctx, const uint16_t* data, uint32
 mx4_status mx4_weight_info(const mx4_weight* w, uint32_t* rows, uint32_t* cols, const uint8_t** packed_dev,
                            const uint8_t** scales_dev) {
     if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
+    if (!w->ctx) return fail(MX4_ERR_ARGUMENT, "the weight's context was destroyed");
     if (rows) *rows = w->rows;
     if (cols) *cols = w->cols;
     if (packed_dev) *packed_dev = w->stored ? w->packed : nullptr;
@@ -684,6 +718,7 @@ mx4_status mx4_weight_info(const mx4_weight* w, uint32_t* rows, uint32_t* cols, 
 
 mx4_status mx4_weight_footprint(const mx4_weight* w, uint64_t* stored_bytes, uint64_t* matrix_core_bytes) {
     if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
+    if (!w->ctx) return fail(MX4_ERR_ARGUMENT, "the weight's context was destroyed");
     const uint64_t e = (uint64_t)w->rows * w->cols;
     if (stored_bytes) *stored_bytes = !w->stored ? 0 : (w->bf16 ? e * 2 : e / 2 + e / 32);
     if (matrix_core_bytes)
@@ -695,6 +730,7 @@ mx4_status mx4_weight_footprint(const mx4_weight* w, uint64_t* stored_bytes, uin
 
 mx4_status mx4_weight_release_prefill(mx4_weight* w) {
     if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
+    if (!w->ctx) return fail(MX4_ERR_ARGUMENT, "the weight's context was destroyed");
     if (!w->frag) return MX4_OK;
     if (!w->stored) return fail(MX4_ERR_UNSUPPORTED, "the matrix-core copy is the weight's only layout");
     if (!w->ctx->passes.empty())
@@ -709,6 +745,7 @@ mx4_status mx4_weight_release_prefill(mx4_weight* w) {
 
 mx4_status mx4_weight_drop_stored(mx4_weight* w) {
     if (!w) return fail(MX4_ERR_ARGUMENT, "null weight");
+    if (!w->ctx) return fail(MX4_ERR_ARGUMENT, "the weight's context was destroyed");
     if (!w->stored) return MX4_OK;
     if (w->bf16) return fail(MX4_ERR_UNSUPPORTED, "a bf16 weight has no matrix-core copy");
     if (!w->allocation) return fail(MX4_ERR_UNSUPPORTED, "a wrapped weight's memory belongs to the caller");
@@ -1401,15 +1438,21 @@ bool qwen_hip_matmul(void* context, const float* x, const void* w, const uint8_t
     if (ensure_pinned(ctx, &ctx->x_pin, &ctx->x_pin_cap, xbytes) != MX4_OK) return false;
     if (ensure_pinned(ctx, &ctx->y_pin, &ctx->y_pin_cap, ybytes) != MX4_OK) return false;
     std::memcpy(ctx->x_pin, x, xbytes);
+    // From here on every exit waits for the stream: the next call writes (or
+    // ensure_pinned frees) x_pin, which an upload still in flight would read.
     if (hipMemcpyAsync(ctx->x_stage, ctx->x_pin, xbytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess) {
         fail(MX4_ERR_DEVICE, "input upload failed");
+        (void)hipStreamSynchronize(ctx->stream);
         return false;
     }
     if (run_matmul(ctx, ctx->x_stage, MX4_F32, rows, weight, static_cast<float*>(ctx->y_stage), MX4_PATH_AUTO) !=
-        MX4_OK)
+        MX4_OK) {
+        (void)hipStreamSynchronize(ctx->stream);
         return false;
-    if (hipMemcpyAsync(ctx->y_pin, ctx->y_stage, ybytes, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess ||
-        hipStreamSynchronize(ctx->stream) != hipSuccess) {
+    }
+    const hipError_t ce = hipMemcpyAsync(ctx->y_pin, ctx->y_stage, ybytes, hipMemcpyDeviceToHost, ctx->stream);
+    const hipError_t se = hipStreamSynchronize(ctx->stream);
+    if (ce != hipSuccess || se != hipSuccess) {
         fail(MX4_ERR_DEVICE, "matmul or copy-back failed");
         return false;
     }

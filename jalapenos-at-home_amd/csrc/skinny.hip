@@ -84,18 +84,17 @@ __device__ __forceinline__ void mfma_drain() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// f32 -> three bf16 terms with x = hi + mid + lo to within f32 rounding.
+// f32 -> three bf16 terms with x = hi + mid + lo exactly (split3_bf16:
+// non-finite values stay in hi).
 __device__ __forceinline__ void split3(const f32x4 a, const f32x4 b, bf16x8& hi, bf16x8& mid, bf16x8& lo) {
-    float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        __bf16 h = (__bf16)v[e];
-        float r1 = v[e] - (float)h;
-        __bf16 m = (__bf16)r1;
-        float r2 = r1 - (float)m;
+        __bf16 h, m, l;
+        split3_bf16(v[e], h, m, l);
         hi[e] = h;
         mid[e] = m;
-        lo[e] = (__bf16)r2;
+        lo[e] = l;
     }
 }
 

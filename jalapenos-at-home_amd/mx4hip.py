@@ -46,6 +46,7 @@ SIGNATURES = {
     "mx4_destroy": (None, [_vp]),
     "mx4_last_error": (ctypes.c_char_p, []),
     "mx4_device_count": (_int, []),
+    "mx4_compute_units": (_int, [_vp, ctypes.POINTER(_int)]),
     "mx4_set_stream": (_int, [_vp, _vp]),
     "mx4_get_stream": (_vp, [_vp]),
     "mx4_synchronize": (_int, [_vp]),
@@ -234,8 +235,9 @@ class Weight:
         check(lib().mx4_weight_drop_stored(self.handle))
 
     def release(self) -> None:
-        # a weight never outlives its context (release after destroy is a use-after-free)
-        if self.handle and self.ctx.handle:
+        # after mx4_destroy of its context the handle is detached (its device
+        # memory already freed) and releasing it only deletes the handle
+        if self.handle:
             lib().mx4_weight_release(self.handle)
         self.handle = None
 
@@ -465,6 +467,11 @@ class Context:
         out = self.buffer(256 * 16 * 4)
         check(lib().mx4_decode_table(self.handle, mode, out.ptr))
         return out.download(np.float32).reshape(256, 16)
+
+    def compute_units(self) -> int:
+        n = ctypes.c_int()
+        check(lib().mx4_compute_units(self.handle, ctypes.byref(n)))
+        return n.value
 
     def mfma_ceiling(self, shape: int, random_codes: bool) -> "tuple[float, float]":
         """Matrix-core ceiling probe: (PFLOP/s, median shader clock in GHz) of

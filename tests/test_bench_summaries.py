@@ -134,3 +134,48 @@ def test_prefill_compare_groups_dispatches_by_plan(tmp_path):
     out = _run("prefill-compare", d)
     assert "| gate | register-direct | 1024 |" in out  # two rows of 512 per dispatch
     assert "| gate | shared | 150 |" in out           # mean of 100 and 200
+
+
+def test_prefill_summary_is_compact_and_reads_the_stamped_counters(tmp_path, monkeypatch):
+    """The top-level `prefill` object of the JSON line: every 8B shape and
+    activation format in one row, the grouped layer, the largest
+    requantization error, and the MFMA counters of the dominant instances
+    taken from the profile only when its stamp names the loaded library; the
+    whole object stays under 1.5 KB so a record keeping top-level keys keeps it."""
+    prof = tmp_path / "prefill.md"
+    prof.write_text(
+        "commit: x\nlibrary_sha256: 1234\n\n"
+        "| shape | act | kernel instance | dispatches | us | TFLOP/s | of peak | MOPS x 512 | MFMA busy |\n"
+        "|---|---|---|---|---|---|---|---|---|\n"
+        "| gate 512x4096->12288 | mxfp4 | prefill_kernel<false, 4, 3, 1, 4, 2, 2, 32> | 10 | 18.38 | 2804 | 27.8% "
+        "| 5.154e+10 (1.000 x 2MNK) | 27.9% |\n"
+        "| gate 512x4096->12288 | exact bf16 | gemm_exact_kernel<true, 2, 2, 2, 3, 3> | 5 | 54.35 | 948 | 37.9% "
+        "| 5.154e+10 (1.000 x 2MNK) | 37.7% |\n")
+    monkeypatch.setattr(bench, "PREFILL_PROFILE", prof)
+    monkeypatch.setattr(bench, "library_sha256", lambda: "1234")
+    c = bench.prefill_counters()
+    assert c["gate mxfp4"] == ["prefill_kernel<false,4,3,1,4,2,2,32>", 18.38, 1.0, 0.279]
+    assert "gate exact" not in c
+    monkeypatch.setattr(bench, "library_sha256", lambda: "9999")
+    assert "!=" in bench.prefill_counters()["note"]
+
+    def entry(us, tf):
+        return {"us": us, "TFLOPs": tf, "frac": round(tf / 10100, 4), "frac_of_measured_ceiling": 0.3}
+    err = {"max_rel": 1.2e-2, "rel_l2": 8.1e-3}
+    pf = {name: {"mxfp4": {"gemm": entry(18.123, 2843.4), "requant+gemm": entry(24.5, 2100.0)},
+                 "mxfp8": {"gemm": entry(23.3, 2211.0), "requant+gemm": entry(29.0, 1777.0)},
+                 "requant_error": {"mxfp4": err, "mxfp8": {"max_rel": 2e-3, "rel_l2": 1e-3},
+                                   "exact_auto": {"max_rel": 3e-7, "rel_l2": 1e-7}}}
+          for name in ("q", "o", "gate", "up", "down")}
+    layer = {a: {"grouped": {"us": 108.1, "frac": 0.181}} for a in ("mxfp4", "mxfp8")}
+    monkeypatch.setattr(bench, "library_sha256", lambda: "1234")
+    for key in ("down mxfp4", "gate mxfp8", "q mxfp4"):  # two more rows the summary keeps, one it drops
+        shape, act = key.split()
+        with open(prof, "a") as f:
+            f.write(f"| {shape} 512x4096->4096 | {act} | prefill_lds_kernel<false, 2, 2, 2, 1, 2, 4, 2> | 10 | 11.36 "
+                    "| 1513 | 15.0% | 1.718e+10 (1.000 x 2MNK) | 15.0% |\n")
+    top = bench.prefill_summary(pf, layer, {"mxfp4": 6560.4, "mxfp8": 4120.0, "bf16": 1680.0})
+    assert sorted(top["counters"]) == ["cols", "down mxfp4", "gate mxfp4", "gate mxfp8", "stamp"]
+    assert top["mxfp4"]["gate"] == [18.123, 2843, 0.2815, 0.3, 24.5, 2100, 0.2079]
+    assert top["requant_error_vs_unquantized"]["mxfp4"]["max_rel"] == 1.2e-2
+    assert len(json.dumps(top)) < 1500

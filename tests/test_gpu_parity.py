@@ -636,6 +636,63 @@ def test_errors_are_reported_not_launched(mx4, ctx):
         ctx.upload_weight(np.zeros(16, np.uint8), np.array([127], np.uint8), 1, 31)
 
 
+def test_weights_outlive_their_context(mx4, oracle):
+    """mx4_destroy detaches the caller's weight handles (the Rust Tensor owns
+    its GpuTensor, engine/src/gpu.rs:225-237, and may drop it after the
+    backend): their device memory is freed with the context, every entry point
+    then refuses them, and mx4_weight_release afterwards frees only the handle.
+    Covers an uploaded weight with its matrix-core copy, a bf16 weight and a
+    wrapped one; a fresh context on the same device works as before."""
+    import ctypes
+
+    L = mx4.lib()
+    n, k = 64, 256
+    rng = np.random.default_rng(31)
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(120, 130, (n, k // 32), dtype=np.uint8)
+    h = ctypes.c_void_p()
+    mx4.check(L.mx4_create(0, ctypes.byref(h)))
+    dead = h.value
+    ws = []
+    w = ctypes.c_void_p()
+    mx4.check(L.mx4_weight_upload(dead, packed.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)),
+                                  scales.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), n, k, ctypes.byref(w)))
+    ws.append(w.value)
+    mx4.check(L.mx4_weight_prepare_prefill(w.value))
+    bits = rng.integers(0, 1 << 15, (n, k), dtype=np.uint16)
+    wb = ctypes.c_void_p()
+    mx4.check(L.mx4_weight_upload_bf16(dead, bits.ctypes.data, n, k, ctypes.byref(wb)))
+    ws.append(wb.value)
+    mem = ctypes.c_void_p()
+    mx4.check(L.mx4_malloc(dead, n * k // 2 + 256 + n * k // 32, ctypes.byref(mem)))
+    mx4.check(L.mx4_upload(dead, mem, packed.ctypes.data, n * k // 2))
+    mx4.check(L.mx4_upload(dead, ctypes.c_void_p(mem.value + n * k // 2 + 256), scales.ctypes.data, n * k // 32))
+    ww = ctypes.c_void_p()
+    mx4.check(L.mx4_weight_wrap(dead, mem, ctypes.c_void_p(mem.value + n * k // 2 + 256), n, k, ctypes.byref(ww)))
+    ws.append(ww.value)
+    mx4.check(L.mx4_synchronize(dead))
+    mx4.check(L.mx4_free(dead, mem))  # the wrapped weight's memory is the caller's
+    L.mx4_destroy(dead)
+    with mx4.Context(0) as fresh:
+        x = fresh.to_device(np.ones(k, np.float32))
+        y = fresh.buffer(n * 4)
+        for i, wh in enumerate(ws):
+            rows = ctypes.c_uint32()
+            st = L.mx4_weight_info(wh, ctypes.byref(rows), None, None, None)
+            assert st == 1 and "destroyed" in L.mx4_last_error().decode(), f"weight {i}: info after destroy"
+            st = L.mx4_matmul(fresh.handle, x.ptr, mx4.F32, 1, wh, y.ptr)
+            assert st == 1 and "destroyed" in L.mx4_last_error().decode(), f"weight {i}: matmul after destroy"
+            assert L.mx4_weight_prepare_prefill(wh) == 1
+        for wh in ws:
+            L.mx4_weight_release(wh)  # frees the handle only
+        # the device is unaffected: a new weight on the fresh context multiplies correctly
+        w2 = fresh.upload_weight(packed, scales, n, k)
+        xv = oracle.bf16_to_f32(oracle.synth_bf16(32, 1.0, k)).reshape(1, k)
+        got = run_matmul(mx4, fresh, xv, w2, mx4.PATH_AUTO)
+        assert_close(got, oracle.matmul(xv, packed.reshape(-1), scales.reshape(-1)), "weight after destroy cycle")
+        w2.release()
+
+
 # ------------------------------------------------------------------ kernel configurations
 
 CONFIG_SHAPES = [(1000, 2048), (1000, 4096), (700, 6144), (999, 8192), (700, 12288)]
@@ -764,6 +821,44 @@ def test_extreme_scales_take_the_exact_path(mx4, ctx, oracle):
     assert np.array_equal(np.isnan(y3), np.isnan(ref3)) and np.array_equal(np.isinf(y3), np.isinf(ref3))
     fin = np.isfinite(ref3)
     assert_close(y3[fin].reshape(1, -1), ref3[fin].reshape(1, -1), "finite rows next to inf rows", scaled=True)
+
+
+@pytest.mark.parametrize("path,m", [("GEMV", 1), ("SKINNY", 8), ("GEMM", 40), ("AUTO", 40)])
+def test_f32_activations_inf_nan_and_huge(mx4, ctx, oracle, path, m):
+    """f32 token rows holding +inf, -inf, NaN or a huge finite value
+    (3.4e38, above the point where rounding to bf16 would give inf), through
+    the exact f32-activation paths (the GEMV's f32 FMA, and the bf16 matrix
+    cores with x split into three bf16 terms in the skinny kernel and the
+    GEMM). The reference's f32 loop (engine/src/lib.rs:240-266) gives +-inf
+    where the weight is nonzero and NaN where it is zero (inf * 0), NaN for a
+    NaN row, and finite sums for the huge row: the NaN/inf pattern must be the
+    oracle's exactly, and every finite row within the usual bars."""
+    rng = np.random.default_rng(17 + m)
+    n, k = 256, 4096
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(118, 125, (n, k // 32), dtype=np.uint8)  # |w| <= 0.75: huge * w stays finite
+    w = ctx.upload_weight(packed, scales, n, k)
+    cases = [("+inf", 5, np.inf), ("-inf", 9, -np.inf), ("nan", 11, np.nan), ("huge", 7, np.float32(3.4e38))]
+    # several token rows: one special row each, in a single call; one row: a call per case
+    plans = [dict(enumerate(cases))] if m >= len(cases) else [{0: c} for c in cases]
+    for pi, special in enumerate(plans):
+        x = oracle.bf16_to_f32(oracle.synth_bf16(18 + pi, 1.0, m * k)).reshape(m, k).copy()
+        for row, (_, col, v) in special.items():
+            x[row, col] = v
+        ref = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
+        say(f"f32 non-finite activations path {path} m {m} plan {pi}")
+        y = run_matmul(mx4, ctx, x, w, getattr(mx4, f"PATH_{path}"), mx4.F32)
+        for row, (label, _, _) in special.items():
+            if label == "huge":
+                assert np.all(np.isfinite(ref[row])), "the huge row's reference must be finite"
+                assert_close(y[row:row + 1], ref[row:row + 1], f"{path} huge finite row", scaled=True)
+            else:
+                assert np.array_equal(np.isnan(y[row]), np.isnan(ref[row])), f"{path} {label} row: NaN pattern"
+                assert np.array_equal(np.isposinf(y[row]), np.isposinf(ref[row])), f"{path} {label}: +inf pattern"
+                assert np.array_equal(np.isneginf(y[row]), np.isneginf(ref[row])), f"{path} {label}: -inf pattern"
+        plain = [r for r in range(m) if r not in special]
+        if plain:
+            assert_close(y[plain], ref[plain], f"{path} finite rows next to non-finite ones")
 
 
 # ------------------------------------------------------------------ skinny (speculative verify)

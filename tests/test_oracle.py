@@ -321,6 +321,19 @@ def test_argmax_first_maximum(oracle):
 
 # ---------------------------------------------------------------- generator
 
+def test_splitmix64_published_outputs():
+    """The generator's u64 stream is SplitMix64 (Steele, Lea, Flood 2014;
+    Vigna's splitmix64.c): output n of seed s is the finaliser of
+    s + (n + 1) * 0x9E3779B97F4A7C15. Pinned to published sequences: seed 0
+    (the first outputs of splitmix64.c with x = 0) and seed 1234567 (the
+    Rosetta Code "Pseudo-random numbers/Splitmix64" task's five values)."""
+    from oracle import mx4_oracle as o
+
+    assert [o.splitmix64(0, i) for i in range(3)] == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+    assert [o.splitmix64(1234567, i) for i in range(5)] == [
+        6457827717110365317, 3203168211198807973, 9817491932198370423, 4593380528125082431, 16408922859458223821]
+
+
 def test_generator_ln_and_cos_match_libm():
     from oracle import mx4_oracle as o
 
