@@ -735,6 +735,88 @@ def test_gemv_every_configuration(mx4, ctx, oracle, n, k):
     assert tried >= 64
 
 
+def test_gemv_writes_every_row_each_launch(mx4, ctx, oracle):
+    """Every M = 1 GEMV launch writes every row of y, whatever its launch shape:
+    the 8B q|k|v and gate|up groups and o, the 1.7B o and k, and explicit
+    configurations (fewer teams than rows, several rows per team, several
+    teams per workgroup, the last workgroup partly empty) run interleaved, 12
+    rounds eagerly and then 4 replays of one recorded pass, each into a y first
+    overwritten with NaN. Every launch must leave no NaN, equal the first
+    launch bit for bit, and that result is the oracle's."""
+    import ctypes
+
+    L = mx4.lib()
+    rng = np.random.default_rng(47)
+    specs = [("8B q|k|v", [(4096, 4096), (1024, 4096), (1024, 4096)], None),
+             ("8B o", [(4096, 4096)], None),
+             ("8B gate|up", [(12288, 4096), (12288, 4096)], None),
+             ("1.7B o", [(2048, 2048)], None),
+             ("1.7B k", [(1024, 2048)], None),
+             ("33 teams of 1 row", [(1000, 4096)], (1, 1, 33, 1)),
+             ("100 teams of 4 rows, 2 per workgroup", [(3001, 2048)], (1, 4, 100, 2)),
+             ("8 teams per workgroup, 2 rows", [(5000, 2048)], (1, 2, 600, 8))]
+    cases = []
+    seed = 700
+    for name, dims, cfg in specs:
+        k = dims[0][1]
+        ws = []
+        for n, _ in dims:
+            ws.append(ctx.synth_weight(seed, n, k, 0.02))
+            seed += 1
+        xv = oracle.bf16_to_f32(oracle.synth_bf16(seed, 1.0, k)).reshape(1, k)
+        xb = ctx.to_device((f32_bits(xv) >> 16).astype(np.uint16))
+        ys = [ctx.buffer(n * 4) for n, _ in dims]
+        nans = [ctx.to_device(np.full(n, np.nan, np.float32)) for n, _ in dims]
+        refs = []
+        for w, (n, _) in zip(ws, dims):
+            packed, scales = ctx.download_weight(w)
+            refs.append(oracle.matmul_rows(xv, packed.reshape(-1), scales.reshape(-1), 0, n, threads=8))
+        cases.append((name, ws, xb, ys, nans, refs, cfg))
+
+    def enqueue(case):
+        name, ws, xb, ys, nans, refs, cfg = case
+        for y, nan in zip(ys, nans):
+            mx4.check(L.mx4_copy(ctx.handle, ctypes.c_void_p(y.ptr), ctypes.c_void_p(nan.ptr), y.nbytes))
+        if cfg is not None:
+            ctx.gemv_config(xb.ptr, mx4.BF16, ws, [y.ptr for y in ys], team=cfg[0], rows=cfg[1], teams=cfg[2],
+                            tpw=cfg[3])
+        elif len(ws) == 1:
+            ctx.matmul_ptr(xb.ptr, mx4.BF16, 1, ws[0], ys[0].ptr)
+        else:
+            ctx.matmul_group(xb.ptr, mx4.BF16, 1, ws, [y.ptr for y in ys])
+
+    first = {}
+    for rnd in range(12):
+        order = list(range(len(cases)))
+        rng.shuffle(order)
+        for ci in order:
+            enqueue(cases[ci])
+            ctx.synchronize()
+            name, _, _, ys, _, refs, _ = cases[ci]
+            got = [y.download(np.float32) for y in ys]
+            for i, g in enumerate(got):
+                assert not np.any(np.isnan(g)), f"{name} round {rnd}: segment {i} has rows no team wrote"
+            if name not in first:
+                first[name] = got
+                for i, (g, r) in enumerate(zip(got, refs)):
+                    assert_close(g.reshape(1, -1), r, f"{name} segment {i}")
+            else:
+                for i, (g, f) in enumerate(zip(got, first[name])):
+                    assert np.array_equal(f32_bits(g), f32_bits(f)), f"{name} round {rnd}: segment {i} differs"
+    p = ctx.record(lambda: [enqueue(c) for c in cases])
+    for rep in range(4):
+        p.launch()
+        ctx.synchronize()
+        for name, _, _, ys, _, _, _ in cases:
+            for i, y in enumerate(ys):
+                assert np.array_equal(f32_bits(y.download(np.float32)), f32_bits(first[name][i])), \
+                    f"{name} replay {rep}: segment {i}"
+    p.release()
+    for c in cases:
+        for w in c[1]:
+            w.release()
+
+
 def test_group_equals_individual(mx4, ctx, oracle):
     """q|k|v and gate|up as one launch give bitwise the same rows as separate launches."""
     k = 4096
