@@ -354,9 +354,13 @@ mx4_status mx4_prefill_matmul_group(mx4_context *ctx, const uint8_t *codes_dev, 
  * of D, workgroup tiles 128 x 192, 128 x 128, 64 x 128, 128 x 64, 64 x 256,
  * 128 x 96, 64 x 192 and 64 x 64 (K % 256 == 0); with H = 2 the workgroup
  * has two sets of four waves, each over one half of K with its own ring,
- * whose tiles are summed in LDS at the end (K % 512 == 0). A ring that does
- * not fit the LDS is cut to the deepest that fits (except (4, 2)), and a
- * stage the waves cannot share evenly is not compiled.
+ * whose tiles are summed in LDS at the end (K % 512 == 0). Adding 256 to an
+ * H = 2 code (U, D = (4, 2), (4, 3), (2, 3) or (2, 4)) runs the two halves in
+ * ping-pong: each stage becomes an LDS-read phase and an MFMA phase, and the
+ * second half runs one phase behind the first, with the same arithmetic (the
+ * same output bits). A ring that does not fit the LDS is cut to the deepest
+ * that fits (except (4, 2)), and a stage the waves cannot share evenly is not
+ * compiled.
  * MX4_ERR_UNSUPPORTED when no compiled instance matches. tile_m == 0 keeps
  * the default choice. */
 mx4_status mx4_prefill_config(mx4_context *ctx, const uint8_t *codes_dev, const uint8_t *scales_dev,

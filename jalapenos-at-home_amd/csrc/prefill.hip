@@ -336,6 +336,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // runs two waves whose loads and MFMAs interleave; at the end the second
 // half's tile crosses LDS and the first half adds it (a fixed order, so
 // repeated calls agree bit for bit).
+// PP (ping-pong, KH = 2 only): every stage is split into a memory tick (the
+// stage's fragments from LDS into registers, the next loads issued) and a
+// matrix tick (its MFMAs), each opened by a workgroup barrier, and the second
+// K half runs one tick behind the first: on every SIMD one wave issues MFMAs
+// while the other reads LDS, instead of both competing for the same phase. The
+// arithmetic and its order are those of the KH = 2 kernel, so the outputs are
+// the same bits.
 template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D, int KH = 1>
 struct LdsGeo {
     static constexpr int NW = WM * WN, NT = 64 * NW * KH;  // waves per K part; threads
@@ -371,12 +378,13 @@ __device__ __forceinline__ void wait_ahead(uint32_t ahead) {
     }
 }
 
-template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D, int KH>
+template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D, int KH, bool PP>
 __global__ __launch_bounds__(64 * WM * WN * KH) void prefill_lds_kernel(const Segs segs, const uint8_t* __restrict__ xf,
                                                                        const uint8_t* __restrict__ xsf, uint32_t m,
                                                                        uint32_t k) {
     using G = LdsGeo<A_FP8, WM, WN, TM, TN, U, D, KH>;
     static_assert(G::ok, "instance outside the kernel's stage, vmcnt and LDS limits");
+    static_assert(!PP || KH == 2, "ping-pong alternates the two K halves");
     constexpr uint32_t AF = A_FP8 ? 2048 : 1024;
     constexpr int P = 4 / U;  // stages per scale quad
     __shared__ __attribute__((aligned(16))) uint8_t lds_all[G::LDS];
@@ -489,17 +497,92 @@ __global__ __launch_bounds__(64 * WM * WN * KH) void prefill_lds_kernel(const Se
 #pragma unroll
     for (int p = 0; p < D - 1; ++p)
         if ((uint32_t)p < stages) issue(p, p);
-    for (uint32_t st0 = 0; st0 < stages; st0 += P) {
+    if constexpr (!PP) {
+        for (uint32_t st0 = 0; st0 < stages; st0 += P) {
 #pragma unroll
-        for (int e = 0; e < P; ++e) {
-            const uint32_t st = st0 + e;
-            const uint32_t left = stages - 1 - st;
-            wait_ahead<G::LPS, D - 2>(left < (uint32_t)(D - 2) ? left : (uint32_t)(D - 2));
-            lds_barrier();
-            if (st + D - 1 < stages) issue(st + D - 1, (st + D - 1) % D);
-            if (e == 0) compute(st % D, std::integral_constant<int, 0>{});
-            else if constexpr (P > 1) compute(st % D, std::integral_constant<int, (P > 1 ? 1 : 0)>{});
+            for (int e = 0; e < P; ++e) {
+                const uint32_t st = st0 + e;
+                const uint32_t left = stages - 1 - st;
+                wait_ahead<G::LPS, D - 2>(left < (uint32_t)(D - 2) ? left : (uint32_t)(D - 2));
+                lds_barrier();
+                if (st + D - 1 < stages) issue(st + D - 1, (st + D - 1) % D);
+                if (e == 0) compute(st % D, std::integral_constant<int, 0>{});
+                else if constexpr (P > 1) compute(st % D, std::integral_constant<int, (P > 1 ? 1 : 0)>{});
+            }
         }
+    } else {
+        // the stage's operands and scale words, read in the memory tick
+        u32x4 ra[U][TM][A_FP8 ? 2 : 1], rb[U][TN];
+        uint32_t rsa[TM], rsb[TN];
+        auto read_stage = [&](uint32_t slot) {
+            const uint8_t* base = lds + slot * G::STAGE;
+            const uint8_t* sbase = base + G::A_BYTES + G::B_BYTES;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const uint32_t g = wm * TM + i;
+                rsa[i] = *reinterpret_cast<const uint32_t*>(sbase + (g / 4) * 1024 + (g % 4) * 256 + 4 * lane);
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const uint32_t g = wn * TN + j;
+                rsb[j] = *reinterpret_cast<const uint32_t*>(sbase + (G::SA + g / 4) * 1024 + (g % 4) * 256 + 4 * lane);
+            }
+#pragma unroll
+            for (int kk = 0; kk < U; ++kk) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const uint8_t* ap = base + (kk * G::GA + wm * TM + i) * AF + 16 * lane;
+                    ra[kk][i][0] = *reinterpret_cast<const u32x4*>(ap);
+                    if constexpr (A_FP8) ra[kk][i][1] = *reinterpret_cast<const u32x4*>(ap + 1024);
+                }
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    rb[kk][j] = *reinterpret_cast<const u32x4*>(base + G::A_BYTES + (kk * G::GB + wn * TN + j) * 1024 +
+                                                                16 * lane);
+            }
+        };
+        // a barrier the scheduler moves nothing across
+        auto tick = []() {
+            __builtin_amdgcn_sched_barrier(0);
+            lds_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // both halves pass 2 * stages + 1 barriers here: the second half's
+        // extra one comes first, the first half's last
+        if (kh == 1) tick();
+        for (uint32_t st0 = 0; st0 < stages; st0 += P) {
+#pragma unroll
+            for (int e = 0; e < P; ++e) {
+                const uint32_t st = st0 + e;
+                const uint32_t left = stages - 1 - st;
+                // memory tick: stage st has landed (every wave of this half
+                // waited for its own loads before the barrier); slot
+                // (st - 1) % D was read by all of them before the previous
+                // matrix tick's barrier, so the next loads may take it
+                wait_ahead<G::LPS, D - 2>(left < (uint32_t)(D - 2) ? left : (uint32_t)(D - 2));
+                tick();
+                read_stage(st % D);
+                if (st + D - 1 < stages) issue(st + D - 1, (st + D - 1) % D);
+                // matrix tick (the barrier waits for the LDS reads)
+                tick();
+#pragma unroll
+                for (int kk = 0; kk < U; ++kk) {
+                    switch (e * U + kk) {
+                        case 0: kstep<0, A_FP8, TM, TN>(ra[kk], rb[kk], rsa, rsb, acc); break;
+                        case 1: kstep<1, A_FP8, TM, TN>(ra[kk], rb[kk], rsa, rsb, acc); break;
+                        case 2: kstep<2, A_FP8, TM, TN>(ra[kk], rb[kk], rsa, rsb, acc); break;
+                        default: kstep<3, A_FP8, TM, TN>(ra[kk], rb[kk], rsa, rsb, acc); break;
+                    }
+                }
+                // the MFMAs stay in their tick (the compiler would otherwise
+                // sink them past the next memory tick's barrier)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(acc[i][j]));
+            }
+        }
+        if (kh == 0) tick();
     }
     mfma_drain();
 
@@ -630,7 +713,7 @@ constexpr int fit_depth() {
     else return fit_depth<A_FP8, WM, WN, TM, TN, U, D - 1, KH>();
 }
 
-template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D, int KH = 1>
+template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D, int KH = 1, bool PP = false>
 hipError_t go_lds(const PrefillArgs& a) {
     using G = LdsGeo<A_FP8, WM, WN, TM, TN, U, D, KH>;
     if constexpr (!G::ok) {
@@ -653,7 +736,7 @@ hipError_t go_lds(const PrefillArgs& a) {
             }
         }
         dim3 grid(cols, (a.m + G::BM - 1) / G::BM);
-        hipLaunchKernelGGL((prefill_lds_kernel<A_FP8, WM, WN, TM, TN, U, D, KH>), grid, dim3(G::NT), 0, a.stream,
+        hipLaunchKernelGGL((prefill_lds_kernel<A_FP8, WM, WN, TM, TN, U, D, KH, PP>), grid, dim3(G::NT), 0, a.stream,
                            sg, a.xf, a.xsf, a.m, a.k);
         return hipGetLastError();
     }
@@ -673,12 +756,30 @@ hipError_t go_parts(const PrefillArgs& a) {
 template <bool A_FP8>
 hipError_t dispatch(const PrefillArgs& a) {
     if (a.tile_m != 0 && a.split_k >= 16) {
-        // workgroup-shared operands (prefill_lds_kernel): split_k = 128 (KH - 1)
-        // + 16 U + D (K in KH parts of their own waves, stages of U k-steps, a
-        // ring of D), tile_m x tile_n workgroup tiles; a ring too deep for the
-        // LDS is cut to the deepest that fits
-        const uint32_t kh = a.split_k >= 128 ? 2 : 1, code = a.split_k % 128;
+        // workgroup-shared operands (prefill_lds_kernel): split_k = 256 P +
+        // 128 (KH - 1) + 16 U + D (K in KH parts of their own waves, stages of
+        // U k-steps, a ring of D; P = 1: the two K halves in ping-pong, KH = 2
+        // and (U, D) = (4, 2), (4, 3), (2, 3) or (2, 4) only), tile_m x tile_n
+        // workgroup tiles; a ring too deep for the LDS is cut to the deepest
+        // that fits
+        if (a.split_k >= 512 || (a.split_k >= 256 && a.split_k < 384)) return hipErrorNotSupported;
+        const bool pp = a.split_k >= 256;
+        const uint32_t kh = (a.split_k & 128) ? 2 : 1, code = a.split_k % 128;
         const uint32_t u = code / 16, d = code % 16;
+#define MX4_LDS_PP                                                                                       \
+            if (pp) {                                                                                    \
+                if (u == 4 && d == 2) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 4, 2, 2, true>(a);      \
+                if (u == 4 && d == 3)                                                                    \
+                    return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 4,                                      \
+                                  fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 4, 3, 2>(), 2, true>(a);       \
+                if (u == 2 && d == 3)                                                                    \
+                    return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 2,                                      \
+                                  fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 2, 3, 2>(), 2, true>(a);       \
+                if (u == 2 && d == 4)                                                                    \
+                    return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 2,                                      \
+                                  fit_depth<A_FP8, WM_c, WN_c, TM_c, TN_c, 2, 4, 2>(), 2, true>(a);       \
+                return hipErrorNotSupported;                                                             \
+            }
 #define MX4_LDS_KH(KH_)                                                                                  \
             if (kh == KH_) {                                                                             \
                 if (u == 4 && d == 2) return go_lds<A_FP8, WM_c, WN_c, TM_c, TN_c, 4, 2, KH_>(a);          \
@@ -704,6 +805,7 @@ hipError_t dispatch(const PrefillArgs& a) {
 #define MX4_LDS(BM_, BN_, WM_, WN_, TM_, TN_)                                                           \
         if (a.tile_m == BM_ && a.tile_n == BN_) {                                                       \
             constexpr int WM_c = WM_, WN_c = WN_, TM_c = TM_, TN_c = TN_;                               \
+            MX4_LDS_PP                                                                                  \
             MX4_LDS_KH(1)                                                                               \
             MX4_LDS_KH(2)                                                                               \
             return hipErrorNotSupported;                                                                \
@@ -718,6 +820,7 @@ hipError_t dispatch(const PrefillArgs& a) {
         MX4_LDS(64, 64, 2, 2, 1, 1)
 #undef MX4_LDS
 #undef MX4_LDS_KH
+#undef MX4_LDS_PP
         return hipErrorNotSupported;
     }
     if (a.tile_m != 0) {
@@ -746,52 +849,57 @@ hipError_t dispatch(const PrefillArgs& a) {
     }
     uint32_t ntot = 0;
     for (uint32_t s = 0; s < a.count; ++s) ntot += a.n[s];
-    // Workgroup-shared operands (prefill_lds_kernel) where they measured faster,
-    // cold weights at M = 512 (Qwen3-8B; split_k code 128 (KH - 1) + 16 U + D
-    // of the tuning call):
-    //  q|k|v (6144 rows, K = 4096): 64 x 128 tiles; MXFP4 in stages of 2
-    //  k-steps, 4 deep (19.4 -> 14.7 us), MX-FP8 in stages of 4, 2 deep
-    //  (24.0 -> 18.2 us);
-    //  gate|up (24576 rows), MXFP4: 128 x 192 tiles in stages of 2, 3 deep, so
-    //  two workgroups share a CU (46.1 -> 43.2 us);
-    //  q / o (4096 rows, K = 4096): K in two halves of their own four waves
-    //  (two waves per SIMD), stages of 2, 4 deep; MXFP4 on 128 x 64 tiles
-    //  (11.4 -> 10.7 us against the one-ring tile in two sweeps, even in a
-    //  third), MX-FP8 on 64 x 128 tiles (14.7 -> 13.5 and 14.8 -> 14.2 us
-    //  against 2 x 4 wave tiles in K quarters).
-    // gate or down alone and the other MX-FP8 shapes measured no faster there
-    // (down with K halves of their own waves: ahead in one sweep, 2-10% behind
-    // in three repetitions on another machine).
+    // Qwen3-8B shapes (K = 4096, and 12288 for down), measured on MI355X at
+    // M = 512 on cold weights, the alternatives timed in one process (split_k
+    // code 256 P + 128 (KH - 1) + 16 U + D of the tuning call):
+    //  q / o (4096 rows): K in two halves of their own four waves (two waves
+    //  per SIMD) in ping-pong, stages of 2 k-steps, 4 deep; MXFP4 on 128 x 64
+    //  tiles (11.2-11.5 -> 10.5-10.8 us against the same halves without
+    //  ping-pong; 10.5 -> 9.6 us warm), MX-FP8 on 64 x 128 tiles (14.1-14.3 ->
+    //  12.4-12.6 us);
+    //  q|k|v (6144 rows): MXFP4 on 128 x 128 tiles, K halves in ping-pong,
+    //  stages of 4, 2 deep (15.9-16.3 -> 13.6 us against 64 x 128 tiles over
+    //  the whole K in stages of 2, 4 deep); MX-FP8 keeps 64 x 128 tiles over
+    //  the whole K in stages of 4, 2 deep (18.2 us; ping-pong on 128 x 128
+    //  tiles the same);
+    //  gate|up (24576 rows), MXFP4: 128 x 192 tiles over the whole K in stages
+    //  of 2, 3 deep, two workgroups per CU (36-44 us; with K halves in
+    //  ping-pong a workgroup needs the LDS of a whole CU: 42-47 us);
+    //  gate alone (12288 rows) and gate|up MX-FP8: 128 x 192 tiles, K halves
+    //  in ping-pong, stages of 2, 3 deep (2 for MX-FP8, by the LDS): gate
+    //  MXFP4 24.1-24.7 -> 21.3-23.7 us (warm 19.5-20.0 -> 20.5-20.7), MX-FP8
+    //  31.8-32.7 -> 26.6-28.0 us; gate|up MX-FP8 60.5 -> 56.5 us, against 4 x
+    //  3 wave tiles in K halves without LDS;
+    //  down (4096 rows, K = 12288), MXFP4: 128 x 64 tiles, K halves in
+    //  ping-pong, stages of 2, 4 deep (27.3-28.2 -> 25.5-26.5 us against 4 x
+    //  2 wave tiles in K quarters; warm the same).
     if (a.k == 4096 && ntot <= 4096) {
-        if constexpr (A_FP8) return go_lds<true, 2, 2, 1, 2, 2, 4, 2>(a);
-        else return go_lds<false, 2, 2, 2, 1, 2, 4, 2>(a);
+        if constexpr (A_FP8) return go_lds<true, 2, 2, 1, 2, 2, 4, 2, true>(a);
+        else return go_lds<false, 2, 2, 2, 1, 2, 4, 2, true>(a);
     }
     if (a.k == 4096) {
-        if (ntot > 4096 && ntot <= 8192) {
+        if (ntot <= 8192) {
             if constexpr (A_FP8) return go_lds<true, 2, 2, 1, 2, 4, 2>(a);
-            else return go_lds<false, 2, 2, 1, 2, 2, 4>(a);
+            else return go_lds<false, 2, 2, 2, 2, 4, 2, 2, true>(a);
         }
         if constexpr (!A_FP8) {
             if (ntot >= 16384) return go_lds<false, 2, 2, 2, 3, 2, 3>(a);
         }
+        return go_lds<A_FP8, 2, 2, 2, 3, 2, fit_depth<A_FP8, 2, 2, 2, 3, 2, 3, 2>(), 2, true>(a);
     }
-    // measured on MI355X at M = 512 (Qwen3-8B shapes): wide N takes 4 x 3 tiles
-    // per wave with K in halves (gate/up: MXFP4 23.0 -> 21.9 us, MX-FP8 36.8
+    // other K: wide N takes 4 x 3 tiles per wave with K in halves (at K =
+    // 4096 before the shared kernels: gate MXFP4 23.0 -> 21.9 us, MX-FP8 36.8
     // -> 27.6 us against 2 x 3 tiles over the full K); otherwise 2 x 2 tiles
-    // with K split in two inside the workgroup, fully unrolled for the model's
-    // K sizes (larger tiles and K quarters measured slower there)
+    // with K split in two inside the workgroup, fully unrolled for the
+    // model's K sizes (larger tiles and K quarters measured slower there)
     if (ntot >= 8192 && a.k % 512 == 0) return go_parts<A_FP8, 4, 3, 2>(a);
-    // q|k|v in one launch (4096 + 1024 + 1024 rows, K = 4096): 128 x 128
-    // workgroup tiles over the full K, 192 workgroups (MXFP4 17.3 -> 15.9 us,
-    // MX-FP8 22.4 -> 20.6 us against 2 x 2 tiles in K halves)
-    if (ntot > 4096 && a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 1, 2, 0>(a);
-    // K = 12288 (down) in K quarters: MX-FP8 on 2 x 4 wave tiles (29.5 -> 27.1 us
-    // warm), MXFP4 on 4 x 2 wave tiles (cold weights: 30.9 -> 26.4 us)
+    // down, MX-FP8: K quarters on 2 x 4 wave tiles (29.5 -> 27.1 us warm
+    // against 2 x 2 tiles in K halves; K halves of 64 x 128 tiles in ping-pong
+    // 33.8 -> 32.6 us cold but 27.4 -> 28.3 us warm)
     if (a.k == 12288 && ntot <= 4096) {
         if constexpr (A_FP8) return go_parts<true, 2, 4, 4>(a);
-        else return go_parts<false, 4, 2, 4>(a);
+        else return go_lds<false, 2, 2, 2, 1, 2, 4, 2, true>(a);
     }
-    if (a.k == 4096) return go<A_FP8, 2, 2, 2, 4, 2, 2, 32>(a);
     if (a.k == 12288) return go<A_FP8, 2, 2, 2, 4, 2, 2, 96>(a);
     if (a.k % 512 == 0) return go<A_FP8, 2, 2, 2, 4, 2, 2, 0>(a);
     return go<A_FP8, 2, 2, 2, 2, 1, 1, 0>(a);

@@ -1411,12 +1411,19 @@ def test_prefill_instances_match_oracle(mx4, ctx, oracle, act, k, tile):
 
 
 # Workgroup-shared prefill instances: tile -> waves along M x N and MFMA tiles
-# per wave along M x N; split_k code 128 (H - 1) + 16 U + D (K in H halves of
-# their own waves, stages of U k-steps, ring of D).
+# per wave along M x N; split_k code 256 P + 128 (H - 1) + 16 U + D (K in H
+# halves of their own waves, stages of U k-steps, ring of D; P = 1: the two
+# halves in ping-pong).
 LDS_TILES = {(128, 192): (2, 2, 2, 3), (128, 128): (2, 2, 2, 2), (64, 128): (2, 2, 1, 2), (128, 64): (2, 2, 2, 1),
              (64, 256): (1, 4, 2, 2), (128, 96): (4, 1, 1, 3), (64, 192): (2, 2, 1, 3), (64, 64): (2, 2, 1, 1)}
+PP_CODES = (384 + 16 * 4 + 2, 384 + 16 * 4 + 3, 384 + 16 * 2 + 3, 384 + 16 * 2 + 4)
 LDS_CODES = (16 * 4 + 2, 16 * 4 + 3, 16 * 2 + 3, 16 * 2 + 4, 16 * 2 + 5, 16 * 2 + 8, 16 * 4 + 5,
-             128 + 16 * 4 + 2, 128 + 16 * 2 + 3, 128 + 16 * 2 + 4, 128 + 16 * 2 + 8)
+             128 + 16 * 4 + 2, 128 + 16 * 2 + 3, 128 + 16 * 2 + 4, 128 + 16 * 2 + 8) + PP_CODES
+
+
+def code_name(c):
+    """h<H>u<U>d<D>, with a trailing pp for the ping-pong schedule."""
+    return f"h{2 if c & 128 else 1}u{c % 128 // 16}d{c % 16}" + ("pp" if c >= 256 else "")
 
 
 def lds_depth(fp8, tile, code, k):
@@ -1425,8 +1432,11 @@ def lds_depth(fp8, tile, code, k):
     piece per wave, waits within vmcnt, the rings -- and with two K halves the
     hand-over of the second half's tile -- within 160 KiB of LDS, each K half
     on whole scale quads), a ring that does not fit cut to the deepest that
-    does (not below 2)."""
-    h, u, d = (2 if code >= 128 else 1), (code % 128) // 16, code % 16
+    does (not below 2); ping-pong only with two K halves and (U, D) = (4, 2),
+    (4, 3), (2, 3) or (2, 4)."""
+    h, u, d = (2 if code & 128 else 1), (code % 128) // 16, code % 16
+    if code >= 256 and (code >= 512 or h != 2 or (u, d) not in ((4, 2), (4, 3), (2, 3), (2, 4))):
+        return None
     if k % (256 * h) != 0:
         return None
     wm, wn, tm, tn = LDS_TILES[tile]
@@ -1448,12 +1458,13 @@ def lds_depth(fp8, tile, code, k):
 
 LDS_CASES = ([(4096, t, c) for t in LDS_TILES for c in LDS_CODES] +
              [(k, t, c) for k in (256, 1280) for t in LDS_TILES for c in (16 * 4 + 2, 16 * 2 + 4)] +
-             [(k, t, c) for k in (1536, 1280) for t in LDS_TILES for c in (128 + 16 * 4 + 2, 128 + 16 * 2 + 4)])
+             [(k, t, c) for k in (1536, 1280) for t in LDS_TILES
+              for c in (128 + 16 * 4 + 2, 128 + 16 * 2 + 4, 384 + 16 * 4 + 2, 384 + 16 * 2 + 4)])
 
 
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
 @pytest.mark.parametrize("k,tile,code", LDS_CASES,
-                         ids=[f"k{k}-{t[0]}x{t[1]}-h{1 + c // 128}u{c % 128 // 16}d{c % 16}" for k, t, c in LDS_CASES])
+                         ids=[f"k{k}-{t[0]}x{t[1]}-{code_name(c)}" for k, t, c in LDS_CASES])
 def test_prefill_shared_instances_match_oracle(mx4, ctx, oracle, act, k, tile, code):
     """Every workgroup-shared prefill instance reachable through
     mx4_prefill_config is compiled exactly where the kernel's limits allow it;
@@ -1463,7 +1474,7 @@ def test_prefill_shared_instances_match_oracle(mx4, ctx, oracle, act, k, tile, c
     halves off the quad grid, which the library refuses), matches the oracle on
     dequant(requant(x)), twice bitwise equal."""
     fp8 = act == "mxfp8"
-    h, u = 1 + code // 128, code % 128 // 16
+    h, u = (2 if code & 128 else 1), code % 128 // 16
     depth = lds_depth(fp8, tile, code, k)
     m, n = 70, 300
     acode = mx4.ACT_MXFP8 if fp8 else mx4.ACT_MXFP4
@@ -1478,7 +1489,7 @@ def test_prefill_shared_instances_match_oracle(mx4, ctx, oracle, act, k, tile, c
         assert status == mx4.ERR_UNSUPPORTED
         return
     assert status == 0, mx4.last_error()
-    say(f"shared prefill {act} k={k} tile={tile} H={h} U={u} D={depth}")
+    say(f"shared prefill {act} k={k} tile={tile} H={h} U={u} D={depth} pp={code >= 256}")
     packed, scales = ctx.download_weight(w)
     ref, _ = _prefill_ref(oracle, x, packed, scales, act)
     outs = []
@@ -1512,7 +1523,7 @@ def test_prefill_shared_identity_is_exact(mx4, ctx, oracle, act, tile):
     dec = oracle.dequantize(packed, scales)
     yb = ctx.buffer(m * n * 4)
     ran = 0
-    for code in (16 * 4 + 2, 16 * 2 + 3, 128 + 16 * 4 + 2, 128 + 16 * 2 + 3):
+    for code in (16 * 4 + 2, 16 * 2 + 3, 128 + 16 * 4 + 2, 128 + 16 * 2 + 3, 384 + 16 * 4 + 2, 384 + 16 * 2 + 3):
         if lds_depth(act == "mxfp8", tile, code, k) is None:
             continue
         yb.upload(np.full(m * n, np.nan, np.float32))
@@ -1522,8 +1533,41 @@ def test_prefill_shared_identity_is_exact(mx4, ctx, oracle, act, tile):
     assert ran >= 1
 
 
+PP_CASES = [(k, t, c) for k in (4096, 1536) for t in LDS_TILES for c in PP_CODES]
+
+
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+@pytest.mark.parametrize("k,tile,code", PP_CASES, ids=[f"k{k}-{t[0]}x{t[1]}-{code_name(c)}" for k, t, c in PP_CASES])
+def test_prefill_ping_pong_equals_halves(mx4, ctx, oracle, act, k, tile, code):
+    """The ping-pong schedule changes when each K half's waves read LDS and
+    issue MFMAs, not the arithmetic: its output is the same bits as the two K
+    halves without it (same tile, stage and ring), on ragged m and n, and
+    repeated calls agree."""
+    fp8 = act == "mxfp8"
+    depth = lds_depth(fp8, tile, code, k)
+    if depth is None:
+        return
+    assert lds_depth(fp8, tile, code - 256, k) == depth
+    m, n = 100, 250
+    acode = mx4.ACT_MXFP8 if fp8 else mx4.ACT_MXFP4
+    w = ctx.synth_weight(830 + k // 256, n, k, 0.02)
+    x = oracle.bf16_to_f32(oracle.synth_bf16(840 + k // 256, 1.0, m * k)).reshape(m, k)
+    codes, sc = ctx.prefill_act_buffers(m, k, acode)
+    ctx.prefill_quantize(ctx.to_device((f32_bits(x) >> 16).astype(np.uint16)), mx4.BF16, m, k, acode, codes, sc)
+    yb = ctx.buffer(m * n * 4)
+    outs = []
+    for c in (code - 256, code, code):
+        yb.upload(np.full(m * n, np.nan, np.float32))
+        assert ctx.prefill_config(codes, sc, acode, m, w, yb, tile[0], tile[1], c) == 0, mx4.last_error()
+        outs.append(yb.download(np.float32))
+    assert np.all(np.isfinite(outs[0]))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), (tile, code_name(code))
+    assert np.array_equal(outs[1].view(np.uint32), outs[2].view(np.uint32))
+
+
 GROUP_TILES = [(0, 0, 0), (128, 192, 1), (128, 128, 1), (64, 128, 2), (128, 192, 2), (128, 64, 4), (64, 128, 4),
-               (64, 128, 16 * 2 + 4), (128, 192, 16 * 2 + 3), (64, 128, 16 * 4 + 2)]
+               (64, 128, 16 * 2 + 4), (128, 192, 16 * 2 + 3), (64, 128, 16 * 4 + 2),
+               (128, 128, 384 + 16 * 4 + 2), (128, 192, 384 + 16 * 2 + 3)]
 
 
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
@@ -1543,6 +1587,8 @@ def test_prefill_group_equals_individual(mx4, ctx, oracle, act):
     ys = [ctx.buffer(m * n * 4) for n in ns]
     y1 = ctx.buffer(max(ns) * m * 4)
     for tile in GROUP_TILES:
+        if tile[2] >= 16 and lds_depth(act == "mxfp8", tile[:2], tile[2], k) is None:
+            continue  # e.g. stages of 4 on 128 x 128 MX-FP8 tiles in two rings outgrow the LDS
         say(f"prefill group {act} tile {tile}")
         for y, n in zip(ys, ns):
             y.upload(np.full(m * n, np.nan, np.float32))
@@ -1611,6 +1657,11 @@ def test_prefill_config_rejects_unknown_instance(mx4, ctx):
     assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 96, 64, 16 * 4 + 2) == mx4.ERR_UNSUPPORTED
     assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 64, 128, 16 * 3 + 3) == mx4.ERR_UNSUPPORTED
     assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 64, 128, 16 * 2 + 6) == mx4.ERR_UNSUPPORTED
+    # ping-pong: without two K halves, with a stage and ring it does not
+    # compile, and codes past it
+    assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 64, 128, 256 + 16 * 2 + 3) == mx4.ERR_UNSUPPORTED
+    assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 64, 128, 384 + 16 * 2 + 5) == mx4.ERR_UNSUPPORTED
+    assert ctx.prefill_config(codes, sc, mx4.ACT_MXFP4, m, w, yb, 64, 128, 512 + 128 + 16 * 2 + 3) == mx4.ERR_UNSUPPORTED
     # K quarters must start on whole scale quads (K % 1024 == 0)
     w2 = ctx.synth_weight(8, n, 1536, 0.02)
     codes2, sc2 = ctx.prefill_act_buffers(m, 1536, mx4.ACT_MXFP4)
