@@ -1218,12 +1218,13 @@ def main() -> int:
         for (nm, n, k, w) in weights:
             by.setdefault(nm, (n, k, w))
         ctx.reserve_prefill(m, 12288)
-        plan = [("gate", "register-direct 4x3 tiles, K halves (default)", (0, 0, 0)),
-                ("gate", "workgroup-shared 128x192, U=4, D=2", (128, 192, 16 * 4 + 2)),
+        plan = [("gate", "register-direct 4x3 tiles, K halves", (128, 192, 2)),
+                ("gate", "workgroup-shared 128x192, U=2, D=3, K halves", (128, 192, 128 + 16 * 2 + 3)),
+                ("gate", "the same in ping-pong (default)", (128, 192, 384 + 16 * 2 + 3)),
                 ("q", "register-direct 2x2 tiles, K halves", (64, 128, 2)),
                 ("q", "workgroup-shared 128x64, U=2, D=4, one ring", (128, 64, 16 * 2 + 4)),
-                ("q", "workgroup-shared 128x64, U=2, D=4, K halves of their own waves (default)",
-                 (128, 64, 128 + 16 * 2 + 4))]
+                ("q", "workgroup-shared 128x64, U=2, D=4, K halves", (128, 64, 128 + 16 * 2 + 4)),
+                ("q", "the same in ping-pong (default)", (128, 64, 384 + 16 * 2 + 4))]
         for name, _, inst in plan:
             n, k, w = by[name]
             w.prepare_prefill()

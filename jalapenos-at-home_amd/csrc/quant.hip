@@ -166,81 +166,102 @@ hipError_t launch_quantize_fp8(const void* in, bool in_bf16, uint64_t rows, uint
 }
 
 // Fragment-native output (prefill.hip): the same rules as above. A workgroup
-// of four waves takes one row group g and scale quad q; wave u quantizes
-// k-step 4 q + u, lane t the block 8 q + 2 u + t / 32 of row 32 g + t % 32 --
-// exactly lane t's part of fragment (g, 4 q + u), so each wave stores one
-// contiguous 1 KiB (FP8: 2 KiB) and reads whole 128-byte spans of 32 rows
-// (lanes t and t + 32 read the two halves). The four scale bytes of lane t
-// (byte u from wave u) meet in LDS and leave as one 4-byte word, 256 bytes per
-// workgroup. Rows past `rows` in the last group are written as zero codes and
-// scales; a block with a non-finite value gets scale byte 0xff (E8M0 NaN).
+// of four waves takes row group g and k-step kk (32 rows x 64 columns), so a
+// launch has a workgroup per 2048 values and each SIMD several waves to hide
+// the load latency behind. Thread i reads the 8 consecutive values [8 p, +8)
+// of row 32 g + i / 8 (p = i % 8), so each wave reads whole row spans (one
+// 128-byte line per row for bf16). The four threads of a 32-element block (p
+// in 0..3 or 4..7: block h = p / 4 of the k-step) meet in a DPP max for its
+// scale; each encodes its 8 values and stores them where the fragment holds
+// them: FP4 bytes [4 (p % 4), +4) of lane r32 + 32 h's 16, FP8 the 8 bytes of
+// K [8 p, +8) (lane group (p % 4) / 2 of KiB h). The block's first thread
+// stores the scale byte: byte kk % 4 of lane r32 + 32 h's word of quad kk / 4.
+// Rows past `rows` in the last group are written as zero codes and scales; a
+// block with a non-finite value gets scale byte 0xff (E8M0 NaN), so its
+// products -- and the row's outputs -- are NaN instead of finite values of a
+// meaningless scale.
 template <bool BF16, bool FP8>
 __global__ __launch_bounds__(256) void quantize_fragments_kernel(const void* __restrict__ in, uint32_t rows,
                                                                  uint32_t cols, uint8_t* __restrict__ codes,
                                                                  uint8_t* __restrict__ scales,
                                                                  uint32_t* __restrict__ bad) {
-    __shared__ uint32_t sbytes[4][64];
-    const uint32_t lane = threadIdx.x % 64, u = threadIdx.x / 64;
-    const uint32_t nblk = cols / 32, nk = cols / 64, nq = cols / 256;
-    const uint32_t q = blockIdx.x % nq, g = blockIdx.x / nq;
-    const uint32_t r32 = lane % 32, half = lane / 32;
-    const uint32_t row = 32 * g + r32, kk = 4 * q + u;
-    float v[32];
+    constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E;  // DPP quad_perm [1,0,3,2], [2,3,0,1]
+    const uint32_t t = threadIdx.x, p = t % 8, r32 = t / 8, h = p / 4;
+    const uint32_t nk = cols / 64, nq = cols / 256;
+    const uint32_t kk = blockIdx.x % nk, g = blockIdx.x / nk;
+    const uint32_t row = 32 * g + r32;
+    float v[8];
     if (row < rows) {
-        load_block32<BF16>(in, (uint64_t)row * nblk + 2 * kk + half, v);
+        const uint64_t e0 = (uint64_t)row * cols + 64 * kk + 8 * p;
+        if constexpr (BF16) {
+            const u32x4 w = load_u32x4(static_cast<const uint8_t*>(in) + 2 * e0);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                v[2 * c] = bf16_bits_to_f32(w[c] & 0xffffu);
+                v[2 * c + 1] = bf16_bits_to_f32(w[c] >> 16);
+            }
+        } else {
+            const f32x4* src = reinterpret_cast<const f32x4*>(static_cast<const float*>(in) + e0);
+            const f32x4 a = src[0], b = src[1];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                v[c] = a[c];
+                v[4 + c] = b[c];
+            }
+        }
     } else {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) v[i] = 0.0f;
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
     }
-    bool finite;
-    const float amax = block_amax(v, finite);
-    if (!finite) atomicOr(bad, 1u);
+    // the block's largest magnitude, as bits (non-negative floats order like
+    // their bit patterns, so the maximum is exact in any order), and whether
+    // any value is inf or NaN
+    uint32_t mx = 0, nonfinite = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t a = __float_as_uint(v[i]) & 0x7fffffffu;
+        mx = a > mx ? a : mx;
+        nonfinite |= a >= 0x7f800000u ? 1u : 0u;
+    }
+    {
+        uint32_t om = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, kQuadXor1, 0xF, 0xF, false);
+        nonfinite |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)nonfinite, kQuadXor1, 0xF, 0xF, false);
+        mx = om > mx ? om : mx;
+        om = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, kQuadXor2, 0xF, 0xF, false);
+        nonfinite |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)nonfinite, kQuadXor2, 0xF, 0xF, false);
+        mx = om > mx ? om : mx;
+    }
+    const float amax = __uint_as_float(mx);
+    const bool finite = nonfinite == 0;
+    if (!finite && p % 4 == 0) atomicOr(bad, 1u);
+    const uint64_t frag = (uint64_t)g * nk + kk;
     uint32_t s;
     if constexpr (FP8) {
         s = fp8_scale_byte(amax);
-        // bytes [16p, 16p + 16) of the block belong to lane group p, in the
-        // first (block 2kk) or second (block 2kk + 1) KiB of the fragment
+        uint32_t w0 = 0, w1 = 0;
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            u32x4 out;
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                uint32_t word = 0;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) word |= e4m3_code(v[16 * p + 4 * d + i], s) << (8 * i);
-                out[d] = word;
-            }
-            *reinterpret_cast<u32x4*>(codes + ((uint64_t)g * nk + kk) * 2048 + half * 1024 + (32 * p + r32) * 16) =
-                out;
+        for (int i = 0; i < 4; ++i) {
+            w0 |= e4m3_code(v[i], s) << (8 * i);
+            w1 |= e4m3_code(v[4 + i], s) << (8 * i);
         }
+        uint8_t* dst = codes + frag * 2048 + h * 1024 + (32 * ((p % 4) / 2) + r32) * 16 + 8 * (p % 2);
+        *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
     } else {
         s = mxfp4_scale_byte(amax);
-        u32x4 out;
+        uint32_t word = 0;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) word |= mxfp4_code(v[8 * d + i], s) << (4 * i);
-            out[d] = word;
-        }
-        *reinterpret_cast<u32x4*>(codes + (((uint64_t)g * nk + kk) * 64 + lane) * 16) = out;
+        for (int i = 0; i < 8; ++i) word |= mxfp4_code(v[i], s) << (4 * i);
+        *reinterpret_cast<uint32_t*>(codes + (frag * 64 + r32 + 32 * h) * 16 + 4 * (p % 4)) = word;
     }
-    // block 8q + 2u + h: byte u of lane 32h + r32 of quad q. A block holding
-    // inf or NaN gets the E8M0 NaN byte, so its products -- and the row's
-    // outputs -- are NaN instead of finite values of a meaningless scale.
-    sbytes[u][lane] = finite ? s : 0xffu;
-    __syncthreads();
-    if (u == 0) {
-        const uint32_t word = sbytes[0][lane] | (sbytes[1][lane] << 8) | (sbytes[2][lane] << 16) | (sbytes[3][lane] << 24);
-        reinterpret_cast<uint32_t*>(scales)[((uint64_t)g * nq + q) * 64 + lane] = word;
-    }
+    if (p % 4 == 0)
+        scales[(((uint64_t)g * nq + kk / 4) * 64 + r32 + 32 * h) * 4 + kk % 4] = (uint8_t)(finite ? s : 0xffu);
 }
 
 hipError_t launch_quantize_fragments(const void* in, bool in_bf16, uint32_t rows, uint32_t cols, bool fp8,
                                      uint8_t* codes_f, uint8_t* scales_f, uint32_t* bad, hipStream_t s) {
     if (rows == 0 || cols == 0) return hipSuccess;
     if (cols % 256 != 0) return hipErrorInvalidValue;
-    const uint64_t wgs = (uint64_t)((rows + 31) / 32) * (cols / 256);
+    const uint64_t wgs = (uint64_t)((rows + 31) / 32) * (cols / 64);
     if (wgs > 0x7fffffffu) return hipErrorInvalidValue;
     dim3 grid((unsigned)wgs);
     if (in_bf16) {
