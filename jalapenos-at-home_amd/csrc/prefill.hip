@@ -853,10 +853,11 @@ hipError_t dispatch(const PrefillArgs& a) {
     // M = 512 on cold weights, the alternatives timed in one process (split_k
     // code 256 P + 128 (KH - 1) + 16 U + D of the tuning call):
     //  q / o (4096 rows): K in two halves of their own four waves (two waves
-    //  per SIMD) in ping-pong, stages of 2 k-steps, 4 deep; MXFP4 on 128 x 64
-    //  tiles (11.2-11.5 -> 10.5-10.8 us against the same halves without
-    //  ping-pong; 10.5 -> 9.6 us warm), MX-FP8 on 64 x 128 tiles (14.1-14.3 ->
-    //  12.4-12.6 us);
+    //  per SIMD) in ping-pong; MXFP4 on 128 x 64 tiles in stages of 4 k-steps,
+    //  2 deep (10.9 -> 10.8 us against stages of 2, 4 deep, and 11.2-11.5
+    //  against the same halves without ping-pong; 9.9 -> 9.0 us warm), MX-FP8
+    //  on 64 x 128 tiles in stages of 4, 2 deep (12.9 -> 12.3 us against
+    //  stages of 2, 4 deep, 14.1-14.3 without ping-pong);
     //  q|k|v (6144 rows): MXFP4 on 128 x 128 tiles, K halves in ping-pong,
     //  stages of 4, 2 deep (15.9-16.3 -> 13.6 us against 64 x 128 tiles over
     //  the whole K in stages of 2, 4 deep); MX-FP8 keeps 64 x 128 tiles over
@@ -870,12 +871,14 @@ hipError_t dispatch(const PrefillArgs& a) {
     //  MXFP4 24.1-24.7 -> 21.3-23.7 us (warm 19.5-20.0 -> 20.5-20.7), MX-FP8
     //  31.8-32.7 -> 26.6-28.0 us; gate|up MX-FP8 60.5 -> 56.5 us, against 4 x
     //  3 wave tiles in K halves without LDS;
-    //  down (4096 rows, K = 12288), MXFP4: 128 x 64 tiles, K halves in
-    //  ping-pong, stages of 2, 4 deep (27.3-28.2 -> 25.5-26.5 us against 4 x
-    //  2 wave tiles in K quarters; warm the same).
+    //  down (4096 rows, K = 12288): 64 x 128 tiles, K halves in ping-pong,
+    //  stages of 2, 4 deep; MXFP4 26.7-27.1 -> 25.3-25.4 us (warm 22.6-23.7
+    //  -> 20.4-20.6) against 128 x 64 tiles the same way and 27.3-28.2 us
+    //  against 4 x 2 wave tiles in K quarters; MX-FP8 33.5-33.6 -> 31.0-31.3
+    //  us against 2 x 4 wave tiles in K quarters (three repetitions each).
     if (a.k == 4096 && ntot <= 4096) {
-        if constexpr (A_FP8) return go_lds<true, 2, 2, 1, 2, 2, 4, 2, true>(a);
-        else return go_lds<false, 2, 2, 2, 1, 2, 4, 2, true>(a);
+        if constexpr (A_FP8) return go_lds<true, 2, 2, 1, 2, 4, 2, 2, true>(a);
+        else return go_lds<false, 2, 2, 2, 1, 4, 2, 2, true>(a);
     }
     if (a.k == 4096) {
         if (ntot <= 8192) {
@@ -893,13 +896,7 @@ hipError_t dispatch(const PrefillArgs& a) {
     // with K split in two inside the workgroup, fully unrolled for the
     // model's K sizes (larger tiles and K quarters measured slower there)
     if (ntot >= 8192 && a.k % 512 == 0) return go_parts<A_FP8, 4, 3, 2>(a);
-    // down, MX-FP8: K quarters on 2 x 4 wave tiles (29.5 -> 27.1 us warm
-    // against 2 x 2 tiles in K halves; K halves of 64 x 128 tiles in ping-pong
-    // 33.8 -> 32.6 us cold but 27.4 -> 28.3 us warm)
-    if (a.k == 12288 && ntot <= 4096) {
-        if constexpr (A_FP8) return go_parts<true, 2, 4, 4>(a);
-        else return go_lds<false, 2, 2, 2, 1, 2, 4, 2, true>(a);
-    }
+    if (a.k == 12288 && ntot <= 4096) return go_lds<A_FP8, 2, 2, 1, 2, 2, 4, 2, true>(a);
     if (a.k == 12288) return go<A_FP8, 2, 2, 2, 4, 2, 2, 96>(a);
     if (a.k % 512 == 0) return go<A_FP8, 2, 2, 2, 4, 2, 2, 0>(a);
     return go<A_FP8, 2, 2, 2, 2, 1, 1, 0>(a);
