@@ -1224,7 +1224,7 @@ def main() -> int:
                 ("q", "register-direct 2x2 tiles, K halves", (64, 128, 2)),
                 ("q", "workgroup-shared 128x64, U=2, D=4, one ring", (128, 64, 16 * 2 + 4)),
                 ("q", "workgroup-shared 128x64, U=2, D=4, K halves", (128, 64, 128 + 16 * 2 + 4)),
-                ("q", "the same in ping-pong (default)", (128, 64, 384 + 16 * 2 + 4))]
+                ("q", "the same in ping-pong", (128, 64, 384 + 16 * 2 + 4))]
         for name, _, inst in plan:
             n, k, w = by[name]
             w.prepare_prefill()
