@@ -25,7 +25,10 @@
 //  * split K (KS > 1, rows too wide for a workgroup's activations to stay
 //    resident): KS workgroups share a tile, each over one K slice with its
 //    slice's activations resident, and the last of them to finish adds the KS
-//    partial tiles in slice order.
+//    partial tiles in slice order;
+//  * up to 5 bf16 tokens at K = 12288 (XLM): the activations are loaded once
+//    per workgroup into LDS and each unit's operand fragments read from there,
+//    instead of every unit loading its 16-token fragments from the L2.
 #include <type_traits>
 
 #include "mx4_device.h"
@@ -107,7 +110,7 @@ __device__ __forceinline__ void split3(const f32x4 a, const f32x4 b, bf16x8& hi,
 // ahead of the MFMAs, or, with one unit per tile, two tiles ahead. After a
 // tile's last unit the TW partial 16x16 tiles are summed through LDS
 // (double-buffered: one barrier per tile).
-template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS>
+template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS, int XLM = 0>
 __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restrict__ packed,
                                                          const uint8_t* __restrict__ scales,
                                                          const void* __restrict__ x, float* __restrict__ y,
@@ -128,6 +131,24 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     const uint32_t kb = slice * (ks / 32);
     const __amdgpu_buffer_rsrc_t empty = rsrc(packed, 0);
     const __amdgpu_buffer_rsrc_t xr = rsrc(x, m * k * (XBF16 ? 2u : 4u));
+    // XLM > 0 (bf16 x, m <= XLM, rows too wide for registers): the token rows
+    // are loaded once per workgroup into LDS, XS bytes apart (16 bytes of
+    // padding put the 16 token rows of an operand read in different bank
+    // groups), and each unit's activation fragments are read from there
+    // instead of from the L2 -- a unit's global loads are then its weights
+    // and scales only.
+    constexpr uint32_t XS = k * 2 + 16;
+    __shared__ __attribute__((aligned(16))) uint8_t xl[XLM > 0 ? XLM * XS : 16];
+    if constexpr (XLM > 0) {
+        static_assert(XBF16 && MT == 1 && !RESX, "LDS-resident activations: bf16, one token tile");
+        constexpr uint32_t per_row = k * 2 / 16;
+        const uint32_t chunks = (m < (uint32_t)XLM ? m : (uint32_t)XLM) * per_row;
+        for (uint32_t c = threadIdx.x; c < chunks; c += 64 * TW) {
+            const uint32_t r = c / per_row, o = c % per_row;
+            *reinterpret_cast<u32x4*>(xl + r * XS + 16 * o) = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * c, 0, 0);
+        }
+        __syncthreads();
+    }
 
     struct Unit {
         u32x4 w[U];
@@ -186,6 +207,18 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
             else
                 out.w[q] = __builtin_amdgcn_raw_buffer_load_b128(wr, col * row_bytes + 16 * blk, 0, kNT);
             if constexpr (RESX) continue;
+            if constexpr (XLM > 0) {
+                // token row col of the operand; rows >= m are zeros (the
+                // address stays in row 0, the value is not used)
+                const bool live = col < m;
+                const uint8_t* src = xl + (live ? col : 0u) * XS + 64 * blk;
+#pragma unroll
+                for (int c = 0; c < XQ; ++c) {
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(src + 16 * c);
+                    out.xa[0][q][c] = live ? v : u32x4{0u, 0u, 0u, 0u};
+                }
+                continue;
+            }
 #pragma unroll
             for (int j = 0; j < MT; ++j) {
                 const uint32_t off = ((16 * j + col) * k + 32 * blk) * (XBF16 ? 2u : 4u);
@@ -398,7 +431,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     }
 }
 
-template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS = 1>
+template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS = 1, int XLM = 0>
 hipError_t go(const GemvArgs& a, int cus, const SkinnyScratch& sc = {}) {
     const uint32_t tiles = (a.n + 15) / 16;
     // two workgroups of TW waves per CU; with one unit per tile, eight waves
@@ -411,7 +444,7 @@ hipError_t go(const GemvArgs& a, int cus, const SkinnyScratch& sc = {}) {
     if (grid == 0) grid = 1;
     const uint32_t per = (tiles + grid - 1) / grid;
     grid = (tiles + per - 1) / per;
-    hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX, KS>), dim3(grid * KS), dim3(64 * TW), 0, a.stream,
+    hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX, KS, XLM>), dim3(grid * KS), dim3(64 * TW), 0, a.stream,
                        a.packed, a.scales, a.x, a.y, a.m, a.n, sc.part, sc.count);
     return hipGetLastError();
 }
@@ -495,6 +528,12 @@ hipError_t go_k(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
                     if constexpr (MT == 1) return go<XBF16, 1, 2, 1, 12, true, 4>(a, cus, sc);
                     else return go<XBF16, MT, 4, 1, 6, true, 4>(a, cus, sc);
                 }
+            // up to 5 bf16 tokens: the activations stay in LDS (5 x 24 KiB
+            // beside the kernel's 32 KiB of stage and reduction buffers): 8B
+            // down at 3 / 4 / 5 tokens 10.0 / 10.3 / 10.3 -> 7.7 / 8.0 / 8.3 us
+            // (two repetitions, the same bits)
+            if constexpr (XBF16 && MT == 1)
+                if (a.m <= 5) return go<XBF16, 1, U, 12 / U, TW, false, 1, 5>(a, cus);
             return go<XBF16, MT, U, 12 / U, TW, false>(a, cus);
         default: return hipErrorNotSupported;
     }
