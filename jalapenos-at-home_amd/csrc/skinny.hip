@@ -26,8 +26,9 @@
 //    resident): KS workgroups share a tile, each over one K slice with its
 //    slice's activations resident, and the last of them to finish adds the KS
 //    partial tiles in slice order;
-//  * up to 5 bf16 tokens at K = 12288 (XLM): the activations are loaded once
-//    per workgroup into LDS and each unit's operand fragments read from there,
+//  * up to 15 bf16 tokens at K = 12288 (XLM, NP): the activations are loaded
+//    into LDS by the workgroup -- all of K up to 5 tokens, one K half or third
+//    at a time above -- and each unit's operand fragments read from there,
 //    instead of every unit loading its 16-token fragments from the L2.
 #include <type_traits>
 
@@ -110,7 +111,7 @@ __device__ __forceinline__ void split3(const f32x4 a, const f32x4 b, bf16x8& hi,
 // ahead of the MFMAs, or, with one unit per tile, two tiles ahead. After a
 // tile's last unit the TW partial 16x16 tiles are summed through LDS
 // (double-buffered: one barrier per tile).
-template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS, int XLM = 0>
+template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS, int XLM = 0, int NP = 1>
 __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restrict__ packed,
                                                          const uint8_t* __restrict__ scales,
                                                          const void* __restrict__ x, float* __restrict__ y,
@@ -132,24 +133,32 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     const __amdgpu_buffer_rsrc_t empty = rsrc(packed, 0);
     const __amdgpu_buffer_rsrc_t xr = rsrc(x, m * k * (XBF16 ? 2u : 4u));
     // XLM > 0 (bf16 x, m <= XLM, rows too wide for registers): the token rows
-    // are loaded once per workgroup into LDS, XS bytes apart (16 bytes of
-    // padding put the 16 token rows of an operand read in different bank
-    // groups), and each unit's activation fragments are read from there
-    // instead of from the L2 -- a unit's global loads are then its weights
-    // and scales only.
-    constexpr uint32_t XS = k * 2 + 16;
+    // live in LDS, XS bytes apart (16 bytes of padding put the 16 token rows
+    // of an operand read in different bank groups), and each unit's
+    // activation fragments are read from there instead of from the L2 -- a
+    // unit's global loads are then its weights and scales only. With NP > 1
+    // passes LDS holds one K slice of them at a time (units s NU / NP to
+    // (s + 1) NU / NP cover slice s), loaded by the whole workgroup between
+    // two barriers when its first unit comes up.
+    static_assert(NP == 1 || (XLM > 0 && KS == 1 && NU % NP == 0), "passes over K slices need whole units");
+    constexpr uint32_t KP = k / NP;  // K elements of one pass
+    constexpr uint32_t XS = KP * 2 + 16;
+    constexpr int UPP = NU / NP;     // units per pass
     __shared__ __attribute__((aligned(16))) uint8_t xl[XLM > 0 ? XLM * XS : 16];
-    if constexpr (XLM > 0) {
-        static_assert(XBF16 && MT == 1 && !RESX, "LDS-resident activations: bf16, one token tile");
-        constexpr uint32_t per_row = k * 2 / 16;
+    auto fill = [&](uint32_t pass) {
+        constexpr uint32_t per_row = KP * 2 / 16;
         const uint32_t chunks = (m < (uint32_t)XLM ? m : (uint32_t)XLM) * per_row;
         for (uint32_t c = threadIdx.x; c < chunks; c += 64 * TW) {
             const uint32_t r = c / per_row, o = c % per_row;
-            *reinterpret_cast<u32x4*>(xl + r * XS + 16 * o) = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * c, 0, 0);
+            *reinterpret_cast<u32x4*>(xl + r * XS + 16 * o) =
+                __builtin_amdgcn_raw_buffer_load_b128(xr, r * k * 2 + pass * KP * 2 + 16 * o, 0, 0);
         }
+    };
+    if constexpr (XLM > 0) {
+        static_assert(XBF16 && MT == 1 && !RESX, "LDS-resident activations: bf16, one token tile");
+        fill(0);
         __syncthreads();
     }
-
     struct Unit {
         u32x4 w[U];
         uint32_t s[U];  // scale-byte runs: chunk q's byte for lane group g is byte g of s[q]
@@ -189,7 +198,24 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
         if constexpr (U == 4) return 64 * i + 16 * j + ((b + 2 * j + (i & 1)) & 15);
         else return 64 * i + 8 * j + ((b + (j & ~1u)) & 7);
     };
-    auto load = [&](uint32_t tile, uint32_t unit, Unit& out) {
+    // chunk q of unit `unit`: its activation fragments from the LDS slice
+    // now loaded (the unit lies in slice unit / UPP)
+    auto read_xq = [&](uint32_t unit, int q, Unit& out) {
+        // token rows >= m: zeros, the address in row 0 (the dispatcher keeps m <= XLM)
+        const bool live = col < m;
+        const uint32_t blk = kb + 4 * ((unit * TW + wave) * U + q) + g - (NP > 1 ? (unit / UPP) * (KP / 32) : 0u);
+        const uint8_t* src = xl + (live ? col : 0u) * XS + 64 * blk;
+#pragma unroll
+        for (int c = 0; c < XQ; ++c) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(src + 16 * c);
+            out.xa[0][q][c] = live ? v : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto read_x = [&](uint32_t unit, Unit& out) {
+#pragma unroll
+        for (int q = 0; q < U; ++q) read_xq(unit, q, out);
+    };
+    auto load = [&](uint32_t tile, uint32_t unit, Unit& out, bool xnow = true) {
         const bool valid = tile < tiles;
         const uint32_t row0 = valid ? tile * 16 : 0;
         const uint32_t rows = valid ? (n - row0 < 16u ? n - row0 : 16u) : 0;
@@ -207,7 +233,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
             else
                 out.w[q] = __builtin_amdgcn_raw_buffer_load_b128(wr, col * row_bytes + 16 * blk, 0, kNT);
             if constexpr (RESX) continue;
-            if constexpr (XLM > 0) {
+            if constexpr (XLM > 0 && NP == 1) {
                 // token row col of the operand; rows >= m are zeros (the
                 // address stays in row 0, the value is not used)
                 const bool live = col < m;
@@ -217,6 +243,10 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
                     const u32x4 v = *reinterpret_cast<const u32x4*>(src + 16 * c);
                     out.xa[0][q][c] = live ? v : u32x4{0u, 0u, 0u, 0u};
                 }
+                continue;
+            }
+            if constexpr (XLM > 0) {
+                if (xnow) read_xq(unit, q, out);
                 continue;
             }
 #pragma unroll
@@ -371,19 +401,50 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
         static_assert(NU % 2 == 0, "an odd unit count needs the copy-free rotation");
         Unit u[2];
         load(tile, 0, u[0]);
+        if constexpr (NP == 1) {
+            for (;;) {
+                const uint32_t next = tile + stride;
+#pragma unroll
+                for (int p = 0; p < NU; ++p) {
+                    if (p + 1 < NU)
+                        load(tile, (uint32_t)(p + 1), u[(p + 1) % 2]);
+                    else
+                        load(next, 0, u[(p + 1) % 2]);
+                    compute(u[p % 2], p);
+                }
+                reduce_write(tile);
+                if (next >= tiles) break;
+                tile = next;
+            }
+        } else {
+        bool first = true;
         for (;;) {
             const uint32_t next = tile + stride;
 #pragma unroll
             for (int p = 0; p < NU; ++p) {
+                if constexpr (NP > 1) {
+                    // the first unit of a pass after the first: its slice
+                    // replaces the previous one once every wave is done with it
+                    if (p % UPP == 0 && (p > 0 || !first)) {
+                        __syncthreads();
+                        fill((uint32_t)(p / UPP));
+                        __syncthreads();
+                        read_x((uint32_t)p, u[p % 2]);
+                    }
+                }
+                // the next unit's activations wait for its slice when it opens a pass
+                const bool xnow = NP == 1 || (p + 1) % UPP != 0;
                 if (p + 1 < NU)
-                    load(tile, (uint32_t)(p + 1), u[(p + 1) % 2]);
+                    load(tile, (uint32_t)(p + 1), u[(p + 1) % 2], xnow);
                 else
-                    load(next, 0, u[(p + 1) % 2]);
+                    load(next, 0, u[(p + 1) % 2], xnow);
                 compute(u[p % 2], p);
             }
             reduce_write(tile);
+            first = false;
             if (next >= tiles) break;
             tile = next;
+        }
         }
     }
     if constexpr (KS > 1) {
@@ -431,7 +492,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     }
 }
 
-template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS = 1, int XLM = 0>
+template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS = 1, int XLM = 0, int NP = 1>
 hipError_t go(const GemvArgs& a, int cus, const SkinnyScratch& sc = {}) {
     const uint32_t tiles = (a.n + 15) / 16;
     // two workgroups of TW waves per CU; with one unit per tile, eight waves
@@ -444,7 +505,7 @@ hipError_t go(const GemvArgs& a, int cus, const SkinnyScratch& sc = {}) {
     if (grid == 0) grid = 1;
     const uint32_t per = (tiles + grid - 1) / grid;
     grid = (tiles + per - 1) / per;
-    hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX, KS, XLM>), dim3(grid * KS), dim3(64 * TW), 0, a.stream,
+    hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX, KS, XLM, NP>), dim3(grid * KS), dim3(64 * TW), 0, a.stream,
                        a.packed, a.scales, a.x, a.y, a.m, a.n, sc.part, sc.count);
     return hipGetLastError();
 }
@@ -528,12 +589,17 @@ hipError_t go_k(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
                     if constexpr (MT == 1) return go<XBF16, 1, 2, 1, 12, true, 4>(a, cus, sc);
                     else return go<XBF16, MT, 4, 1, 6, true, 4>(a, cus, sc);
                 }
-            // up to 5 bf16 tokens: the activations stay in LDS (5 x 24 KiB
-            // beside the kernel's 32 KiB of stage and reduction buffers): 8B
-            // down at 3 / 4 / 5 tokens 10.0 / 10.3 / 10.3 -> 7.7 / 8.0 / 8.3 us
-            // (two repetitions, the same bits)
-            if constexpr (XBF16 && MT == 1)
+            // bf16 activations in LDS beside the kernel's 32 KiB of stage and
+            // reduction buffers: up to 5 tokens all of K (5 x 24 KiB), up to
+            // 10 one K half at a time, up to 15 one third. 8B down at 3 / 4 /
+            // 5 tokens 10.0 / 10.3 / 10.3 -> 7.7-8.0 / 8.0-8.3 / 8.3-8.7 us,
+            // at 6 / 8 / 10 / 11 tokens 11.0 / 12.4 / 13.2 / 13.8 -> 9.4 /
+            // 10.2 / 10.9 / 11.6 us (repetitions on two machines, the same bits)
+            if constexpr (XBF16 && MT == 1) {
                 if (a.m <= 5) return go<XBF16, 1, U, 12 / U, TW, false, 1, 5>(a, cus);
+                if (a.m <= 10) return go<XBF16, 1, U, 12 / U, TW, false, 1, 10, 2>(a, cus);
+                if (a.m <= 15) return go<XBF16, 1, U, 12 / U, TW, false, 1, 15, 3>(a, cus);
+            }
             return go<XBF16, MT, U, 12 / U, TW, false>(a, cus);
         default: return hipErrorNotSupported;
     }

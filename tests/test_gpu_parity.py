@@ -989,30 +989,33 @@ def test_skinny_resident_activations(mx4, ctx, oracle, n, k):
             assert_close(y[:, rows], ref, f"skinny {k}->{n} m={m} xtype={xtype}")
 
 
-@pytest.mark.parametrize("n", [333, 4096 + 5])
+@pytest.mark.parametrize("n", [333, 4096 + 5, 8192 + 37])
 def test_skinny_lds_activations(mx4, ctx, oracle, n):
-    """K = 12288 with 1..5 bf16 token rows: the skinny kernel keeps the
-    activations in LDS (padded rows) and reads each unit's operand fragments
-    from there. Ragged N against the oracle on every row, and one-hot
-    activations (one column per token) return the decoded weights bit for bit,
-    which pins the LDS row and element placement; f32 activations (the
-    per-unit loading form) on the same weights."""
+    """K = 12288 with 1..11 bf16 token rows: the skinny kernel keeps the
+    activations in LDS (padded rows; all of K up to 5 tokens, K halves up to
+    10, thirds at 11, each slice loaded when its first unit comes up) and reads
+    each unit's operand fragments from there. Ragged N against the oracle on
+    every row (several 16-row tiles per workgroup on the wider N, so every
+    slice is reloaded per tile), and one-hot activations (one column per token,
+    drawn across all slices) return the decoded weights bit for bit, which pins
+    the LDS row, slice and element placement; f32 activations (the per-unit
+    loading form) on the same weights."""
     k = 12288
     say(f"skinny LDS x {k}->{n}")
     rng = np.random.default_rng(n)
     w = ctx.synth_weight(1300 + n % 7, n, k, 0.02)
     packed, scales = ctx.download_weight(w)
-    for m in (1, 2, 3, 4, 5):
+    for m in (1, 2, 3, 4, 5, 6, 8, 10, 11):
         x = oracle.bf16_to_f32(oracle.synth_bf16(1310 + m, 1.0, m * k)).reshape(m, k)
         ref = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
         assert_close(run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.BF16), ref, f"skinny LDS x m={m} n={n}")
-        if m == 5:
+        if m in (5, 11):
             assert_close(run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.F32), ref, f"skinny f32 x m={m} n={n}")
     p2 = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
     s2 = rng.integers(110, 140, (n, k // 32), dtype=np.uint8)
     w2 = ctx.upload_weight(p2, s2, n, k)
     dec = oracle.dequantize(p2, s2)
-    for m in (1, 3, 5):
+    for m in (1, 3, 5, 7, 10, 11):
         cols = rng.choice(k, m, replace=False)
         x = np.zeros((m, k), np.float32)
         x[np.arange(m), cols] = 1.0
