@@ -57,7 +57,7 @@ hipError_t launch_embed(const uint8_t* packed, const uint8_t* scales, const uint
 
 // Exact skinny path (1 <= m <= 32) on bf16 MFMA with decoded weights.
 bool skinny_supported(uint32_t m, uint32_t k);
-// Device scratch of the split-K launches (bf16 x; K = 12288 from 12 tokens,
+// Device scratch of the split-K launches (bf16 x; K = 12288 from 17 tokens,
 // K = 4096 from 17 tokens on 1024-row weights (four ways) and, two ways,
 // from 20 tokens on ring-length weights only (gate/up; q/o at K = 4096 run
 // unsplit), when the partial tiles fit): part_tiles partial tiles of 1 KiB and

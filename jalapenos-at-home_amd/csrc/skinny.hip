@@ -26,10 +26,10 @@
 //    resident): KS workgroups share a tile, each over one K slice with its
 //    slice's activations resident, and the last of them to finish adds the KS
 //    partial tiles in slice order;
-//  * up to 15 bf16 tokens at K = 12288 (XLM, NP): the activations are loaded
-//    into LDS by the workgroup -- all of K up to 5 tokens, one K half or third
-//    at a time above -- and each unit's operand fragments read from there,
-//    instead of every unit loading its 16-token fragments from the L2.
+//  * up to 16 bf16 tokens at K = 12288 (XLM, NP): the activations are loaded
+//    into LDS by the workgroup -- all of K up to 5 tokens, one K half, third
+//    or sixth at a time above -- and each unit's operand fragments read from
+//    there, instead of every unit loading its 16-token fragments from the L2.
 #include <type_traits>
 
 #include "mx4_device.h"
@@ -573,33 +573,30 @@ hipError_t go_k(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
         // they need 16 or 12 waves per workgroup and measured slower (down)
         case 8192: return go<XBF16, MT, U, 8 / U, TW, false>(a, cus);
         case 12288:
-            // bf16 x from 12 tokens on: four workgroups per tile, each over a
-            // 3072-wide K slice with its activations resident and the
-            // three-tile ring, so that every workgroup reads a quarter of x
-            // instead of all of it. 8B down at 8 / 12 / 16 / 24 / 32 tokens:
-            // 11.8 / 14.2 / 16.5 / 26.8 / 32.7 unsplit; split, with the
-            // agent-scope fences of the arrival count (about 2 us per
-            // launch), 13.5 at 8 and 14.3 / 18.6 at 16 / 32 (12 waves of two
-            // chunks for one token tile, 6 waves of four for two;
-            // three-chunk units, with half-line loads, measured 0.8-1.4 us
-            // slower). Below 12 tokens the end-of-launch count and fences
-            // cost more than the activation loads they save.
-            if constexpr (XBF16)
-                if (a.m >= 12 && split_fits(a, cus, sc, 4, MT)) {
-                    if constexpr (MT == 1) return go<XBF16, 1, 2, 1, 12, true, 4>(a, cus, sc);
-                    else return go<XBF16, MT, 4, 1, 6, true, 4>(a, cus, sc);
-                }
-            // bf16 activations in LDS beside the kernel's 32 KiB of stage and
-            // reduction buffers: up to 5 tokens all of K (5 x 24 KiB), up to
-            // 10 one K half at a time, up to 15 one third. 8B down at 3 / 4 /
-            // 5 tokens 10.0 / 10.3 / 10.3 -> 7.7-8.0 / 8.0-8.3 / 8.3-8.7 us,
-            // at 6 / 8 / 10 / 11 tokens 11.0 / 12.4 / 13.2 / 13.8 -> 9.4 /
-            // 10.2 / 10.9 / 11.6 us (repetitions on two machines, the same bits)
+            // bf16 activations of one token tile (up to 16 tokens) in LDS
+            // beside the kernel's 32 KiB of stage and reduction buffers: all
+            // of K up to 5 tokens (5 x 24 KiB), one K half at a time up to
+            // 10, one third up to 15, one sixth at 16. 8B down at 3 / 4 / 5
+            // tokens 10.0 / 10.3 / 10.3 -> 7.7-8.0 / 8.0-8.3 / 8.3-8.7 us, at
+            // 6 / 8 / 10 / 11 tokens 11.0 / 12.4 / 13.2 / 13.8 -> 9.4 / 10.2 /
+            // 10.9 / 11.6 us against the per-unit activation loads, and at 12
+            // / 14 / 16 tokens 14.3 / 14.2 / 14.5 -> 12.4 / 13.0 / 13.8 us
+            // against the split-K form (repetitions on two machines).
             if constexpr (XBF16 && MT == 1) {
                 if (a.m <= 5) return go<XBF16, 1, U, 12 / U, TW, false, 1, 5>(a, cus);
                 if (a.m <= 10) return go<XBF16, 1, U, 12 / U, TW, false, 1, 10, 2>(a, cus);
                 if (a.m <= 15) return go<XBF16, 1, U, 12 / U, TW, false, 1, 15, 3>(a, cus);
+                return go<XBF16, 1, U, 12 / U, TW, false, 1, 16, 6>(a, cus);
             }
+            // bf16 x, two token tiles (17-32 tokens): four workgroups per
+            // tile, each over a 3072-wide K slice with its activations resident
+            // and the three-tile ring, so that every workgroup reads a quarter
+            // of x instead of all of it (6 waves of four chunks; 8B down at 32
+            // tokens 32.7 -> 18.6 us with the agent-scope fences of the
+            // arrival count, about 2 us per launch; three-chunk units, with
+            // half-line loads, measured 0.8-1.4 us slower)
+            if constexpr (XBF16 && MT == 2)
+                if (split_fits(a, cus, sc, 4, MT)) return go<XBF16, MT, 4, 1, 6, true, 4>(a, cus, sc);
             return go<XBF16, MT, U, 12 / U, TW, false>(a, cus);
         default: return hipErrorNotSupported;
     }

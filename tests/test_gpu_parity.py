@@ -991,9 +991,10 @@ def test_skinny_resident_activations(mx4, ctx, oracle, n, k):
 
 @pytest.mark.parametrize("n", [333, 4096 + 5, 8192 + 37])
 def test_skinny_lds_activations(mx4, ctx, oracle, n):
-    """K = 12288 with 1..11 bf16 token rows: the skinny kernel keeps the
+    """K = 12288 with 1..16 bf16 token rows: the skinny kernel keeps the
     activations in LDS (padded rows; all of K up to 5 tokens, K halves up to
-    10, thirds at 11, each slice loaded when its first unit comes up) and reads
+    10, thirds up to 15, sixths at 16, each slice loaded when its first unit
+    comes up) and reads
     each unit's operand fragments from there. Ragged N against the oracle on
     every row (several 16-row tiles per workgroup on the wider N, so every
     slice is reloaded per tile), and one-hot activations (one column per token,
@@ -1005,17 +1006,17 @@ def test_skinny_lds_activations(mx4, ctx, oracle, n):
     rng = np.random.default_rng(n)
     w = ctx.synth_weight(1300 + n % 7, n, k, 0.02)
     packed, scales = ctx.download_weight(w)
-    for m in (1, 2, 3, 4, 5, 6, 8, 10, 11):
+    for m in (1, 2, 3, 4, 5, 6, 8, 10, 11, 12, 15, 16):
         x = oracle.bf16_to_f32(oracle.synth_bf16(1310 + m, 1.0, m * k)).reshape(m, k)
         ref = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
         assert_close(run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.BF16), ref, f"skinny LDS x m={m} n={n}")
-        if m in (5, 11):
+        if m in (5, 16):
             assert_close(run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.F32), ref, f"skinny f32 x m={m} n={n}")
     p2 = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
     s2 = rng.integers(110, 140, (n, k // 32), dtype=np.uint8)
     w2 = ctx.upload_weight(p2, s2, n, k)
     dec = oracle.dequantize(p2, s2)
-    for m in (1, 3, 5, 7, 10, 11):
+    for m in (1, 3, 5, 7, 10, 11, 13, 16):
         cols = rng.choice(k, m, replace=False)
         x = np.zeros((m, k), np.float32)
         x[np.arange(m), cols] = 1.0
@@ -1079,8 +1080,9 @@ def test_skinny_tile_ring(mx4, ctx, oracle, n, k):
 @pytest.mark.parametrize("n,k", [(4096 + 5, 12288), (8192 + 37, 12288), (1024 - 5, 4096), (4096 + 5, 4096),
                                  (8192 + 5, 4096)])
 def test_skinny_split_k(mx4, ctx, oracle, n, k):
-    """Split K with bf16 activations: K = 12288 from 12 tokens on (four
-    workgroups per 16-row tile, each over a quarter of K), K = 4096 from 17 on
+    """Split K with bf16 activations: K = 12288 from 17 tokens on (four
+    workgroups per 16-row tile, each over a quarter of K; up to 16 tokens the
+    activations sit in LDS instead), K = 4096 from 17 on
     (four slices when every CU gets one tile, as for 1019 rows; two from 20
     tokens on for weights long enough for the tile ring, as 8197 rows; 4101
     rows stay unsplit); the last workgroup of a tile adds the partials (fewer

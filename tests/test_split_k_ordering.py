@@ -42,11 +42,11 @@ def kernels(asm):
 
 
 def split_ks(name):
-    # template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS>:
-    # the mangled name ends in ...Lb?ELi<KS>EEE
-    m = re.search(r"Lb[01]ELi(\d+)EEE", name)
-    assert m, name
-    return int(m.group(1))
+    # template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS,
+    # int XLM, int NP>: KS is the integer right after the last bool (RESX)
+    m = re.findall(r"Lb[01]ELi(\d+)E", name)
+    assert len(m) == 2, name
+    return int(m[-1])
 
 
 def test_split_instances_carry_release_and_acquire(skinny_asm):
