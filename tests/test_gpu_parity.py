@@ -1348,12 +1348,15 @@ def _to_fragments(codes, scales, fp8):
 
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
 @pytest.mark.parametrize("xtype", ["bf16", "f32"])
-def test_prefill_quantize_fragments_bit_exact(mx4, ctx, oracle, act, xtype):
+@pytest.mark.parametrize("k", [768, 8448])
+def test_prefill_quantize_fragments_bit_exact(mx4, ctx, oracle, act, xtype, k):
     """mx4_prefill_quantize = the oracle's quantizer (python/quantize_mxfp4.py:18-39,
     or the E4M3 rule) permuted into the fragment order, byte for byte, with the
-    padding rows of the last group zero; ragged rows, exact midpoints, signed zeros."""
+    padding rows of the last group zero; ragged rows, exact midpoints, signed zeros.
+    K = 768 takes the one-k-step workgroups, K = 8448 (33 scale quads) the
+    whole-quad ones."""
     rng = np.random.default_rng(17)
-    m, k = 45, 768
+    m = 45
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[3, :64] = (rng.integers(-24, 25, 64) * 0.25).astype(np.float32)
     x[5, :32] = -0.0
@@ -1377,19 +1380,22 @@ def test_prefill_quantize_fragments_bit_exact(mx4, ctx, oracle, act, xtype):
 
 
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
-def test_prefill_non_finite_activations_give_nan_rows(mx4, ctx, oracle, act):
+@pytest.mark.parametrize("k", [512, 8448])
+def test_prefill_non_finite_activations_give_nan_rows(mx4, ctx, oracle, act, k):
     """A token row holding inf or NaN: the reference's sums over it are inf or
     NaN (engine/src/lib.rs:240-266); requantized here, its blocks carry the E8M0
-    NaN scale, so every output of that row is NaN. The other rows are unaffected."""
-    m, n, k = 40, 96, 512
+    NaN scale, so every output of that row is NaN. The other rows are unaffected.
+    (K = 8448: the requantizer's whole-quad workgroups, the last column too.)"""
+    m, n = 40, 96
     w = ctx.synth_weight(33, n, k, 0.02)
     packed, scales = ctx.download_weight(w)
     x = oracle.bf16_to_f32(oracle.synth_bf16(34, 1.0, m * k)).reshape(m, k)
     x[3, 100] = np.inf
     x[17, 5] = np.nan
+    x[20, k - 1] = -np.inf
     y = _run_prefill(mx4, ctx, x, w, act, mx4.F32)
-    assert np.all(np.isnan(y[3])) and np.all(np.isnan(y[17]))
-    ok = np.setdiff1d(np.arange(m), [3, 17])
+    assert np.all(np.isnan(y[3])) and np.all(np.isnan(y[17])) and np.all(np.isnan(y[20]))
+    ok = np.setdiff1d(np.arange(m), [3, 17, 20])
     ref, _ = _prefill_ref(oracle, x[ok], packed, scales, act)
     assert_close(y[ok], ref, f"prefill {act} finite rows")
 
