@@ -288,6 +288,38 @@ def time_skinny(ctx, ms=(1, 2, 4, 8, 16, 32)) -> dict:
     return out
 
 
+def time_skinny_groups(ctx, ms=(2, 4, 8, 16, 32), separate: dict | None = None) -> dict:
+    """The verify step's grouped launches: q|k|v and gate|up at M token rows
+    through mx4_matmul_group (one launch of the few-token GEMV or the skinny
+    kernel over every weight's rows), over >= 512 MiB of cold copies; per-call
+    latency, effective GB/s, and the sum of the members' separate calls from
+    time_skinny (`separate`) when given."""
+    dims = {name: (n, k) for name, n, k in LAYER}
+    out = {}
+    for gi, (label, members) in enumerate((("qkv", ["q", "k", "v"]), ("gate_up", ["gate", "up"]))):
+        shapes = [dims[nm] for nm in members]
+        k = shapes[0][1]
+        arena, copies = rotation(ctx, shapes, 45000 + 1000 * gi)
+        row = {}
+        for m in ms:
+            xb = ctx.buffer(m * k * 2)
+            ctx.synth_bf16(2, 1.0, m * k, xb)
+            ys = [ctx.buffer(m * n * 4) for n, _ in shapes]
+            t = time_pass(ctx, lambda: [ctx.matmul_group(xb.ptr, mx4hip.BF16, m, ws, [y.ptr for y in ys])
+                                        for ws in copies], len(copies))
+            b = sum(gemv_bytes(m, n, k) for n, _ in shapes) - (len(shapes) - 1) * m * k * 2  # x read once
+            e = {"us": t["us"], "GBps": round(b / (t["us"] * 1e-6) / 1e9, 1)}
+            if separate and all(f"M{m}" in separate.get(nm, {}) for nm in members):
+                e["separate_us"] = round(sum(separate[nm][f"M{m}"]["us"] for nm in members), 3)
+            row[f"M{m}"] = e
+            for y in ys:
+                y.free()
+            xb.free()
+        out[label] = row
+        arena.release()
+    return out
+
+
 def time_mfma_ceiling(ctx) -> dict:
     """What the matrix cores sustain on the prefill GEMM's instruction:
     scaled FP4 MFMAs back to back on every SIMD (mx4_mfma_ceiling), on random
@@ -1321,6 +1353,8 @@ def main() -> int:
     if not args.no_skinny:
         log("skinny (speculative verify) timing")
         extra["skinny"] = time_skinny(ctx)
+        log("grouped verify launches (q|k|v, gate|up) timing")
+        extra["skinny_group"] = time_skinny_groups(ctx, separate=extra["skinny"])
 
     prefill_top = None
     if not args.no_prefill:

@@ -199,8 +199,14 @@ mx4_status mx4_matmul_path(mx4_context *ctx, const void *x_dev, mx4_dtype x_type
                            const mx4_weight *w, float *y_dev, mx4_path path);
 /* Up to 4 weights of the same width that read the same activations (q|k|v,
  * gate|up) in one launch: y_dev[i][m][w[i].rows] = x . W_i^T. For m == 1 this
- * is one GEMV over the concatenated rows; otherwise the projections run one
- * after another. Same arithmetic as mx4_matmul. */
+ * is one GEMV over the concatenated rows; for 2 <= m <= 32 (a speculative
+ * verify step) one launch of the few-token GEMV or the skinny kernel over all
+ * the weights' rows, chosen as mx4_matmul would choose for one weight of the
+ * group's total rows; otherwise (and for bf16 weights or scale bytes outside
+ * 2..252) the projections run one after another. Same arithmetic as
+ * mx4_matmul: exact products, f32 sums, so each output equals mx4_matmul's
+ * for its weight within f32 rounding (the same bits when both choose the same
+ * kernel instance). */
 mx4_status mx4_matmul_group(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m,
                             const mx4_weight *const *w, float *const *y_dev, uint32_t count);
 

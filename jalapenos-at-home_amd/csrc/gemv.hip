@@ -264,8 +264,20 @@ __device__ __forceinline__ void load_rowset_in(const Seg& sgm, uint32_t rs, uint
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool XBF16, int WG, int BPL, int R>
-__device__ __forceinline__ void load_rowset(const Segs& sg, uint32_t rs, uint32_t rowsets, uint32_t t,
+// One weight: the segment table of a single-weight launch of the few-token
+// GEMV, small enough for its fields to arrive preloaded in SGPRs (the first
+// weight load then waits for no scalar memory round trip).
+struct OneSeg {
+    const uint8_t* packed;
+    const uint8_t* scales;
+    float* y;
+    uint32_t n;
+};
+
+__device__ __forceinline__ Seg pick_seg(const OneSeg& o, uint32_t) { return Seg{o.packed, o.scales, o.y, o.n, 0u}; }
+
+template <bool XBF16, int WG, int BPL, int R, class SG>
+__device__ __forceinline__ void load_rowset(const SG& sg, uint32_t rs, uint32_t rowsets, uint32_t t,
                                             uint32_t row_bytes, uint32_t nblk, RowSet<XBF16, BPL, R>& out) {
     load_rowset_in<XBF16, WG, BPL, R>(pick_seg(sg, rs), rs, rowsets, t, row_bytes, nblk, out);
 }
@@ -617,12 +629,10 @@ __device__ __forceinline__ void rows_dot_mt(const LaneX<true, BPL> (&xr)[MT], co
 
 // SHARED: several teams per workgroup share one LDS copy of the token rows
 // (tpw > 1); otherwise each team loads its own into registers (tpw == 1).
-template <int WG, int BPL, int R, int MT, bool SHARED>
-__global__ __launch_bounds__(512) void gemv_mt_kernel(const uint8_t* __restrict__ packed,
-                                                      const uint8_t* __restrict__ scales,
-                                                      const void* __restrict__ x, uint32_t m, uint32_t n,
-                                                      uint32_t rowsets, uint32_t tpw, uint32_t grid,
-                                                      float* __restrict__ y) {
+// SG: OneSeg (one weight) or Segs (a group: each weight a run of row-sets).
+template <int WG, int BPL, int R, int MT, bool SHARED, class SG>
+__global__ __launch_bounds__(512) void gemv_mt_kernel(const SG sg, const void* __restrict__ x, uint32_t m,
+                                                      uint32_t rowsets, uint32_t tpw, uint32_t grid) {
     constexpr int RM = R * MT;
     static_assert(RM == 2 || RM == 4 || RM == 8, "rows x tokens per team");
     constexpr uint32_t T = 64 * WG;
@@ -630,20 +640,6 @@ __global__ __launch_bounds__(512) void gemv_mt_kernel(const uint8_t* __restrict_
     const uint32_t team = __builtin_amdgcn_readfirstlane(threadIdx.x / T);
     const uint32_t t = threadIdx.x % T, lane = t % 64;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t / 64);
-    Segs sg;
-#pragma unroll
-    for (int q = 0; q < kMaxSegs; ++q) {
-        sg.packed[q] = packed;
-        sg.scales[q] = scales;
-        sg.y[q] = y;
-        sg.n[q] = n;
-        sg.first[q + 1] = rowsets;
-    }
-    sg.first[0] = 0;
-    sg.count = 1;
-    sg.rowsets = rowsets;
-    sg.am_partial = nullptr;
-
     const uint32_t stride = grid * tpw;
     const uint32_t first = blockIdx.x * tpw;  // the workgroup's first team visits the most row-sets
     uint32_t rs = first + team;
@@ -703,7 +699,11 @@ __global__ __launch_bounds__(512) void gemv_mt_kernel(const uint8_t* __restrict_
         float acc[RM];
 #pragma unroll
         for (int i = 0; i < R; ++i) rows_dot_mt<BPL, MT>(xr, cur.w[i], cur.s[i], acc + i * MT);
-        const uint32_t row0 = set * R;  // past n for a team beyond the last row-set: nothing is written
+        // the row-set's weight; past its n for a team beyond the last
+        // row-set, so nothing is written
+        const Seg sgm = pick_seg(sg, set);
+        const uint32_t row0 = (set - sgm.first) * R, n = sgm.n;
+        float* const y = sgm.y;
         const float total = wave_reduce_rows<RM>(acc, lane);
         const uint32_t idx = reduced_row_of_lane<RM>(lane);
         if constexpr (WG == 1) {
@@ -1048,7 +1048,24 @@ static void mt_default(uint32_t rowsets, int wg, int cus, bool x_fits, uint32_t&
 // the partial sums within 64 KiB).
 template <int WG, int BPL, int R, int MT>
 static hipError_t go_mt(const GemvArgs& a, int cus, uint32_t teams, uint32_t tpw) {
-    const uint32_t rowsets = (a.n + R - 1) / R;
+    // a group: each weight a run of row-sets
+    Segs sg{};
+    uint32_t rowsets = (a.n + R - 1) / R;
+    if (a.group) {
+        sg.count = a.group->count;
+        sg.first[0] = 0;
+        for (uint32_t s = 0; s < sg.count; ++s) {
+            sg.packed[s] = a.group->packed[s];
+            sg.scales[s] = a.group->scales[s];
+            sg.y[s] = a.group->y[s];
+            sg.n[s] = a.group->n[s];
+            sg.first[s + 1] = sg.first[s] + (sg.n[s] + R - 1) / R;
+        }
+        for (uint32_t s = sg.count; s < (uint32_t)kMaxSegs; ++s) sg.first[s + 1] = sg.first[sg.count];
+        rowsets = sg.first[sg.count];
+        sg.rowsets = rowsets;
+    }
+    const OneSeg one{a.packed, a.scales, a.y, a.n};
     constexpr uint32_t xbytes = MT * 2048u * WG * BPL * 2;
     if (teams == 0 || tpw == 0)
         mt_default(rowsets, WG, cus, xbytes + (8 / WG) * 2 * WG * R * MT * 4 <= 65536, teams, tpw);
@@ -1057,12 +1074,21 @@ static hipError_t go_mt(const GemvArgs& a, int cus, uint32_t teams, uint32_t tpw
     if (teams > rowsets) teams = rowsets;
     const uint32_t grid = (teams + tpw - 1) / tpw;
     const size_t lds = (tpw > 1 ? xbytes : 0) + (size_t)tpw * 2 * WG * R * MT * sizeof(float);
-    if (tpw > 1)
-        hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, true>), dim3(grid), dim3(64 * WG * tpw), lds, a.stream,
-                           a.packed, a.scales, a.x, a.m, a.n, rowsets, tpw, grid, a.y);
-    else
-        hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, false>), dim3(grid), dim3(64 * WG * tpw), lds, a.stream,
-                           a.packed, a.scales, a.x, a.m, a.n, rowsets, tpw, grid, a.y);
+    if (a.group) {
+        if (tpw > 1)
+            hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, true, Segs>), dim3(grid), dim3(64 * WG * tpw), lds,
+                               a.stream, sg, a.x, a.m, rowsets, tpw, grid);
+        else
+            hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, false, Segs>), dim3(grid), dim3(64 * WG * tpw), lds,
+                               a.stream, sg, a.x, a.m, rowsets, tpw, grid);
+    } else {
+        if (tpw > 1)
+            hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, true, OneSeg>), dim3(grid), dim3(64 * WG * tpw), lds,
+                               a.stream, one, a.x, a.m, rowsets, tpw, grid);
+        else
+            hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, false, OneSeg>), dim3(grid), dim3(64 * WG * tpw), lds,
+                               a.stream, one, a.x, a.m, rowsets, tpw, grid);
+    }
     return hipGetLastError();
 }
 
@@ -1071,7 +1097,14 @@ bool gemv_mt_supported(uint32_t m, uint32_t k, bool x_bf16) {
 }
 
 hipError_t launch_gemv_mt(const GemvArgs& a, int cus, uint32_t teams, uint32_t tpw) {
-    if (!gemv_mt_supported(a.m, a.k, a.x_bf16) || a.n == 0) return hipErrorNotSupported;
+    if (!gemv_mt_supported(a.m, a.k, a.x_bf16)) return hipErrorNotSupported;
+    if (a.group) {
+        if (a.group->count < 1 || a.group->count > (uint32_t)kMaxSegs) return hipErrorNotSupported;
+        for (uint32_t s = 0; s < a.group->count; ++s)
+            if (a.group->n[s] == 0) return hipErrorNotSupported;
+    } else if (a.n == 0) {
+        return hipErrorNotSupported;
+    }
 #define MX4_MT(K, W, B)                                                                                  \
     if (a.k == K) return a.m <= 2 ? go_mt<W, B, 2, 2>(a, cus, teams, tpw) : go_mt<W, B, 2, 4>(a, cus, teams, tpw);
     MX4_MT(2048, 1, 1)

@@ -7,6 +7,7 @@
 namespace mx4 {
 
 // y[m, n] = x[m, k] . dequant(W[n, k])^T on one stream.
+struct GemvGroup;
 struct GemvArgs {
     const uint8_t* packed;  // [n][k/2]
     const uint8_t* scales;  // [n][k/32]
@@ -15,6 +16,11 @@ struct GemvArgs {
     uint32_t m, n, k;
     bool x_bf16;
     hipStream_t stream;
+    // The few-token GEMV and the skinny kernel: when set, one launch over the
+    // group's weights (all of width k, sharing x; y[s] is [m][n[s]]) instead
+    // of packed / scales / y / n, each weight's rows a run of whole row-sets
+    // or 16-row tiles of the launch.
+    const GemvGroup* group = nullptr;
 };
 
 bool gemv_m1_supported(uint32_t k);

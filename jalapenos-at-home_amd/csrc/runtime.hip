@@ -806,6 +806,40 @@ mx4_status mx4_matmul_group(mx4_context* ctx, const void* x, mx4_dtype xt, uint3
         if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
         return MX4_OK;
     }
+    // 2..32 token rows (a speculative verify step): one launch of the
+    // few-token GEMV or the skinny kernel over all the weights' rows, chosen
+    // as mx4_matmul chooses for one weight of the group's total rows
+    bool stored = true;
+    uint32_t total = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        stored &= w[i]->bf16 == nullptr;
+        total += w[i]->rows;
+    }
+    const uint32_t k = w[0]->cols;
+    const bool tokens = mx4::gemv_mt_supported(m, k, xt == MX4_BF16) &&
+                        ((m == 2 && total < 65536) || (total <= 1024 && k >= 4096));
+    const bool skinny = !tokens && m >= 2 && mx4::skinny_supported(m, k);
+    if (count > 1 && stored && foldable && (tokens || skinny)) {
+        mx4::GemvGroup gg{};
+        gg.count = count;
+        gg.k = k;
+        gg.x = x;
+        gg.x_bf16 = xt == MX4_BF16;
+        gg.stream = ctx->stream;
+        for (uint32_t i = 0; i < count; ++i) {
+            gg.packed[i] = w[i]->packed;
+            gg.scales[i] = w[i]->scales;
+            gg.y[i] = y[i];
+            gg.n[i] = w[i]->rows;
+        }
+        mx4::GemvArgs a{w[0]->packed, w[0]->scales, x, y[0], m, w[0]->rows, k, xt == MX4_BF16, ctx->stream};
+        a.group = &gg;
+        const hipError_t e =
+            tokens ? mx4::launch_gemv_mt(a, ctx->cus)
+                   : mx4::launch_skinny(a, ctx->cus, {ctx->split_part, ctx->split_count, kSplitPartTiles, kSplitCounts});
+        if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
+        return MX4_OK;
+    }
     for (uint32_t i = 0; i < count; ++i) {
         mx4_status st = run_matmul(ctx, x, xt, m, w[i], y[i], MX4_PATH_AUTO);
         if (st != MX4_OK) return st;

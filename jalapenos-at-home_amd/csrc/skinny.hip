@@ -111,11 +111,51 @@ __device__ __forceinline__ void split3(const f32x4 a, const f32x4 b, bf16x8& hi,
 // ahead of the MFMAs, or, with one unit per tile, two tiles ahead. After a
 // tile's last unit the TW partial 16x16 tiles are summed through LDS
 // (double-buffered: one barrier per tile).
-template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS, int XLM = 0, int NP = 1>
-__global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restrict__ packed,
-                                                         const uint8_t* __restrict__ scales,
-                                                         const void* __restrict__ x, float* __restrict__ y,
-                                                         uint32_t m, uint32_t n, float* __restrict__ part,
+// The weights of a launch. One weight (OneTiles: small enough for its fields
+// to arrive preloaded in SGPRs), or up to four of one width sharing x
+// (TileSegs: weight s owns the 16-row tiles [first[s], first[s + 1]) of the
+// launch; q|k|v or gate|up of a few-token verify step in one launch). A
+// tile's weight is picked with uniform selects, as in the GEMV.
+struct TileSeg {
+    const uint8_t* packed;
+    const uint8_t* scales;
+    float* y;
+    uint32_t n, first;
+};
+struct OneTiles {
+    const uint8_t* packed;
+    const uint8_t* scales;
+    float* y;
+    uint32_t n;
+};
+struct TileSegs {
+    const uint8_t* packed[4];
+    const uint8_t* scales[4];
+    float* y[4];
+    uint32_t n[4];
+    uint32_t first[4];
+    uint32_t count;
+};
+__device__ __forceinline__ TileSeg pick_tiles(const OneTiles& o, uint32_t) {
+    return TileSeg{o.packed, o.scales, o.y, o.n, 0u};
+}
+__device__ __forceinline__ TileSeg pick_tiles(const TileSegs& sg, uint32_t tile) {
+    TileSeg s{sg.packed[0], sg.scales[0], sg.y[0], sg.n[0], 0u};
+#pragma unroll
+    for (int q = 1; q < 4; ++q) {
+        const bool in = q < (int)sg.count && tile >= sg.first[q];
+        s.packed = in ? sg.packed[q] : s.packed;
+        s.scales = in ? sg.scales[q] : s.scales;
+        s.y = in ? sg.y[q] : s.y;
+        s.n = in ? sg.n[q] : s.n;
+        s.first = in ? sg.first[q] : s.first;
+    }
+    return s;
+}
+
+template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS, int XLM = 0, int NP = 1, class SG = OneTiles>
+__global__ __launch_bounds__(64 * TW) void skinny_kernel(const SG sg, const void* __restrict__ x, uint32_t m,
+                                                         uint32_t tiles, float* __restrict__ part,
                                                          uint32_t* __restrict__ count) {
     constexpr uint32_t ks = 128 * U * NU * TW;  // K of one slice
     constexpr uint32_t k = ks * KS;
@@ -126,11 +166,10 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     const uint32_t lane = threadIdx.x % 64;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t col = lane % 16, g = lane / 16;
-    const uint32_t tiles = (n + 15) / 16;
     // the slice's first MX block in a row (KS divides the grid: uniform)
     const uint32_t slice = KS > 1 ? blockIdx.x % KS : 0u;
     const uint32_t kb = slice * (ks / 32);
-    const __amdgpu_buffer_rsrc_t empty = rsrc(packed, 0);
+    const __amdgpu_buffer_rsrc_t empty = rsrc(x, 0);
     const __amdgpu_buffer_rsrc_t xr = rsrc(x, m * k * (XBF16 ? 2u : 4u));
     // XLM > 0 (bf16 x, m <= XLM, rows too wide for registers): the token rows
     // live in LDS, XS bytes apart (16 bytes of padding put the 16 token rows
@@ -217,10 +256,11 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     };
     auto load = [&](uint32_t tile, uint32_t unit, Unit& out, bool xnow = true) {
         const bool valid = tile < tiles;
-        const uint32_t row0 = valid ? tile * 16 : 0;
-        const uint32_t rows = valid ? (n - row0 < 16u ? n - row0 : 16u) : 0;
-        const __amdgpu_buffer_rsrc_t wr = valid ? rsrc(packed + (size_t)row0 * row_bytes, rows * row_bytes) : empty;
-        const __amdgpu_buffer_rsrc_t sr = valid ? rsrc(scales + (size_t)row0 * nblk, rows * nblk) : empty;
+        const TileSeg sw = pick_tiles(sg, tile);
+        const uint32_t row0 = valid ? (tile - sw.first) * 16 : 0;
+        const uint32_t rows = valid ? (sw.n - row0 < 16u ? sw.n - row0 : 16u) : 0;
+        const __amdgpu_buffer_rsrc_t wr = valid ? rsrc(sw.packed + (size_t)row0 * row_bytes, rows * row_bytes) : empty;
+        const __amdgpu_buffer_rsrc_t sr = valid ? rsrc(sw.scales + (size_t)row0 * nblk, rows * nblk) : empty;
         const __amdgpu_buffer_rsrc_t xq = valid ? xr : empty;
         load_scale_run<U>(sr, col * nblk + kb + 4 * (unit * TW + wave) * U, out.s);
         const uint32_t span = 16 * kb + 64 * (unit * TW + wave) * U;  // the unit's first byte in a row
@@ -310,12 +350,13 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     // they are not kept in the per-XCD L2s; the fences below order them.
     constexpr int kDeviceScope = 0x10;
     auto write_y = [&](uint32_t tile, uint32_t j, const f32x4& sum) {
-        const uint32_t row = tile * 16 + col;
-        if (row < n) {
+        const TileSeg sw = pick_tiles(sg, tile);
+        const uint32_t row = (tile - sw.first) * 16 + col;
+        if (row < sw.n) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t tok = 16 * j + 4 * g + r;
-                if (tok < m) y[(size_t)tok * n + row] = sum[r];
+                if (tok < m) sw.y[(size_t)tok * sw.n + row] = sum[r];
             }
         }
     };
@@ -492,9 +533,18 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     }
 }
 
+// 16-row tiles of a launch: one weight's, or those of every weight of a group
+// (each weight starts a tile of its own).
+uint32_t tiles_of(const GemvArgs& a) {
+    if (!a.group) return (a.n + 15) / 16;
+    uint32_t t = 0;
+    for (uint32_t s = 0; s < a.group->count; ++s) t += (a.group->n[s] + 15) / 16;
+    return t;
+}
+
 template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS = 1, int XLM = 0, int NP = 1>
 hipError_t go(const GemvArgs& a, int cus, const SkinnyScratch& sc = {}) {
-    const uint32_t tiles = (a.n + 15) / 16;
+    const uint32_t tiles = tiles_of(a);
     // two workgroups of TW waves per CU; with one unit per tile, eight waves
     // per CU (two per SIMD: the three buffers need more than the 128 VGPRs of
     // four waves per SIMD). With split K, one workgroup per CU and KS of them
@@ -505,8 +555,24 @@ hipError_t go(const GemvArgs& a, int cus, const SkinnyScratch& sc = {}) {
     if (grid == 0) grid = 1;
     const uint32_t per = (tiles + grid - 1) / grid;
     grid = (tiles + per - 1) / per;
-    hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX, KS, XLM, NP>), dim3(grid * KS), dim3(64 * TW), 0, a.stream,
-                       a.packed, a.scales, a.x, a.y, a.m, a.n, sc.part, sc.count);
+    if (a.group) {
+        TileSegs sg{};
+        sg.count = a.group->count;
+        for (uint32_t s = 0, t = 0; s < sg.count; ++s) {
+            sg.packed[s] = a.group->packed[s];
+            sg.scales[s] = a.group->scales[s];
+            sg.y[s] = a.group->y[s];
+            sg.n[s] = a.group->n[s];
+            sg.first[s] = t;
+            t += (sg.n[s] + 15) / 16;
+        }
+        hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX, KS, XLM, NP, TileSegs>), dim3(grid * KS),
+                           dim3(64 * TW), 0, a.stream, sg, a.x, a.m, tiles, sc.part, sc.count);
+    } else {
+        hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX, KS, XLM, NP, OneTiles>), dim3(grid * KS),
+                           dim3(64 * TW), 0, a.stream, OneTiles{a.packed, a.scales, a.y, a.n}, a.x, a.m, tiles,
+                           sc.part, sc.count);
+    }
     return hipGetLastError();
 }
 
@@ -514,7 +580,7 @@ hipError_t go(const GemvArgs& a, int cus, const SkinnyScratch& sc = {}) {
 // counts a workgroup's tiles with one lane each (at most 64 tiles per
 // workgroup; the launch puts cus / KS workgroups on each slice).
 bool split_fits(const GemvArgs& a, int cus, const SkinnyScratch& sc, uint32_t ks, uint32_t mt) {
-    const uint64_t tiles = (a.n + 15) / 16;
+    const uint64_t tiles = tiles_of(a);
     uint64_t grid = (uint64_t)cus / ks;
     if (grid > tiles) grid = tiles;
     if (grid == 0) grid = 1;
@@ -525,7 +591,7 @@ bool split_fits(const GemvArgs& a, int cus, const SkinnyScratch& sc, uint32_t ks
 // The three-tile ring (bf16 activations, K 2048 or 4096) pays from two tiles
 // per workgroup at eight waves per CU (K = 2048 runs 4-wave workgroups).
 bool tile_ring(const GemvArgs& a, int cus) {
-    const uint32_t tiles = (a.n + 15) / 16;
+    const uint32_t tiles = tiles_of(a);
     const uint32_t waves = (uint32_t)(cus > 0 ? cus : 256) * 8u;
     const uint32_t tw = a.k == 2048 ? 4u : 8u;
     return a.x_bf16 && (a.k == 2048 || a.k == 4096) && tiles >= 2 * waves / tw;
@@ -561,7 +627,7 @@ hipError_t go_k(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
             // q/o the fenced split measured slower than unsplit (12.9 against
             // 12.0 us at 32 tokens).
             if constexpr (XBF16 && MT == 2) {
-                if (4 * ((a.n + 15) / 16) <= (uint32_t)cus && split_fits(a, cus, sc, 4, MT))
+                if (4 * tiles_of(a) <= (uint32_t)cus && split_fits(a, cus, sc, 4, MT))
                     return go<XBF16, MT, 2, 1, 4, true, 4>(a, cus, sc);
                 if (a.m >= 20 && tile_ring(a, cus) && split_fits(a, cus, sc, 2, MT))
                     return go<XBF16, MT, 2, 1, 8, true, 2>(a, cus, sc);
@@ -620,6 +686,11 @@ bool skinny_supported(uint32_t m, uint32_t k) {
 // at 20 / 32 tokens: 18.3 / 20.2 -> 16.1 / 16.9 us).
 hipError_t launch_skinny(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
     if (!skinny_supported(a.m, a.k)) return hipErrorNotSupported;
+    if (a.group) {
+        if (a.group->count < 1 || a.group->count > 4) return hipErrorNotSupported;
+        for (uint32_t s = 0; s < a.group->count; ++s)
+            if (a.group->n[s] == 0) return hipErrorNotSupported;
+    }
     auto one = [&](const GemvArgs& b) { return b.x_bf16 ? go_k<true, 1>(b, cus, sc) : go_k<false, 1>(b, cus, sc); };
     if (a.m <= 16) return one(a);
     if (!tile_ring(a, cus)) return a.x_bf16 ? go_k<true, 2>(a, cus, sc) : go_k<false, 2>(a, cus, sc);
@@ -631,6 +702,13 @@ hipError_t launch_skinny(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
     hi.m = a.m - 16;
     hi.x = static_cast<const uint8_t*>(a.x) + (size_t)16 * a.k * (a.x_bf16 ? 2 : 4);
     hi.y = a.y + (size_t)16 * a.n;
+    GemvGroup hg{};
+    if (a.group) {
+        // every weight's outputs from token row 16 on
+        hg = *a.group;
+        for (uint32_t s = 0; s < hg.count; ++s) hg.y[s] = a.group->y[s] + (size_t)16 * a.group->n[s];
+        hi.group = &hg;
+    }
     const hipError_t e = one(lo);
     return e != hipSuccess ? e : one(hi);
 }

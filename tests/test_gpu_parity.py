@@ -870,6 +870,55 @@ def test_group_segments_against_oracle(mx4, ctx, oracle, k, shapes):
             assert np.array_equal(f32_bits(y.download(np.float32)), f32_bits(g)), f"segment {i} xt={xt}"
 
 
+GROUP_FEW = [
+    (4096, [4096, 1024, 1024], (2, 3, 8, 17, 32)),  # 8B q|k|v: few-token GEMV at 2, skinny above, two launches past 16
+    (4096, [12288, 12288], (2, 4, 8, 20, 32)),      # 8B gate|up: the tile ring; from 20 tokens one split-K launch
+    (4096, [501, 299, 7], (3, 4)),                  # 807 rows: the few-token GEMV at 3-4 tokens, ragged row-sets
+    (4096, [1000, 70, 70], (3, 5, 16)),             # 1140 rows: skinny, a ragged tile at every weight's end
+    (2048, [2048, 1024, 1024], (2, 4, 8, 24)),      # 1.7B q|k|v
+    (4096, [40, 8, 24, 100], (2, 5, 16)),           # four tiny weights, 13 tiles
+]
+
+
+@pytest.mark.parametrize("k,shapes,ms", GROUP_FEW, ids=[f"k{k}-{'_'.join(map(str, s))}" for k, s, _ in GROUP_FEW])
+def test_group_few_tokens_against_oracle(mx4, ctx, oracle, k, shapes, ms):
+    """2..32 token rows through mx4_matmul_group: a verify step's q|k|v or
+    gate|up as one launch of the few-token GEMV or the skinny kernel, each
+    weight a run of row-sets or 16-row tiles of it. Every weight's outputs
+    against the oracle (on weights wider than 1024 rows: their first and last
+    16 rows and 64 drawn), and against separate mx4_matmul calls within f32
+    rounding; outputs start as NaN, so a tile written to the wrong weight, or
+    not written, shows. bf16 activations, and f32 ones (the skinny kernel's
+    three-term split) on the small groups."""
+    rng = np.random.default_rng(k + len(shapes))
+    ws = [ctx.synth_weight(400 + i, n, k, 0.02) for i, n in enumerate(shapes)]
+    dl = [ctx.download_weight(w) for w in ws]
+    rows = [np.arange(n) if n <= 1024 else np.unique(np.r_[0:16, n - 16:n, rng.choice(n, 64)]) for n in shapes]
+    for m in ms:
+        xb16 = oracle.synth_bf16(410 + m, 1.0, m * k)
+        x = oracle.bf16_to_f32(xb16).reshape(m, k)
+        xts = [mx4.BF16] + ([mx4.F32] if sum(shapes) <= 2048 and m >= 3 else [])
+        for xt in xts:
+            say(f"grouped few tokens k={k} shapes={shapes} m={m} xt={xt}")
+            xd = ctx.to_device(xb16 if xt == mx4.BF16 else x)
+            ys = [ctx.buffer(m * n * 4) for n in shapes]
+            for y, n in zip(ys, shapes):
+                y.upload(np.full(m * n, np.nan, np.float32))
+            ctx.matmul_group(xd.ptr, xt, m, ws, [y.ptr for y in ys])
+            grouped = [y.download(np.float32).reshape(m, n) for y, n in zip(ys, shapes)]
+            for i, ((packed, scales), n, g, r) in enumerate(zip(dl, shapes, grouped, rows)):
+                assert np.all(np.isfinite(g)), f"weight {i} m={m}: rows left unwritten"
+                ref = oracle.matmul(x, packed[r].reshape(-1), scales[r].reshape(-1))
+                assert_close(g[:, r], ref, f"grouped weight {i} m={m} xt={xt}")
+                ctx.matmul_ptr(xd.ptr, xt, m, ws[i], ys[i].ptr)
+                assert_close(g, ys[i].download(np.float32).reshape(m, n), f"grouped vs separate {i} m={m} xt={xt}")
+            for y in ys:
+                y.free()
+            xd.free()
+    for w in ws:
+        w.release()
+
+
 def test_extreme_scales_take_the_exact_path(mx4, ctx, oracle):
     """Scale bytes 0, 1 (subnormal weights) and 253, 254 (inf weights) are outside
     the converter-folding range; AUTO routes them to the exact generic kernel."""
