@@ -159,21 +159,55 @@ def build_step(ctx, layer=LAYER, lm_head=LM_HEAD, layers=LAYERS, seed0=1000):
     return weights, arena
 
 
-def enqueue_grouped_step(ctx, weights, xs, yq, layer=LAYER, layers=LAYERS):
+def enqueue_grouped_step(ctx, weights, xs, yq, layer=LAYER, layers=LAYERS, m: int = 1):
     """One decode step as the model issues it: per layer q|k|v (one grouped
-    launch on the shared x), o, gate|up (grouped), down; then lm_head."""
+    launch on the shared x), o, gate|up (grouped), down; then lm_head. With
+    m > 1, a speculative verify step over m token rows (xs and yq sized for
+    them)."""
     hidden = layer[0][2]
     inter = layer[-1][2]
     per = len(layer)
     for li in range(layers):
         lw = {name: w for (name, _, _, w) in weights[li * per:(li + 1) * per]}
-        ctx.matmul_group(xs[hidden].ptr, mx4hip.BF16, 1, [lw["q"], lw["k"], lw["v"]],
+        ctx.matmul_group(xs[hidden].ptr, mx4hip.BF16, m, [lw["q"], lw["k"], lw["v"]],
                          [yq["q"].ptr, yq["k"].ptr, yq["v"].ptr])
-        ctx.matmul_ptr(xs[hidden].ptr, mx4hip.BF16, 1, lw["o"], yq["o"].ptr)
-        ctx.matmul_group(xs[hidden].ptr, mx4hip.BF16, 1, [lw["gate"], lw["up"]], [yq["gate"].ptr, yq["up"].ptr])
-        ctx.matmul_ptr(xs[inter].ptr, mx4hip.BF16, 1, lw["down"], yq["down"].ptr)
+        ctx.matmul_ptr(xs[hidden].ptr, mx4hip.BF16, m, lw["o"], yq["o"].ptr)
+        ctx.matmul_group(xs[hidden].ptr, mx4hip.BF16, m, [lw["gate"], lw["up"]], [yq["gate"].ptr, yq["up"].ptr])
+        ctx.matmul_ptr(xs[inter].ptr, mx4hip.BF16, m, lw["down"], yq["down"].ptr)
     _, n, k, w = weights[-1]
-    ctx.matmul_ptr(xs[k].ptr, mx4hip.BF16, 1, w, yq["lm_head"].ptr)
+    ctx.matmul_ptr(xs[k].ptr, mx4hip.BF16, m, w, yq["lm_head"].ptr)
+
+
+def time_verify_step(ctx, weights, ms=(2, 4, 8, 16), steps: int = 10) -> dict:
+    """The whole 8B step at m token rows (a speculative verify step: 36 layers
+    of q|k|v and gate|up grouped, o, down, then the lm_head) recorded as one
+    pass over the decode step's resident weights; at 8 tokens also with one
+    launch per projection. GPU ms per step and GB/s over the weight bytes plus
+    activations and outputs."""
+    out = {}
+    for m in ms:
+        xs = {}
+        for k in sorted({k for (_, _, k, _) in weights}):
+            xs[k] = ctx.buffer(m * k * 2)
+            ctx.synth_bf16(3, 1.0, m * k, xs[k])
+        yq = {name: ctx.buffer(m * n * 4) for name, n, _ in LAYER + [LM_HEAD]}
+        nbytes = sum(gemv_bytes(m, n, k) for (_, n, k, _) in weights)
+        p = ctx.record(lambda: enqueue_grouped_step(ctx, weights, xs, yq, m=m))
+        ms_g = time_step(ctx, p, steps)
+        p.release()
+        row = {"gpu_ms_per_step": round(ms_g, 4), "GBps": round(nbytes / (ms_g * 1e-3) / 1e9, 1)}
+        if m == 8:
+            ys = {n: ctx.buffer(m * n * 4) for n in sorted({n for (_, n, _, _) in weights})}
+            ops = ctx.make_ops([(xs[k].ptr, mx4hip.BF16, m, w, ys[n].ptr) for (_, n, k, w) in weights])
+            p = ctx.record(lambda: ctx.matmul_batch(ops))
+            row["one_launch_per_projection_ms"] = round(time_step(ctx, p, steps), 4)
+            p.release()
+            for y in ys.values():
+                y.free()
+        out[f"M{m}"] = row
+        for b in list(xs.values()) + list(yq.values()):
+            b.free()
+    return out
 
 
 def rotation(ctx, members, seed0: int, min_bytes: int = ROTATION_BYTES) -> tuple[Arena, list]:
@@ -1355,6 +1389,8 @@ def main() -> int:
         extra["skinny"] = time_skinny(ctx)
         log("grouped verify launches (q|k|v, gate|up) timing")
         extra["skinny_group"] = time_skinny_groups(ctx, separate=extra["skinny"])
+        log("verify step timing (the whole 8B step at 2-16 token rows)")
+        extra["verify_step"] = time_verify_step(ctx, weights)
 
     prefill_top = None
     if not args.no_prefill:
