@@ -1215,6 +1215,23 @@ def main() -> int:
                 ctx.synchronize()
                 plan.append([name, m, n, k, len(copies), VERIFY_REPS])
             arena.release()
+        # the grouped launches of a verify step (mx4_matmul_group): n is the
+        # group's rows, whose bytes per call are one x read and every output
+        dims = {name: (n, k) for name, n, k in LAYER}
+        for gi, (label, members) in enumerate((("q|k|v", ["q", "k", "v"]), ("gate|up", ["gate", "up"]))):
+            shapes = [dims[nm] for nm in members]
+            k = shapes[0][1]
+            arena, copies = rotation(ctx, shapes, 45000 + 1000 * gi)
+            for m in (2, 4, 8, 16, 32):
+                xb = ctx.buffer(m * k * 2)
+                ctx.synth_bf16(2, 1.0, m * k, xb)
+                ys = [ctx.buffer(m * n * 4) for n, _ in shapes]
+                for _ in range(VERIFY_REPS):
+                    for ws in copies:
+                        ctx.matmul_group(xb.ptr, mx4hip.BF16, m, ws, [y.ptr for y in ys])
+                ctx.synchronize()
+                plan.append([label, m, sum(n for n, _ in shapes), k, len(copies), VERIFY_REPS])
+            arena.release()
         write_stamp(args.stamp, {"profile_verify": True, "plan": plan})
         ctx.close()
         return 0
