@@ -919,6 +919,41 @@ def test_group_few_tokens_against_oracle(mx4, ctx, oracle, k, shapes, ms):
         w.release()
 
 
+def test_group_few_tokens_replayed(mx4, ctx, oracle):
+    """Grouped verify launches recorded in a pass and replayed three times, the
+    program's own synchronizations between replays: every replay gives the
+    eager call's bits, for the few-token GEMV (2 tokens), the tile ring (8)
+    and the split-K launch whose arrival counts each launch re-arms (24
+    tokens on ring-length weights)."""
+    k = 4096
+    shapes = [12288, 12288]
+    ws = [ctx.synth_weight(420 + i, n, k, 0.02) for i, n in enumerate(shapes)]
+    for m in (2, 8, 24):
+        say(f"grouped few tokens replayed m={m}")
+        xd = ctx.to_device(oracle.synth_bf16(430 + m, 1.0, m * k))
+        ys = [ctx.buffer(m * n * 4) for n in shapes]
+
+        def run():
+            ctx.matmul_group(xd.ptr, mx4.BF16, m, ws, [y.ptr for y in ys])
+
+        run()
+        eager = [y.download(np.float32).view(np.uint32) for y in ys]
+        p = ctx.record(run)
+        for _ in range(3):
+            for y, n in zip(ys, shapes):
+                y.upload(np.full(m * n, np.nan, np.float32))
+            p.launch()
+            ctx.synchronize()
+            for y, e in zip(ys, eager):
+                assert np.array_equal(y.download(np.float32).view(np.uint32), e), m
+        p.release()
+        for y in ys:
+            y.free()
+        xd.free()
+    for w in ws:
+        w.release()
+
+
 def test_extreme_scales_take_the_exact_path(mx4, ctx, oracle):
     """Scale bytes 0, 1 (subnormal weights) and 253, 254 (inf weights) are outside
     the converter-folding range; AUTO routes them to the exact generic kernel."""
