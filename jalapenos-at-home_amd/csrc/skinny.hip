@@ -206,21 +206,52 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const SG sg, const void
     // RESX: a wave's K chunks are the same for every tile, so its activation
     // fragments for all of them are loaded once, here, instead of with every
     // tile's weights (for the lm_head that halves the bytes the kernel reads).
+    // A chunk of a token tile is 16 token rows x 256 bytes (4 MX blocks of
+    // bf16). The MFMA wants lane (col, g) to hold row col's block g as four
+    // 16-byte pieces; loaded that way, every instruction touches 64 cache
+    // lines for 16 bytes each. Instead instruction c loads rows 4c .. 4c + 3
+    // whole (lane l: row 4c + l / 16, piece l % 16, 8 full lines per
+    // instruction), and settle_x() moves each chunk into the MFMA layout
+    // through the wave's own 4 KiB of LDS, after the first tiles' weight
+    // loads are out (so only these loads are waited for). Slot 16 t + (s ^ t)
+    // holds piece s of row t: the writes and the reads of any 8 consecutive
+    // lanes fall in 8 different 16-byte bank groups.
+    static_assert(!RESX || XBF16, "resident activations are bf16");
     u32x4 xres[RESX ? NU : 1][RESX ? U : 1][RESX ? MT : 1][RESX ? XQ : 1];
+    __shared__ u32x4 xt[RESX ? TW : 1][RESX ? 256 : 1];
     if constexpr (RESX) {
 #pragma unroll
         for (int p = 0; p < NU; ++p)
 #pragma unroll
             for (int q = 0; q < U; ++q) {
-                const uint32_t blk = kb + 4 * ((p * TW + wave) * U + q) + g;
+                const uint32_t b0 = kb + 4 * ((p * TW + wave) * U + q);  // the chunk's first block
 #pragma unroll
-                for (int j = 0; j < MT; ++j) {
-                    const uint32_t off = ((16 * j + col) * k + 32 * blk) * (XBF16 ? 2u : 4u);
+                for (int j = 0; j < MT; ++j)
 #pragma unroll
-                    for (int c = 0; c < XQ; ++c) xres[p][q][j][c] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16 * c, 0, 0);
-                }
+                    for (int c = 0; c < XQ; ++c) {
+                        const uint32_t off = ((16 * j + 4 * c + lane / 16) * k + 32 * b0) * 2 + 16 * (lane % 16);
+                        xres[p][q][j][c] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+                    }
             }
     }
+    auto settle_x = [&]() {
+        if constexpr (RESX) {
+#pragma unroll
+            for (int p = 0; p < NU; ++p)
+#pragma unroll
+                for (int q = 0; q < U; ++q)
+#pragma unroll
+                    for (int j = 0; j < MT; ++j) {
+#pragma unroll
+                        for (int c = 0; c < XQ; ++c) {
+                            const uint32_t t = 4 * c + lane / 16;
+                            xt[wave][16 * t + ((lane % 16) ^ t)] = xres[p][q][j][c];
+                        }
+#pragma unroll
+                        for (int c = 0; c < XQ; ++c) xres[p][q][j][c] = xt[wave][16 * col + ((4 * g + c) ^ col)];
+                    }
+        }
+    };
     // TRANS (two or four chunks per unit): a unit's 16 rows x 64U bytes are
     // loaded as 16/U rows per instruction, 64U contiguous bytes each (whole
     // cache lines instead of one half line per row: half the memory requests),
@@ -410,6 +441,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const SG sg, const void
         Unit u[D];
 #pragma unroll
         for (int d = 0; d + 1 < D; ++d) load(tile + d * stride, 0, u[d]);
+        settle_x();
         auto step = [&](uint32_t cur, auto slot) {
             constexpr int S = decltype(slot)::value % D;
             load(cur + (D - 1) * stride, 0, u[(S + D - 1) % D]);
@@ -442,6 +474,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const SG sg, const void
         static_assert(NU % 2 == 0, "an odd unit count needs the copy-free rotation");
         Unit u[2];
         load(tile, 0, u[0]);
+        settle_x();
         if constexpr (NP == 1) {
             for (;;) {
                 const uint32_t next = tile + stride;
