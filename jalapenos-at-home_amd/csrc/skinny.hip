@@ -413,12 +413,23 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const SG sg, const void
             zero();
             return;
         }
-        if (wave < (uint32_t)MT) {
-            const uint32_t j = wave;
-            f32x4 sum = red[parity][0][j][lane];
+        // The tile's 256 MT sums, spread over 4 MT waves (a single wave
+        // summing the whole tile kept the other seven waiting at the next
+        // barrier): wave (j, g) owns the 16 rows x 4 tokens of lane group g
+        // of token tile j, lane (col, r) = (lane / 4, lane % 4) one of them,
+        // added over the waves in wave order as before, so the same bits.
+        // The reads are consecutive floats of the hand-over; each store
+        // instruction writes four 64-byte runs of rows.
+        const float* rf = reinterpret_cast<const float*>(&red[parity][0][0][0]);
+        for (uint32_t v = wave; v < 4u * MT; v += TW) {
+            const uint32_t j = v / 4, gg = v % 4, c = lane / 4, r = lane % 4;
+            const uint32_t at = (j * 64 + 16 * gg + c) * 4 + r;  // float index within one wave's hand-over
+            float sum = rf[at];
 #pragma unroll
-            for (int w = 1; w < TW; ++w) sum += red[parity][w][j][lane];
-            write_y(tile, j, sum);
+            for (int w = 1; w < TW; ++w) sum += rf[w * MT * 256 + at];
+            const TileSeg sw = pick_tiles(sg, tile);
+            const uint32_t row = (tile - sw.first) * 16 + c, tok = 16 * j + 4 * gg + r;
+            if (row < sw.n && tok < m) sw.y[(size_t)tok * sw.n + row] = sum;
         }
         parity ^= 1;
         zero();
