@@ -18,6 +18,7 @@
 //    (register double-buffering), keeping R*BPL KiB in flight per wave;
 //  * E2M1 -> bf16/f32 by the hardware converter, bf16 dot2 (or f32 FMA)
 //    accumulation, wave reduction through lane shuffles, cross-wave through LDS.
+#include <type_traits>
 #include "mx4_device.h"
 #include "mx4_kernels.h"
 
@@ -264,9 +265,13 @@ __device__ __forceinline__ void load_rowset_in(const Seg& sgm, uint32_t rs, uint
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// One weight: the segment table of a single-weight launch of the few-token
-// GEMV, small enough for its fields to arrive preloaded in SGPRs (the first
-// weight load then waits for no scalar memory round trip).
+// One weight: the segment of a single-weight launch of the few-token GEMV,
+// built in the kernel from its leading scalar arguments (which arrive
+// preloaded in SGPRs, so the first weight load waits for no scalar memory
+// round trip; a by-value struct argument ends the preloaded run). A group
+// launch passes its table as the trailing argument; NoSegs stands there for
+// one weight.
+struct NoSegs {};
 struct OneSeg {
     const uint8_t* packed;
     const uint8_t* scales;
@@ -629,10 +634,18 @@ __device__ __forceinline__ void rows_dot_mt(const LaneX<true, BPL> (&xr)[MT], co
 
 // SHARED: several teams per workgroup share one LDS copy of the token rows
 // (tpw > 1); otherwise each team loads its own into registers (tpw == 1).
-// SG: OneSeg (one weight) or Segs (a group: each weight a run of row-sets).
+// SG: NoSegs (one weight: packed, scales, n, y) or Segs (a group: each
+// weight a run of row-sets; packed, scales, n and y unused).
 template <int WG, int BPL, int R, int MT, bool SHARED, class SG>
-__global__ __launch_bounds__(512) void gemv_mt_kernel(const SG sg, const void* __restrict__ x, uint32_t m,
-                                                      uint32_t rowsets, uint32_t tpw, uint32_t grid) {
+__global__ __launch_bounds__(512) void gemv_mt_kernel(const uint8_t* __restrict__ packed,
+                                                      const uint8_t* __restrict__ scales,
+                                                      const void* __restrict__ x, uint32_t m, uint32_t n,
+                                                      uint32_t rowsets, uint32_t tpw, uint32_t grid,
+                                                      float* __restrict__ y, const SG group) {
+    const auto sg = [&]() {
+        if constexpr (std::is_same_v<SG, Segs>) return group;
+        else return OneSeg{packed, scales, y, n};
+    }();
     constexpr int RM = R * MT;
     static_assert(RM == 2 || RM == 4 || RM == 8, "rows x tokens per team");
     constexpr uint32_t T = 64 * WG;
@@ -1065,7 +1078,7 @@ static hipError_t go_mt(const GemvArgs& a, int cus, uint32_t teams, uint32_t tpw
         rowsets = sg.first[sg.count];
         sg.rowsets = rowsets;
     }
-    const OneSeg one{a.packed, a.scales, a.y, a.n};
+
     constexpr uint32_t xbytes = MT * 2048u * WG * BPL * 2;
     if (teams == 0 || tpw == 0)
         mt_default(rowsets, WG, cus, xbytes + (8 / WG) * 2 * WG * R * MT * 4 <= 65536, teams, tpw);
@@ -1077,17 +1090,17 @@ static hipError_t go_mt(const GemvArgs& a, int cus, uint32_t teams, uint32_t tpw
     if (a.group) {
         if (tpw > 1)
             hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, true, Segs>), dim3(grid), dim3(64 * WG * tpw), lds,
-                               a.stream, sg, a.x, a.m, rowsets, tpw, grid);
+                               a.stream, nullptr, nullptr, a.x, a.m, 0u, rowsets, tpw, grid, nullptr, sg);
         else
             hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, false, Segs>), dim3(grid), dim3(64 * WG * tpw), lds,
-                               a.stream, sg, a.x, a.m, rowsets, tpw, grid);
+                               a.stream, nullptr, nullptr, a.x, a.m, 0u, rowsets, tpw, grid, nullptr, sg);
     } else {
         if (tpw > 1)
-            hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, true, OneSeg>), dim3(grid), dim3(64 * WG * tpw), lds,
-                               a.stream, one, a.x, a.m, rowsets, tpw, grid);
+            hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, true, NoSegs>), dim3(grid), dim3(64 * WG * tpw), lds,
+                               a.stream, a.packed, a.scales, a.x, a.m, a.n, rowsets, tpw, grid, a.y, NoSegs{});
         else
-            hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, false, OneSeg>), dim3(grid), dim3(64 * WG * tpw), lds,
-                               a.stream, one, a.x, a.m, rowsets, tpw, grid);
+            hipLaunchKernelGGL((gemv_mt_kernel<WG, BPL, R, MT, false, NoSegs>), dim3(grid), dim3(64 * WG * tpw), lds,
+                               a.stream, a.packed, a.scales, a.x, a.m, a.n, rowsets, tpw, grid, a.y, NoSegs{});
     }
     return hipGetLastError();
 }

@@ -111,11 +111,14 @@ __device__ __forceinline__ void split3(const f32x4 a, const f32x4 b, bf16x8& hi,
 // ahead of the MFMAs, or, with one unit per tile, two tiles ahead. After a
 // tile's last unit the TW partial 16x16 tiles are summed through LDS
 // (double-buffered: one barrier per tile).
-// The weights of a launch. One weight (OneTiles: small enough for its fields
-// to arrive preloaded in SGPRs), or up to four of one width sharing x
-// (TileSegs: weight s owns the 16-row tiles [first[s], first[s + 1]) of the
-// launch; q|k|v or gate|up of a few-token verify step in one launch). A
-// tile's weight is picked with uniform selects, as in the GEMV.
+// The weights of a launch. One weight (OneTiles, built in the kernel from its
+// leading scalar arguments, which arrive preloaded in SGPRs: a by-value
+// struct argument would end the preloaded run), or up to four of one width
+// sharing x (TileSegs, the trailing argument: weight s owns the 16-row tiles
+// [first[s], first[s + 1]) of the launch; q|k|v or gate|up of a few-token
+// verify step in one launch; NoTiles stands there for one weight). A tile's
+// weight is picked with uniform selects, as in the GEMV.
+struct NoTiles {};
 struct TileSeg {
     const uint8_t* packed;
     const uint8_t* scales;
@@ -153,10 +156,17 @@ __device__ __forceinline__ TileSeg pick_tiles(const TileSegs& sg, uint32_t tile)
     return s;
 }
 
-template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS, int XLM = 0, int NP = 1, class SG = OneTiles>
-__global__ __launch_bounds__(64 * TW) void skinny_kernel(const SG sg, const void* __restrict__ x, uint32_t m,
-                                                         uint32_t tiles, float* __restrict__ part,
-                                                         uint32_t* __restrict__ count) {
+template <bool XBF16, int MT, int U, int NU, int TW, bool RESX, int KS, int XLM = 0, int NP = 1, class SG = NoTiles>
+__global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restrict__ packed,
+                                                         const uint8_t* __restrict__ scales,
+                                                         const void* __restrict__ x, float* __restrict__ y,
+                                                         uint32_t m, uint32_t n, uint32_t tiles,
+                                                         float* __restrict__ part, uint32_t* __restrict__ count,
+                                                         const SG group) {
+    const auto sg = [&]() {
+        if constexpr (std::is_same_v<SG, TileSegs>) return group;
+        else return OneTiles{packed, scales, y, n};
+    }();
     constexpr uint32_t ks = 128 * U * NU * TW;  // K of one slice
     constexpr uint32_t k = ks * KS;
     constexpr uint32_t row_bytes = k / 2, nblk = k / 32;
@@ -611,11 +621,12 @@ hipError_t go(const GemvArgs& a, int cus, const SkinnyScratch& sc = {}) {
             t += (sg.n[s] + 15) / 16;
         }
         hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX, KS, XLM, NP, TileSegs>), dim3(grid * KS),
-                           dim3(64 * TW), 0, a.stream, sg, a.x, a.m, tiles, sc.part, sc.count);
+                           dim3(64 * TW), 0, a.stream, nullptr, nullptr, a.x, nullptr, a.m, 0u, tiles, sc.part,
+                           sc.count, sg);
     } else {
-        hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX, KS, XLM, NP, OneTiles>), dim3(grid * KS),
-                           dim3(64 * TW), 0, a.stream, OneTiles{a.packed, a.scales, a.y, a.n}, a.x, a.m, tiles,
-                           sc.part, sc.count);
+        hipLaunchKernelGGL((skinny_kernel<XBF16, MT, U, NU, TW, RESX, KS, XLM, NP, NoTiles>), dim3(grid * KS),
+                           dim3(64 * TW), 0, a.stream, a.packed, a.scales, a.x, a.y, a.m, a.n, tiles, sc.part,
+                           sc.count, NoTiles{});
     }
     return hipGetLastError();
 }
