@@ -116,7 +116,7 @@ struct Segs {
 
 template <bool A_FP8, int TM, int TN, int U, int Q, int KSPLIT, int RS, int NKC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_kernel(
-    const Segs segs, const uint8_t* __restrict__ xf, const uint8_t* __restrict__ xsf, uint32_t m, uint32_t k) {
+    const uint8_t* __restrict__ xf, const uint8_t* __restrict__ xsf, uint32_t m, uint32_t k, const Segs segs) {
     static_assert((Q * U) % 4 == 0, "slots must cover whole scale quads");
     constexpr int ROT = ((Q * U) / 4) % RS == 0 ? 1 : RS;
     static_assert(((ROT * Q * U) / 4) % RS == 0, "a loop body must cover whole rounds of the scale ring");
@@ -379,9 +379,9 @@ __device__ __forceinline__ void wait_ahead(uint32_t ahead) {
 }
 
 template <bool A_FP8, int WM, int WN, int TM, int TN, int U, int D, int KH, bool PP>
-__global__ __launch_bounds__(64 * WM * WN * KH) void prefill_lds_kernel(const Segs segs, const uint8_t* __restrict__ xf,
+__global__ __launch_bounds__(64 * WM * WN * KH) void prefill_lds_kernel(const uint8_t* __restrict__ xf,
                                                                        const uint8_t* __restrict__ xsf, uint32_t m,
-                                                                       uint32_t k) {
+                                                                       uint32_t k, const Segs segs) {
     using G = LdsGeo<A_FP8, WM, WN, TM, TN, U, D, KH>;
     static_assert(G::ok, "instance outside the kernel's stage, vmcnt and LDS limits");
     static_assert(!PP || KH == 2, "ping-pong alternates the two K halves");
@@ -701,8 +701,8 @@ hipError_t go(const PrefillArgs& a) {
         }
     }
     dim3 grid(cols, (a.m + BM - 1) / BM);
-    hipLaunchKernelGGL((prefill_kernel<A_FP8, TM, TN, U, Q, KSPLIT, RS, NKC>), grid, dim3(256), 0, a.stream, sg,
-                       a.xf, a.xsf, a.m, a.k);
+    hipLaunchKernelGGL((prefill_kernel<A_FP8, TM, TN, U, Q, KSPLIT, RS, NKC>), grid, dim3(256), 0, a.stream, a.xf,
+                       a.xsf, a.m, a.k, sg);
     return hipGetLastError();
 }
 
@@ -737,7 +737,7 @@ hipError_t go_lds(const PrefillArgs& a) {
         }
         dim3 grid(cols, (a.m + G::BM - 1) / G::BM);
         hipLaunchKernelGGL((prefill_lds_kernel<A_FP8, WM, WN, TM, TN, U, D, KH, PP>), grid, dim3(G::NT), 0, a.stream,
-                           sg, a.xf, a.xsf, a.m, a.k);
+                           a.xf, a.xsf, a.m, a.k, sg);
         return hipGetLastError();
     }
 }
