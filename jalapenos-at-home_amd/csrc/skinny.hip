@@ -194,14 +194,20 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
     constexpr uint32_t XS = KP * 2 + 16;
     constexpr int UPP = NU / NP;     // units per pass
     __shared__ __attribute__((aligned(16))) uint8_t xl[XLM > 0 ? XLM * XS : 16];
+    // The slice goes in by direct-to-LDS loads, one 1 KiB piece of a token
+    // row per wave instruction, all in flight at once; the wave then waits
+    // for its own (the caller's barrier follows). Through registers, each
+    // thread's load had to land before its LDS write, one memory latency per
+    // 16 bytes.
+    static_assert(XLM == 0 || (KP * 2) % 1024 == 0, "a pass's row slice is whole 1 KiB pieces");
     auto fill = [&](uint32_t pass) {
-        constexpr uint32_t per_row = KP * 2 / 16;
-        const uint32_t chunks = (m < (uint32_t)XLM ? m : (uint32_t)XLM) * per_row;
-        for (uint32_t c = threadIdx.x; c < chunks; c += 64 * TW) {
-            const uint32_t r = c / per_row, o = c % per_row;
-            *reinterpret_cast<u32x4*>(xl + r * XS + 16 * o) =
-                __builtin_amdgcn_raw_buffer_load_b128(xr, r * k * 2 + pass * KP * 2 + 16 * o, 0, 0);
+        constexpr uint32_t ppr = KP * 2 / 1024;  // pieces per row
+        const uint32_t pieces = (m < (uint32_t)XLM ? m : (uint32_t)XLM) * ppr;
+        for (uint32_t pc = wave; pc < pieces; pc += TW) {
+            const uint32_t r = pc / ppr, o = pc % ppr;
+            load_lds16(xr, (lds_ptr)(xl + r * XS + 1024 * o), r * k * 2 + pass * KP * 2 + 1024 * o + 16 * lane);
         }
+        wait_vm<0>();
     };
     if constexpr (XLM > 0) {
         static_assert(XBF16 && MT == 1 && !RESX, "LDS-resident activations: bf16, one token tile");
