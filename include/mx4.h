@@ -202,8 +202,9 @@ mx4_status mx4_matmul_path(mx4_context *ctx, const void *x_dev, mx4_dtype x_type
  * is one GEMV over the concatenated rows; for 2 <= m <= 32 (a speculative
  * verify step) one launch of the few-token GEMV or the skinny kernel over all
  * the weights' rows, chosen as mx4_matmul would choose for one weight of the
- * group's total rows; otherwise (and for bf16 weights or scale bytes outside
- * 2..252) the projections run one after another. Same arithmetic as
+ * group's total rows; for m > 32 one launch of the exact GEMM over all the
+ * weights' column tiles (K unsplit); otherwise (bf16 weights, scale bytes
+ * outside 2..252) the projections run one after another. Same arithmetic as
  * mx4_matmul: exact products, f32 sums, so each output equals mx4_matmul's
  * for its weight within f32 rounding (the same bits when both choose the same
  * kernel instance). */

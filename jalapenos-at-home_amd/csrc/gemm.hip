@@ -28,6 +28,7 @@
 //  * every global load goes through a buffer resource: token rows >= M and
 //    weight rows >= N read as zeros without touching memory, and their outputs
 //    are not stored.
+#include <type_traits>
 #include "mx4_device.h"
 #include "mx4_kernels.h"
 
@@ -96,13 +97,29 @@ struct Geometry {
     static_assert(D * STAGE <= 160 * 1024, "the stages must fit the LDS");
 };
 
-template <bool XBF16, int WM, int WN, int TM, int TN, int D>
+// Up to four weights of one width sharing x (q|k|v, gate|up at more than 32
+// token rows) in one launch: weight s owns the column tiles [tile0[s],
+// tile0[s + 1]) of the grid; a workgroup picks its weight with uniform
+// selects. Passed as the trailing argument, so the leading scalars keep
+// arriving preloaded; NoGemmSegs stands there for one weight. No K split.
+struct NoGemmSegs {};
+struct GemmSegs {
+    const uint8_t* packed[4];
+    const uint8_t* scales[4];
+    float* y[4];
+    uint32_t n[4];
+    uint32_t tile0[4];
+    uint32_t count;
+};
+
+template <bool XBF16, int WM, int WN, int TM, int TN, int D, class SG = NoGemmSegs>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_exact_kernel(const uint8_t* __restrict__ packed,
                                                                   const uint8_t* __restrict__ scales,
                                                                   const void* __restrict__ x, float* __restrict__ y,
                                                                   uint32_t m, uint32_t n, uint32_t k,
                                                                   uint32_t tiles_n, uint32_t tiles,
-                                                                  uint32_t kslice, float* __restrict__ part) {
+                                                                  uint32_t kslice, float* __restrict__ part,
+                                                                  const SG group) {
     using G = Geometry<XBF16, WM, WN, TM, TN, D>;
     __shared__ __attribute__((aligned(16))) uint8_t lds[D * G::STAGE];
     const uint32_t lane = threadIdx.x % 64, h = lane / 32, r32 = lane % 32;
@@ -111,7 +128,26 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_exact_kernel(const uint8_t*
     // K split: workgroup b takes tile b % tiles over K slice b / tiles and
     // writes its partial tile to part[slice][m][n] (summed afterwards in slice order)
     const uint32_t slice = blockIdx.x / tiles, tile = blockIdx.x % tiles;
-    const uint32_t tn = tile % tiles_n, tm = tile / tiles_n;
+    uint32_t tn = tile % tiles_n;
+    const uint32_t tm = tile / tiles_n;
+    if constexpr (std::is_same_v<SG, GemmSegs>) {
+        // the column tile's weight, and the tile within it
+        uint32_t t0 = 0;
+        packed = group.packed[0];
+        scales = group.scales[0];
+        y = group.y[0];
+        n = group.n[0];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) {
+            const bool in = q < (int)group.count && tn >= group.tile0[q];
+            packed = in ? group.packed[q] : packed;
+            scales = in ? group.scales[q] : scales;
+            y = in ? group.y[q] : y;
+            n = in ? group.n[q] : n;
+            t0 = in ? group.tile0[q] : t0;
+        }
+        tn -= t0;
+    }
     const uint32_t row0 = tm * G::BM, col0 = tn * G::BN;
     const uint32_t k0 = slice * kslice, stages = kslice / kBK;
     if (part) y = part + (size_t)slice * m * n;
@@ -263,11 +299,32 @@ hipError_t go(const GemvArgs& a, uint32_t ks, float* part) {
     constexpr int D = (Geometry<XBF16, WM, WN, TM, TN, 2>::STAGE * 4 <= 160 * 1024 &&
                        2 * Geometry<XBF16, WM, WN, TM, TN, 2>::LPS <= 63) ? 4 : D3;
     using G = Geometry<XBF16, WM, WN, TM, TN, D>;
-    const uint32_t tiles_n = (a.n + G::BN - 1) / G::BN, tiles_m = (a.m + G::BM - 1) / G::BM;
+    const uint32_t tiles_m = (a.m + G::BM - 1) / G::BM;
+    if (a.group) {
+        // each weight of the group a run of column tiles; no K split
+        if (ks > 1) return hipErrorNotSupported;
+        GemmSegs sg{};
+        uint32_t tiles_n = 0;
+        sg.count = a.group->count;
+        for (uint32_t s = 0; s < sg.count; ++s) {
+            sg.packed[s] = a.group->packed[s];
+            sg.scales[s] = a.group->scales[s];
+            sg.y[s] = a.group->y[s];
+            sg.n[s] = a.group->n[s];
+            sg.tile0[s] = tiles_n;
+            tiles_n += (sg.n[s] + G::BN - 1) / G::BN;
+        }
+        const uint32_t tiles = tiles_n * tiles_m;
+        hipLaunchKernelGGL((gemm_exact_kernel<XBF16, WM, WN, TM, TN, D, GemmSegs>), dim3(tiles), dim3(G::NT), 0,
+                           a.stream, nullptr, nullptr, a.x, nullptr, a.m, 0u, a.k, tiles_n, tiles, a.k, nullptr, sg);
+        return hipGetLastError();
+    }
+    const uint32_t tiles_n = (a.n + G::BN - 1) / G::BN;
     const uint32_t tiles = tiles_n * tiles_m;
     if (ks < 1) ks = 1;
     hipLaunchKernelGGL((gemm_exact_kernel<XBF16, WM, WN, TM, TN, D>), dim3(tiles * ks), dim3(G::NT), 0, a.stream,
-                       a.packed, a.scales, a.x, a.y, a.m, a.n, a.k, tiles_n, tiles, a.k / ks, ks > 1 ? part : nullptr);
+                       a.packed, a.scales, a.x, a.y, a.m, a.n, a.k, tiles_n, tiles, a.k / ks, ks > 1 ? part : nullptr,
+                       NoGemmSegs{});
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || ks == 1) return e;
     const uint32_t count = a.m * a.n, threads = count % 4 == 0 ? count / 4 : count;
@@ -306,7 +363,22 @@ bool gemm_exact_supported(uint32_t m, uint32_t n, uint32_t k, bool x_bf16) {
 }
 
 hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* forced, float* part, uint64_t part_bytes) {
-    if (!gemm_exact_supported(a.m, a.n, a.k, a.x_bf16)) return hipErrorNotSupported;
+    if (a.group) {
+        // a group: every weight supported, no explicit configuration
+        if (forced && forced->wm) return hipErrorNotSupported;
+        if (a.group->count < 1 || a.group->count > 4) return hipErrorNotSupported;
+        for (uint32_t s = 0; s < a.group->count; ++s)
+            if (!gemm_exact_supported(a.m, a.group->n[s], a.k, a.x_bf16)) return hipErrorNotSupported;
+    } else if (!gemm_exact_supported(a.m, a.n, a.k, a.x_bf16)) {
+        return hipErrorNotSupported;
+    }
+    // column tiles of width bn over the weight (or over each weight of a group)
+    auto col_tiles = [&](uint32_t bn) -> uint64_t {
+        if (!a.group) return (a.n + bn - 1) / bn;
+        uint64_t t = 0;
+        for (uint32_t s = 0; s < a.group->count; ++s) t += (a.group->n[s] + bn - 1) / bn;
+        return t;
+    };
     GemmConfig c;
     if (forced && forced->wm) {
         c = *forced;
@@ -336,7 +408,7 @@ hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* force
         double best_t = 0.0;
         for (const Cand& cd : cands) {
             if (!a.x_bf16 && cd.wn == 4 && cd.wm == 2) continue;  // no f32 instance of 128 x 256
-            const uint64_t tiles = (uint64_t)((a.m + cd.bm - 1) / cd.bm) * ((a.n + cd.bn - 1) / cd.bn);
+            const uint64_t tiles = (uint64_t)((a.m + cd.bm - 1) / cd.bm) * col_tiles(cd.bn);
             const double t = (double)((tiles + nc - 1) / nc) * cd.round_us;
             if (!best || t < best_t) {
                 best = &cd;
@@ -348,8 +420,12 @@ hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* force
         // A grid still short of the CUs (few token rows): split K across up to
         // four workgroups per tile, each slice whole stages, when the partials
         // fit the scratch; a second small kernel adds them in slice order.
-        const uint64_t tiles = (uint64_t)((a.m + pick.bm - 1) / pick.bm) * ((a.n + pick.bn - 1) / pick.bn);
+        const uint64_t tiles = (uint64_t)((a.m + pick.bm - 1) / pick.bm) * col_tiles(pick.bn);
         c.ks = 1;
+        // a group runs unsplit even when its tiles leave CUs idle: one round
+        // of them beats its weights' separate launches, split or not (8B
+        // q|k|v at 64 token rows: 96 tiles)
+        if (a.group) return a.x_bf16 ? dispatch<true>(a, c, nullptr) : dispatch<false>(a, c, nullptr);
         for (uint32_t ks = 4; ks >= 2 && tiles < want; --ks) {
             if (a.k % (ks * kBK) == 0 && part && (uint64_t)ks * a.m * a.n * 4 <= part_bytes) {
                 c.ks = (int)ks;

@@ -840,6 +840,27 @@ mx4_status mx4_matmul_group(mx4_context* ctx, const void* x, mx4_dtype xt, uint3
         if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
         return MX4_OK;
     }
+    // more than 32 token rows (prefill in the reference's arithmetic): one
+    // exact-GEMM launch over all the weights' column tiles, unsplit
+    if (count > 1 && stored && foldable && m > 32) {
+        mx4::GemvGroup gg{};
+        gg.count = count;
+        gg.k = k;
+        gg.x = x;
+        gg.x_bf16 = xt == MX4_BF16;
+        gg.stream = ctx->stream;
+        for (uint32_t i = 0; i < count; ++i) {
+            gg.packed[i] = w[i]->packed;
+            gg.scales[i] = w[i]->scales;
+            gg.y[i] = y[i];
+            gg.n[i] = w[i]->rows;
+        }
+        mx4::GemvArgs a{w[0]->packed, w[0]->scales, x, y[0], m, w[0]->rows, k, xt == MX4_BF16, ctx->stream};
+        a.group = &gg;
+        const hipError_t e = mx4::launch_gemm_exact(a, ctx->cus, nullptr, ctx->split_part, (uint64_t)kSplitPartTiles * 1024);
+        if (e == hipSuccess) return MX4_OK;
+        if (e != hipErrorNotSupported) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
+    }
     for (uint32_t i = 0; i < count; ++i) {
         mx4_status st = run_matmul(ctx, x, xt, m, w[i], y[i], MX4_PATH_AUTO);
         if (st != MX4_OK) return st;

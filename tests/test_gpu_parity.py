@@ -919,6 +919,48 @@ def test_group_few_tokens_against_oracle(mx4, ctx, oracle, k, shapes, ms):
         w.release()
 
 
+GROUP_EXACT = [
+    (4096, [4096, 1024, 1024], (40, 128, 512)),  # 8B q|k|v (at 40 rows fewer tiles than CUs)
+    (4096, [12288, 12288], (64,)),               # 8B gate|up
+    (4096, [1000, 300, 77], (200,)),             # ragged column tiles at every weight's end
+]
+
+
+@pytest.mark.parametrize("k,shapes,ms", GROUP_EXACT, ids=[f"k{k}-{'_'.join(map(str, s))}" for k, s, _ in GROUP_EXACT])
+def test_group_exact_gemm_against_oracle(mx4, ctx, oracle, k, shapes, ms):
+    """More than 32 token rows through mx4_matmul_group: one exact-GEMM launch
+    over every weight's column tiles, K unsplit. Each weight's outputs against the
+    oracle (first and last 16 rows and 48 drawn on weights wider than 1024)
+    and against separate mx4_matmul calls, bf16 and f32 activations, outputs
+    NaN-filled first."""
+    rng = np.random.default_rng(k + sum(shapes))
+    ws = [ctx.synth_weight(440 + i, n, k, 0.02) for i, n in enumerate(shapes)]
+    dl = [ctx.download_weight(w) for w in ws]
+    rows = [np.arange(n) if n <= 1024 else np.unique(np.r_[0:16, n - 16:n, rng.choice(n, 48)]) for n in shapes]
+    for m in ms:
+        xb16 = oracle.synth_bf16(450 + m, 1.0, m * k)
+        x = oracle.bf16_to_f32(xb16).reshape(m, k)
+        for xt in (mx4.BF16, mx4.F32):
+            say(f"grouped exact GEMM k={k} shapes={shapes} m={m} xt={xt}")
+            xd = ctx.to_device(xb16 if xt == mx4.BF16 else x)
+            ys = [ctx.buffer(m * n * 4) for n in shapes]
+            for y, n in zip(ys, shapes):
+                y.upload(np.full(m * n, np.nan, np.float32))
+            ctx.matmul_group(xd.ptr, xt, m, ws, [y.ptr for y in ys])
+            grouped = [y.download(np.float32).reshape(m, n) for y, n in zip(ys, shapes)]
+            for i, ((packed, scales), n, g, r) in enumerate(zip(dl, shapes, grouped, rows)):
+                assert np.all(np.isfinite(g)), f"weight {i} m={m}: outputs left unwritten"
+                ref = oracle.matmul(x, packed[r].reshape(-1), scales[r].reshape(-1))
+                assert_close(g[:, r], ref, f"grouped exact weight {i} m={m} xt={xt}")
+                ctx.matmul_ptr(xd.ptr, xt, m, ws[i], ys[i].ptr)
+                assert_close(g, ys[i].download(np.float32).reshape(m, n), f"grouped vs separate {i} m={m} xt={xt}")
+            for y in ys:
+                y.free()
+            xd.free()
+    for w in ws:
+        w.release()
+
+
 def test_group_few_tokens_replayed(mx4, ctx, oracle):
     """Grouped verify launches recorded in a pass and replayed three times, the
     program's own synchronizations between replays: every replay gives the
