@@ -585,6 +585,30 @@ def time_prefill_exact(ctx, ms=(33, 128, 512), ceiling: float | None = None) -> 
                 row[f"M{m}"]["frac_of_measured_ceiling"] = round(tf / ceiling, 4)
         out[name] = row
         arena.release()
+    # the grouped launches of an exact prefill (mx4_matmul_group: one exact
+    # GEMM over q|k|v's or gate|up's column tiles), with the members' separate
+    # calls in the same pass form for comparison
+    for gi, (label, members) in enumerate((("qkv_group", ["q", "k", "v"]), ("gate_up_group", ["gate", "up"]))):
+        shapes = [dims[nm] for nm in members]
+        k = shapes[0][1]
+        arena, copies = rotation(ctx, shapes, 63000 + 1000 * gi)
+        row = {"n": sum(n for n, _ in shapes), "k": k, "copies": len(copies)}
+        for m in ms:
+            xb = ctx.buffer(m * k * 2)
+            ctx.synth_bf16(4, 1.0, m * k, xb)
+            ys = [ctx.buffer(m * n * 4) for n, _ in shapes]
+            t = time_pass(ctx, lambda: [ctx.matmul_group(xb.ptr, mx4hip.BF16, m, ws, [y.ptr for y in ys])
+                                        for ws in copies], len(copies))
+            sep = time_pass(ctx, lambda: [ctx.matmul_ptr(xb.ptr, mx4hip.BF16, m, w, y.ptr)
+                                          for ws in copies for w, y in zip(ws, ys)], len(copies))
+            tf = 2.0 * m * row["n"] * k / (t["us"] * 1e-6) / 1e12
+            row[f"M{m}"] = {"us": t["us"], "separate_us": sep["us"], "TFLOPs": round(tf, 1),
+                            "frac_bf16": round(tf / PEAK_TFLOPS["bf16"], 4)}
+            for y in ys:
+                y.free()
+            xb.free()
+        out[label] = row
+        arena.release()
     return out
 
 
