@@ -103,7 +103,7 @@ void qwen_hip_set_cache_limit(void *context, uint64_t bytes);
 
 /* gpu_create (engine/src/gpu.m:27-49): binds HIP device `device` and creates
  * the context's stream (default priority) and its device scratch (argmax
- * partials, and 4 MiB of split-K partial tiles with their arrival counts).
+ * partials, and 32 MiB of split-K partial tiles with their arrival counts).
  * The scratch is shared by every call on the context, so calls on one context
  * must stay ordered: after mx4_set_stream, work still queued on the previous
  * stream must finish before the new stream runs more. */
@@ -235,9 +235,10 @@ mx4_status mx4_gemv_tokens_config(mx4_context *ctx, const void *x_dev, uint32_t 
  * 2x2, 2x1, 1x2 or 1x1; 2x4 waves of 2x2 (bf16 x only) or 1x2; 4x1 waves of
  * 1x2), and K slices across workgroups (0 or 1: none; a split needs K a
  * multiple of 128 * k_slices and k_slices * m * rows * 4 bytes within the
- * context's 4 MiB split scratch); MX4_ERR_UNSUPPORTED otherwise. Zero waves
+ * context's 32 MiB split scratch); MX4_ERR_UNSUPPORTED otherwise. Zero waves
  * keep the default, which splits K on its own when the tiles alone would
- * leave CUs idle. */
+ * leave CUs idle, and for f32 activations or K >= 8192 when a larger tile
+ * with K split fills one round of workgroups. */
 mx4_status mx4_gemm_config(mx4_context *ctx, const void *x_dev, mx4_dtype x_type, uint32_t m, const mx4_weight *w,
                            float *y_dev, int waves_m, int waves_n, int tiles_m, int tiles_n, int k_slices);
 

@@ -362,6 +362,10 @@ bool gemm_exact_supported(uint32_t m, uint32_t n, uint32_t k, bool x_bf16) {
            (uint64_t)(n + 256) * (k / 2) < (1ull << 31);
 }
 
+// The few-token-row K split (a grid short of the CUs) takes at most 4 MiB of
+// partials, the range its picks were measured in.
+constexpr uint64_t kFewRowsSplitBytes = 4ull << 20;
+
 hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* forced, float* part, uint64_t part_bytes) {
     if (a.group) {
         // a group: every weight supported, no explicit configuration
@@ -415,6 +419,42 @@ hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* force
                 best_t = t;
             }
         }
+        // f32 activations, and bf16 ones on wide K (K >= 8192): the largest
+        // tile whose workgroups, with K cut into 1-4 slices of whole stages,
+        // make one round of at least three quarters of the CUs (the most
+        // workgroups among equal tiles). Measured on the 8B q / gate / down
+        // weights at 64..1024 rows (cold): f32 q at 256 / 512 rows 63.9 /
+        // 113.0 -> 44.2 / 75.8 us, gate at 128 / 256 113.3 / 131.7 -> 53.2 /
+        // 90.9, down at 256 / 512 184 / 329 -> 107 / 201; bf16 down at 384 /
+        // 512 / 1024 60.7 / 66.0 / 101.7 -> 47.5 / 54.1 / 93.3. bf16 at K =
+        // 4096 keeps the round-time pick (its splits measured slower there).
+        if (!a.x_bf16 || a.k >= 8192) {
+            const Cand* sel = nullptr;
+            uint32_t sel_ks = 0;
+            uint64_t sel_area = 0, sel_wgs = 0;
+            for (const Cand& cd : cands) {
+                if (!a.x_bf16 && cd.wn == 4 && cd.wm == 2) continue;
+                const uint64_t tiles = (uint64_t)((a.m + cd.bm - 1) / cd.bm) * col_tiles(cd.bn);
+                for (uint32_t ks = 1; ks <= 4; ++ks) {
+                    if (a.k % (ks * kBK) != 0) continue;
+                    if (ks > 1 && (a.group || !part || (uint64_t)ks * a.m * a.n * 4 > part_bytes)) continue;
+                    const uint64_t wgs = tiles * ks, area = (uint64_t)cd.bm * cd.bn;
+                    if (wgs > nc || wgs < want) continue;
+                    if (!sel || area > sel_area || (area == sel_area && wgs > sel_wgs)) {
+                        sel = &cd;
+                        sel_ks = ks;
+                        sel_area = area;
+                        sel_wgs = wgs;
+                    }
+                }
+            }
+            if (sel) {
+                c.wm = sel->wm; c.wn = sel->wn; c.tm = sel->tm; c.tn = sel->tn;
+                c.ks = (int)sel_ks;
+                if (a.group) return a.x_bf16 ? dispatch<true>(a, c, nullptr) : dispatch<false>(a, c, nullptr);
+                return a.x_bf16 ? dispatch<true>(a, c, part) : dispatch<false>(a, c, part);
+            }
+        }
         const Cand pick = *best;
         c.wm = pick.wm; c.wn = pick.wn; c.tm = pick.tm; c.tn = pick.tn;
         // A grid still short of the CUs (few token rows): split K across up to
@@ -427,7 +467,7 @@ hipError_t launch_gemm_exact(const GemvArgs& a, int cus, const GemmConfig* force
         // q|k|v at 64 token rows: 96 tiles)
         if (a.group) return a.x_bf16 ? dispatch<true>(a, c, nullptr) : dispatch<false>(a, c, nullptr);
         for (uint32_t ks = 4; ks >= 2 && tiles < want; --ks) {
-            if (a.k % (ks * kBK) == 0 && part && (uint64_t)ks * a.m * a.n * 4 <= part_bytes) {
+            if (a.k % (ks * kBK) == 0 && part && (uint64_t)ks * a.m * a.n * 4 <= kFewRowsSplitBytes) {
                 c.ks = (int)ks;
                 break;
             }

@@ -151,7 +151,10 @@ constexpr uint64_t kNoAllocHead = 256;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 constexpr uint32_t kArgmaxPartials = 8192;
-// 4 MiB of partial tiles: four K slices of up to 8192 rows at 32 tokens
+// Split-K partials: 32 MiB (the exact GEMM: four K slices of a 512 x 4096
+// f32 output); the skinny kernel's split takes at most 4096 tiles of 1 KiB
+// of it (four K slices of up to 8192 rows at 32 tokens).
+constexpr uint64_t kSplitPartBytes = 32ull << 20;
 constexpr uint32_t kSplitPartTiles = 4096;
 constexpr uint32_t kSplitCounts = 4096;
 
@@ -379,7 +382,7 @@ mx4_status run_matmul(mx4_context* ctx, const void* x, mx4_dtype xt, uint32_t m,
                 return fail(MX4_ERR_UNSUPPORTED, "GEMM path needs K %% 128 == 0 and operands under 2 GiB");
             if (!scales_foldable(w))
                 return fail(MX4_ERR_UNSUPPORTED, "GEMM path folds scales into bf16; scale bytes outside 2..252 need GENERIC");
-            e = mx4::launch_gemm_exact(a, ctx->cus, nullptr, ctx->split_part, (uint64_t)kSplitPartTiles * 1024);
+            e = mx4::launch_gemm_exact(a, ctx->cus, nullptr, ctx->split_part, kSplitPartBytes);
             break;
         case MX4_PATH_GENERIC:
             e = mx4::launch_gemv_generic(a);
@@ -470,7 +473,7 @@ mx4_status mx4_create(int device, mx4_context** out) {
         hipEventCreate(&ctx->ev0) != hipSuccess || hipEventCreate(&ctx->ev1) != hipSuccess ||
         hipMalloc((void**)&ctx->flags, 256) != hipSuccess ||
         hipMalloc((void**)&ctx->am_partial, kArgmaxPartials * sizeof(uint64_t)) != hipSuccess ||
-        hipMalloc((void**)&ctx->split_part, (size_t)kSplitPartTiles * 1024) != hipSuccess ||
+        hipMalloc((void**)&ctx->split_part, (size_t)kSplitPartBytes) != hipSuccess ||
         hipMalloc((void**)&ctx->split_count, kSplitCounts * sizeof(uint32_t)) != hipSuccess ||
         hipMemsetAsync(ctx->split_count, 0, kSplitCounts * sizeof(uint32_t), ctx->own) != hipSuccess ||
         hipStreamSynchronize(ctx->own) != hipSuccess) {
@@ -857,7 +860,7 @@ mx4_status mx4_matmul_group(mx4_context* ctx, const void* x, mx4_dtype xt, uint3
         }
         mx4::GemvArgs a{w[0]->packed, w[0]->scales, x, y[0], m, w[0]->rows, k, xt == MX4_BF16, ctx->stream};
         a.group = &gg;
-        const hipError_t e = mx4::launch_gemm_exact(a, ctx->cus, nullptr, ctx->split_part, (uint64_t)kSplitPartTiles * 1024);
+        const hipError_t e = mx4::launch_gemm_exact(a, ctx->cus, nullptr, ctx->split_part, kSplitPartBytes);
         if (e == hipSuccess) return MX4_OK;
         if (e != hipErrorNotSupported) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
     }
@@ -926,7 +929,7 @@ mx4_status mx4_gemm_config(mx4_context* ctx, const void* x, mx4_dtype xt, uint32
     c.tm = tiles_m;
     c.tn = tiles_n;
     c.ks = k_slices;
-    hipError_t e = mx4::launch_gemm_exact(a, ctx->cus, &c, ctx->split_part, (uint64_t)kSplitPartTiles * 1024);
+    hipError_t e = mx4::launch_gemm_exact(a, ctx->cus, &c, ctx->split_part, kSplitPartBytes);
     if (e == hipErrorNotSupported) return fail(MX4_ERR_UNSUPPORTED, "GEMM instance not compiled");
     if (e != hipSuccess) return fail(MX4_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString(e));
     return MX4_OK;
