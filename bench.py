@@ -583,6 +583,20 @@ def time_prefill_exact(ctx, ms=(33, 128, 512), ceiling: float | None = None) -> 
             row[f"M{m}"] = {"us": t["us"], "TFLOPs": round(tf, 1), "frac_bf16": round(tf / PEAK_TFLOPS["bf16"], 4)}
             if ceiling:
                 row[f"M{m}"]["frac_of_measured_ceiling"] = round(tf / ceiling, 4)
+            yb.free()
+            xb.free()
+        # f32 activations, as a drop-in call passes them (each split into three
+        # bf16 terms: three MFMAs per k-step)
+        for m in (128, 512):
+            xb = ctx.buffer(m * k * 4)
+            xb.upload(np.random.default_rng(m).standard_normal(m * k).astype(np.float32))
+            yb = ctx.buffer(m * n * 4)
+            t = time_pass(ctx, lambda: [ctx.matmul_ptr(xb.ptr, mx4hip.F32, m, ws[0], yb.ptr) for ws in copies],
+                          len(copies))
+            tf = 2.0 * m * n * k / (t["us"] * 1e-6) / 1e12
+            row[f"M{m}_f32"] = {"us": t["us"], "TFLOPs": round(tf, 1)}
+            yb.free()
+            xb.free()
         out[name] = row
         arena.release()
     # the grouped launches of an exact prefill (mx4_matmul_group: one exact
