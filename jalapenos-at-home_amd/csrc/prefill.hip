@@ -754,7 +754,7 @@ hipError_t go_parts(const PrefillArgs& a) {
 }
 
 template <bool A_FP8>
-hipError_t dispatch(const PrefillArgs& a) {
+hipError_t dispatch(const PrefillArgs& a, int cus) {
     if (a.tile_m != 0 && a.split_k >= 16) {
         // workgroup-shared operands (prefill_lds_kernel): split_k = 256 P +
         // 128 (KH - 1) + 16 U + D (K in KH parts of their own waves, stages of
@@ -849,6 +849,49 @@ hipError_t dispatch(const PrefillArgs& a) {
     }
     uint32_t ntot = 0;
     for (uint32_t s = 0; s < a.count; ++s) ntot += a.n[s];
+    // Away from M = 512 (where the defaults below were tuned): the ping-pong
+    // tile whose workgroups come closest to one full round of the CUs without
+    // passing it, the larger tile on a tie (MX-FP8: not 128 x 64, whose
+    // stages of 4 do not fit; 128 x 128 in stages of 2). Measured on the 8B
+    // q / gate / down weights, cold: MXFP4 q at 128 / 256 / 1024 rows 10.3 /
+    // 10.2 / 18.0 -> 8.7 / 8.8 / 13.9 us, gate at 128 / 256 17.6 / 17.4 ->
+    // 11.3 / 13.8, down at 128 / 256 / 1024 25.1 / 24.7 / 47.0 -> 21.5 / 21.9
+    // / 32.4; MX-FP8 q 11.6 / 11.6 / 22.0 -> 9.7 / 9.7 / 19.0, gate at 128 /
+    // 256 21.8 / 21.7 -> 13.8 / 19.1, down 30.3 / 29.9 / 56.3 -> 24.3 / 24.9
+    // / 46.7. Where no tile fits one round (gate at 1024), the defaults below.
+    if ((a.m < 384 || a.m > 768) && a.k % 512 == 0) {
+        struct T { uint32_t bm, bn; };
+        const T ts[] = {{128, 128}, {64, 128}, {128, 64}, {64, 64}};
+        const uint32_t nc = cus > 0 ? (uint32_t)cus : 256u;
+        int sel = -1;
+        uint32_t sel_wgs = 0;
+        for (int i = 0; i < 4; ++i) {
+            if (A_FP8 && i == 2) continue;
+            uint32_t cols = 0;
+            for (uint32_t s = 0; s < a.count; ++s) cols += (a.n[s] + ts[i].bn - 1) / ts[i].bn;
+            const uint32_t wgs = cols * ((a.m + ts[i].bm - 1) / ts[i].bm);
+            if (wgs <= nc && wgs > sel_wgs) {
+                sel = i;
+                sel_wgs = wgs;
+            }
+        }
+        if constexpr (A_FP8) {
+            switch (sel) {
+                case 0: return go_lds<true, 2, 2, 2, 2, 2, fit_depth<true, 2, 2, 2, 2, 2, 3, 2>(), 2, true>(a);
+                case 1: return go_lds<true, 2, 2, 1, 2, 4, 2, 2, true>(a);
+                case 3: return go_lds<true, 2, 2, 1, 1, 4, 2, 2, true>(a);
+                default: break;
+            }
+        } else {
+            switch (sel) {
+                case 0: return go_lds<false, 2, 2, 2, 2, 4, 2, 2, true>(a);
+                case 1: return go_lds<false, 2, 2, 1, 2, 4, 2, 2, true>(a);
+                case 2: return go_lds<false, 2, 2, 2, 1, 4, 2, 2, true>(a);
+                case 3: return go_lds<false, 2, 2, 1, 1, 4, 2, 2, true>(a);
+                default: break;
+            }
+        }
+    }
     // Qwen3-8B shapes (K = 4096, and 12288 for down), measured on MI355X at
     // M = 512 on cold weights, the alternatives timed in one process (split_k
     // code 256 P + 128 (KH - 1) + 16 U + D of the tuning call):
@@ -934,11 +977,11 @@ hipError_t launch_to_fragments(const uint8_t* codes, const uint8_t* scales, uint
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(const PrefillArgs& a, int) {
+hipError_t launch_prefill(const PrefillArgs& a, int cus) {
     if (a.count < 1 || a.count > kMaxPrefillGroup) return hipErrorNotSupported;
     for (uint32_t s = 0; s < a.count; ++s)
         if (!prefill_supported(a.m, a.n[s], a.k)) return hipErrorNotSupported;
-    return a.fp8 ? dispatch<true>(a) : dispatch<false>(a);
+    return a.fp8 ? dispatch<true>(a, cus) : dispatch<false>(a, cus);
 }
 
 }  // namespace mx4
