@@ -1956,17 +1956,18 @@ def test_recorded_pass_survives_workspace_growth(mx4, ctx, oracle):
     w2.release()
 
 
+@pytest.mark.parametrize("m", [128, 256, 512, 1024])
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
 @pytest.mark.parametrize("name", ["q", "o", "gate", "up", "down"])
-def test_prefill_8b_shapes_sampled(mx4, ctx, oracle, name, act):
-    """M = 512 at every Qwen3-8B prefill shape (q/o 4096->4096,
-    gate/up 4096->12288, down 12288->4096), MXFP4 and MX-FP8 activations: 24
-    token rows x sampled weight rows against the oracle on dequant(requant(x)),
-    through the default instance of each shape."""
-    rng = np.random.default_rng(77)
+def test_prefill_8b_shapes_sampled(mx4, ctx, oracle, name, act, m):
+    """Every Qwen3-8B prefill shape (q/o 4096->4096, gate/up 4096->12288,
+    down 12288->4096) at 128 / 256 / 512 / 1024 token rows, MXFP4 and MX-FP8
+    activations: 24 token rows x sampled weight rows against the oracle on
+    dequant(requant(x)), through the default instance of each shape and row
+    count (away from 512 rows, the tile nearest one round of the CUs)."""
+    rng = np.random.default_rng(77 + m)
     n, k = QWEN8[name]
-    m = 512
-    say(f"prefill 8B {name} {act} 512 x {k} -> {n}")
+    say(f"prefill 8B {name} {act} {m} x {k} -> {n}")
     w = ctx.synth_weight(400 + list(QWEN8).index(name), n, k, 0.02)
     packed, scales = ctx.download_weight(w)
     x = oracle.bf16_to_f32(oracle.synth_bf16(401, 1.0, m * k)).reshape(m, k)
