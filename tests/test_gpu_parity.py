@@ -1132,7 +1132,7 @@ def test_skinny_lds_activations(mx4, ctx, oracle, n):
     rng = np.random.default_rng(n)
     w = ctx.synth_weight(1300 + n % 7, n, k, 0.02)
     packed, scales = ctx.download_weight(w)
-    for m in (1, 2, 3, 4, 5, 6, 8, 10, 11, 12, 15, 16):
+    for m in (1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16):
         x = oracle.bf16_to_f32(oracle.synth_bf16(1310 + m, 1.0, m * k)).reshape(m, k)
         ref = oracle.matmul(x, packed.reshape(-1), scales.reshape(-1))
         assert_close(run_matmul(mx4, ctx, x, w, mx4.PATH_SKINNY, mx4.BF16), ref, f"skinny LDS x m={m} n={n}")
