@@ -391,7 +391,14 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
         mfma_drain();
     };
 
-    __shared__ f32x4 red[2][TW][MT][64];
+    // The hand-over of the waves' sums alternates between two buffers, so a
+    // fast wave's next tile cannot overwrite sums a slow one still reads. With
+    // K slices (NP > 1) every tile after the first opens with a workgroup
+    // barrier before its first slice, after every wave's reads of the last
+    // tile's sums: one buffer serves, and the 8 KiB it frees lets 16 tokens
+    // run in thirds of K.
+    constexpr uint32_t RB = NP > 1 ? 1 : 2;
+    __shared__ f32x4 red[RB][TW][MT][64];
     uint32_t parity = 0;
     // Split K: partials are stored and loaded with device scope (SC1), so
     // they are not kept in the per-XCD L2s; the fences below order them.
@@ -425,7 +432,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
                                                            ((slice * MT + j) * 64 + lane) * 16, 0, kDeviceScope);
                 }
             }
-            parity ^= 1;
+            parity = (parity + 1) % RB;
             zero();
             return;
         }
@@ -447,7 +454,7 @@ __global__ __launch_bounds__(64 * TW) void skinny_kernel(const uint8_t* __restri
             const uint32_t row = (tile - sw.first) * 16 + c, tok = 16 * j + 4 * gg + r;
             if (row < sw.n && tok < m) sw.y[(size_t)tok * sw.n + row] = sum;
         }
-        parity ^= 1;
+        parity = (parity + 1) % RB;
         zero();
     };
 
@@ -701,9 +708,11 @@ hipError_t go_k(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
         case 8192: return go<XBF16, MT, U, 8 / U, TW, false>(a, cus);
         case 12288:
             // bf16 activations of one token tile (up to 16 tokens) in LDS
-            // beside the kernel's 32 KiB of stage and reduction buffers: all
-            // of K up to 5 tokens (5 x 24 KiB), one K half at a time up to
-            // 10, one third up to 15, one sixth at 16. 8B down at 3 / 4 / 5
+            // beside the kernel's 32 KiB of stage and reduction buffers (24
+            // KiB with K slices: one reduction buffer): all of K up to 5
+            // tokens (5 x 24 KiB), one K half at a time up to 10, one third up
+            // to 16 (sixths at 16 with two reduction buffers: 11.2 -> 10.1
+            // us in thirds). 8B down at 3 / 4 / 5
             // tokens 10.0 / 10.3 / 10.3 -> 7.7-8.0 / 8.0-8.3 / 8.3-8.7 us, at
             // 6 / 8 / 10 / 11 tokens 11.0 / 12.4 / 13.2 / 13.8 -> 9.4 / 10.2 /
             // 10.9 / 11.6 us against the per-unit activation loads, and at 12
@@ -712,8 +721,7 @@ hipError_t go_k(const GemvArgs& a, int cus, const SkinnyScratch& sc) {
             if constexpr (XBF16 && MT == 1) {
                 if (a.m <= 5) return go<XBF16, 1, U, 12 / U, TW, false, 1, 5>(a, cus);
                 if (a.m <= 10) return go<XBF16, 1, U, 12 / U, TW, false, 1, 10, 2>(a, cus);
-                if (a.m <= 15) return go<XBF16, 1, U, 12 / U, TW, false, 1, 15, 3>(a, cus);
-                return go<XBF16, 1, U, 12 / U, TW, false, 1, 16, 6>(a, cus);
+                return go<XBF16, 1, U, 12 / U, TW, false, 1, 16, 3>(a, cus);
             }
             // bf16 x, two token tiles (17-32 tokens): four workgroups per
             // tile, each over a 3072-wide K slice with its activations resident

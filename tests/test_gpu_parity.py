@@ -1119,8 +1119,8 @@ def test_skinny_resident_activations(mx4, ctx, oracle, n, k):
 def test_skinny_lds_activations(mx4, ctx, oracle, n):
     """K = 12288 with 1..16 bf16 token rows: the skinny kernel keeps the
     activations in LDS (padded rows; all of K up to 5 tokens, K halves up to
-    10, thirds up to 15, sixths at 16, each slice loaded when its first unit
-    comes up) and reads
+    10, thirds up to 16, each slice loaded when its first unit comes up) and
+    reads
     each unit's operand fragments from there. Ragged N against the oracle on
     every row (several 16-row tiles per workgroup on the wider N, so every
     slice is reloaded per tile), and one-hot activations (one column per token,
