@@ -27,8 +27,8 @@
 //    slice's activations resident, and the last of them to finish adds the KS
 //    partial tiles in slice order;
 //  * up to 16 bf16 tokens at K = 12288 (XLM, NP): the activations are loaded
-//    into LDS by the workgroup -- all of K up to 5 tokens, one K half, third
-//    or sixth at a time above -- and each unit's operand fragments read from
+//    into LDS by the workgroup -- all of K up to 5 tokens, one K half or
+//    third at a time above -- and each unit's operand fragments read from
 //    there, instead of every unit loading its 16-token fragments from the L2.
 #include <type_traits>
 
