@@ -466,6 +466,41 @@ def time_prefill(ctx, m: int = 512, ceiling: dict | None = None) -> dict:
     return out
 
 
+def time_prefill_rows(ctx, ms=(128, 1024)) -> dict:
+    """Prefill away from M = 512 (where the default instance is the tile whose
+    workgroups come nearest one round of the CUs): the 8B q, gate and down
+    shapes at `ms` token rows, MXFP4 and MX-FP8 activations requantized
+    beforehand, the GEMM alone through the default instance, over >= 512 MiB
+    of cold weight copies. [us, TFLOP/s] per shape, format and M."""
+    out = {}
+    dims = {name: (n, k) for name, n, k in LAYER}
+    ctx.reserve_prefill(max(ms), 12288)
+    for i, name in enumerate(("q", "gate", "down")):
+        n, k = dims[name]
+        arena, copies = rotation(ctx, [(n, k)], 57000 + 1000 * i)
+        for ws in copies:
+            ws[0].prepare_prefill()
+        row = {}
+        for act, code in (("mxfp4", mx4hip.ACT_MXFP4), ("mxfp8", mx4hip.ACT_MXFP8)):
+            res = {}
+            for m in ms:
+                xb = ctx.buffer(m * k * 2)
+                ctx.synth_bf16(3, 1.0, m * k, xb)
+                yb = ctx.buffer(m * n * 4)
+                xq, xsc = ctx.prefill_act_buffers(m, k, code)
+                ctx.prefill_quantize(xb, mx4hip.BF16, m, k, code, xq, xsc)
+                t = time_pass(ctx, lambda: [ctx.prefill_matmul(xq, xsc, code, m, ws[0], yb) for ws in copies],
+                              len(copies))
+                res[f"M{m}"] = [t["us"], round(2.0 * m * n * k / (t["us"] * 1e-6) / 1e12, 1)]
+                for b_ in (xb, yb, xq, xsc):
+                    b_.free()
+            row[act] = res
+        out[name] = row
+        arena.release()
+    out["cols"] = ["us", "TFLOPs"]
+    return out
+
+
 def prefill_counters() -> dict:
     """MFMA operation and busy counters of the M = 512 prefill dispatches
     from the committed profile summary, when its stamp names the library this
@@ -1455,6 +1490,8 @@ def main() -> int:
                 for act, key in (("mxfp4", "32x32x64"), ("mxfp8", "fp8xfp4_32x32x64"), ("bf16", "bf16_32x32x16"))}
         extra["prefill"] = time_prefill(ctx, ceiling=ceil)
         extra["prefill_layer"] = time_prefill_layer(ctx, weights)
+        log("prefill at 128 and 1024 token rows")
+        extra["prefill_rows"] = time_prefill_rows(ctx)
         prefill_top = prefill_summary(extra["prefill"], extra["prefill_layer"], ceil)
         log("exact matrix-core path for M > 32 (AUTO)")
         extra["prefill_exact_auto"] = time_prefill_exact(ctx, ceiling=ceil["bf16"])
