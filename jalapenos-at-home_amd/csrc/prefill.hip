@@ -859,10 +859,15 @@ hipError_t dispatch(const PrefillArgs& a, int cus) {
     // / 32.4; MX-FP8 q 11.6 / 11.6 / 22.0 -> 9.7 / 9.7 / 19.0, gate at 128 /
     // 256 21.8 / 21.7 -> 13.8 / 19.1, down 30.3 / 29.9 / 56.3 -> 24.3 / 24.9
     // / 46.7. Where no tile fits one round (gate at 1024), the defaults below.
+    const uint32_t nc = cus > 0 ? (uint32_t)cus : 256u;
+    auto rounds = [&](uint32_t bm, uint32_t bn) {
+        uint32_t cols = 0;
+        for (uint32_t s = 0; s < a.count; ++s) cols += (a.n[s] + bn - 1) / bn;
+        return (cols * ((a.m + bm - 1) / bm) + nc - 1) / nc;
+    };
     if ((a.m < 384 || a.m > 768) && a.k % 512 == 0) {
         struct T { uint32_t bm, bn; };
         const T ts[] = {{128, 128}, {64, 128}, {128, 64}, {64, 64}};
-        const uint32_t nc = cus > 0 ? (uint32_t)cus : 256u;
         int sel = -1;
         uint32_t sel_wgs = 0;
         for (int i = 0; i < 4; ++i) {
@@ -890,6 +895,22 @@ hipError_t dispatch(const PrefillArgs& a, int cus) {
                 case 3: return go_lds<false, 2, 2, 1, 1, 4, 2, 2, true>(a);
                 default: break;
             }
+        }
+    }
+    // Beyond 768 rows, where no tile fits one round, the 512-row tiles of q /
+    // o and down (128 x 64 or 64 x 128: 192 operand rows per k-step) against
+    // 128 x 128 in ping-pong (256 rows per k-step for twice the outputs):
+    // whichever needs fewer rounds x rows per k-step. 8B, cold: MXFP4 q at
+    // 1536 / 2048 / 4096 rows 24.8 / 32.4 / 61.2 -> 23.7 / 26.4 / 48.9 us,
+    // down 62.8 / 81.3 / 155.5 -> 53.9 / 60.6 / 117.8; MX-FP8 q 30.8 / 38.9 /
+    // 74.4 -> 31.2 / 35.4 / 67.2, down 78.7 / 102.5 / 195.8 -> 78.7 / 89.2 /
+    // 170.5. (MX-FP8 q|k|v keeps its one-ring tiles: 128 x 128 measured the
+    // same at 1024 and 2048 rows and slower at 1536.)
+    if (a.m > 768 && ntot <= 4096 && (a.k == 4096 || a.k == 12288)) {
+        const uint32_t dbm = (!A_FP8 && a.k == 4096) ? 128u : 64u;
+        if (rounds(128, 128) * 256 < rounds(dbm, 192 - dbm) * 192) {
+            if constexpr (A_FP8) return go_lds<true, 2, 2, 2, 2, 2, fit_depth<true, 2, 2, 2, 2, 2, 3, 2>(), 2, true>(a);
+            else return go_lds<false, 2, 2, 2, 2, 4, 2, 2, true>(a);
         }
     }
     // Qwen3-8B shapes (K = 4096, and 12288 for down), measured on MI355X at
