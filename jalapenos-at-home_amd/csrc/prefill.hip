@@ -950,7 +950,12 @@ hipError_t dispatch(const PrefillArgs& a, int cus) {
             else return go_lds<false, 2, 2, 2, 2, 4, 2, 2, true>(a);
         }
         if constexpr (!A_FP8) {
-            if (ntot >= 16384) return go_lds<false, 2, 2, 2, 3, 2, 3>(a);
+            // one ring, two workgroups per CU (72 KiB each; a ping-pong one
+            // needs a whole CU): gate|up, and gate or up alone once its
+            // 128 x 192 tiles need more than one round of CUs (gate at 768 /
+            // 1024 / 1536 / 2048 / 4096 rows 35.0 / 39.4 / 55.4 / 72.9 / 140.5
+            // -> 28.6 / 33.6 / 49.5 / 63.6 / 121.5 us; the same at 512)
+            if (ntot >= 16384 || rounds(128, 192) > 1) return go_lds<false, 2, 2, 2, 3, 2, 3>(a);
         }
         return go_lds<A_FP8, 2, 2, 2, 3, 2, fit_depth<A_FP8, 2, 2, 2, 3, 2, 3, 2>(), 2, true>(a);
     }
