@@ -899,18 +899,21 @@ hipError_t dispatch(const PrefillArgs& a, int cus) {
     }
     // Beyond 768 rows, where no tile fits one round, the 512-row tiles of q /
     // o and down (128 x 64 or 64 x 128: 192 operand rows per k-step) against
-    // 128 x 128 in ping-pong (256 rows per k-step for twice the outputs):
-    // whichever needs fewer rounds x rows per k-step. 8B, cold: MXFP4 q at
-    // 1536 / 2048 / 4096 rows 24.8 / 32.4 / 61.2 -> 23.7 / 26.4 / 48.9 us,
-    // down 62.8 / 81.3 / 155.5 -> 53.9 / 60.6 / 117.8; MX-FP8 q 30.8 / 38.9 /
-    // 74.4 -> 31.2 / 35.4 / 67.2, down 78.7 / 102.5 / 195.8 -> 78.7 / 89.2 /
-    // 170.5. (MX-FP8 q|k|v keeps its one-ring tiles: 128 x 128 measured the
-    // same at 1024 and 2048 rows and slower at 1536.)
+    // 128 x 128 (256 rows per k-step for twice the outputs): whichever needs
+    // fewer rounds x rows per k-step. MXFP4 runs 128 x 128 over the whole K
+    // in stages of 4, 2 deep, two workgroups per CU; MX-FP8 (twice the A
+    // bytes) K halves in ping-pong. 8B, cold: MXFP4 q at 1536 / 2048 / 4096
+    // rows 24.8 / 32.4 / 61.2 -> 19.7 / 23.8 / 45.0 us (ping-pong 23.8 / 26.4
+    // / 49.3), down 62.8 / 81.3 / 155.5 -> 48.2 / 58.9 / 113.7 (ping-pong
+    // 54.3 / 61.2 / 118.0); MX-FP8 q 30.8 / 38.9 / 74.4 -> 31.2 / 35.4 / 67.2,
+    // down 78.7 / 102.5 / 195.8 -> 78.7 / 89.2 / 170.5 (one ring 15-20%
+    // slower). (MX-FP8 q|k|v keeps its one-ring 64 x 128 tiles: 128 x 128
+    // measured the same at 1024 and 2048 rows and slower at 1536.)
     if (a.m > 768 && ntot <= 4096 && (a.k == 4096 || a.k == 12288)) {
         const uint32_t dbm = (!A_FP8 && a.k == 4096) ? 128u : 64u;
         if (rounds(128, 128) * 256 < rounds(dbm, 192 - dbm) * 192) {
             if constexpr (A_FP8) return go_lds<true, 2, 2, 2, 2, 2, fit_depth<true, 2, 2, 2, 2, 2, 3, 2>(), 2, true>(a);
-            else return go_lds<false, 2, 2, 2, 2, 4, 2, 2, true>(a);
+            else return go_lds<false, 2, 2, 2, 2, 4, 2>(a);
         }
     }
     // Qwen3-8B shapes (K = 4096, and 12288 for down), measured on MI355X at
