@@ -2027,6 +2027,37 @@ def test_weight_layouts_footprint_release_and_drop(mx4, ctx, oracle):
     w2.release()
 
 
+@pytest.mark.parametrize("m", [1024, 2048])
+@pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
+def test_prefill_8b_qkv_group_many_rows(mx4, ctx, oracle, act, m):
+    """q|k|v beyond 768 token rows through mx4_matmul_prefill_group (MXFP4:
+    128 x 128 tiles over the whole K, two workgroups per CU; MX-FP8: its
+    one-ring 64 x 128 tiles) against the oracle on sampled token rows and
+    weight rows of each member, and against each member's single launch."""
+    rng = np.random.default_rng(79 + m)
+    k = 4096
+    ns = [QWEN8["q"][0], QWEN8["k"][0], QWEN8["v"][0]]
+    say(f"prefill 8B q|k|v group {act} {m} rows")
+    ws = [ctx.synth_weight(420 + i, n, k, 0.02) for i, n in enumerate(ns)]
+    x = oracle.bf16_to_f32(oracle.synth_bf16(421 + m, 1.0, m * k)).reshape(m, k)
+    xb = ctx.to_device((f32_bits(x) >> 16).astype(np.uint16))
+    code = mx4.ACT_MXFP4 if act == "mxfp4" else mx4.ACT_MXFP8
+    ys = [ctx.buffer(m * n * 4) for n in ns]
+    ctx.matmul_prefill_group(xb, mx4.BF16, m, ws, code, ys)
+    rows = np.unique(np.concatenate([[0, m - 1], rng.choice(m, 14, replace=False)]))
+    xd = _requant(oracle, x[rows], act)
+    for i, (w, n) in enumerate(zip(ws, ns)):
+        got = ys[i].download(np.float32).reshape(m, n)
+        packed, scales = ctx.download_weight(w)
+        cols = _sample_rows(n, 48, rng)
+        assert_close(got[np.ix_(rows, cols)], _sampled_ref(oracle, xd, packed, scales, cols),
+                     f"q|k|v group {act} m={m} weight {i}")
+        single = _run_prefill(mx4, ctx, x, w, act, mx4.BF16)
+        assert_close(got, single, f"q|k|v group {act} m={m} weight {i} against its single launch")
+    for w in ws:
+        w.release()
+
+
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
 def test_prefill_8b_gate_up_group(mx4, ctx, oracle, act):
     """gate|up at M = 512 through mx4_matmul_prefill_group (engine/src/lib.rs:459-467:
