@@ -849,23 +849,26 @@ hipError_t dispatch(const PrefillArgs& a, int cus) {
     }
     uint32_t ntot = 0;
     for (uint32_t s = 0; s < a.count; ++s) ntot += a.n[s];
-    // Away from M = 512 (where the defaults below were tuned): the ping-pong
-    // tile whose workgroups come closest to one full round of the CUs without
-    // passing it, the larger tile on a tie (MX-FP8: not 128 x 64, whose
-    // stages of 4 do not fit; 128 x 128 in stages of 2). Measured on the 8B
-    // q / gate / down weights, cold: MXFP4 q at 128 / 256 / 1024 rows 10.3 /
-    // 10.2 / 18.0 -> 8.7 / 8.8 / 13.9 us, gate at 128 / 256 17.6 / 17.4 ->
-    // 11.3 / 13.8, down at 128 / 256 / 1024 25.1 / 24.7 / 47.0 -> 21.5 / 21.9
-    // / 32.4; MX-FP8 q 11.6 / 11.6 / 22.0 -> 9.7 / 9.7 / 19.0, gate at 128 /
-    // 256 21.8 / 21.7 -> 13.8 / 19.1, down 30.3 / 29.9 / 56.3 -> 24.3 / 24.9
-    // / 46.7. Where no tile fits one round (gate at 1024), the defaults below.
+    // Outside 384..512 rows (where the defaults below were tuned): the
+    // ping-pong tile whose workgroups come closest to one full round of the
+    // CUs without passing it, the larger tile on a tie (MX-FP8: not 128 x 64,
+    // whose stages of 4 do not fit; 128 x 128 in stages of 2). Measured on
+    // the 8B q / gate / down weights, cold: MXFP4 q at 128 / 256 / 1024 rows
+    // 10.3 / 10.2 / 18.0 -> 8.7 / 8.8 / 13.9 us, gate at 128 / 256 17.6 /
+    // 17.4 -> 11.3 / 13.8, down at 128 / 256 / 1024 25.1 / 24.7 / 47.0 ->
+    // 21.5 / 21.9 / 32.4; MX-FP8 q 11.6 / 11.6 / 22.0 -> 9.7 / 9.7 / 19.0,
+    // gate at 128 / 256 21.8 / 21.7 -> 13.8 / 19.1, down 30.3 / 29.9 / 56.3
+    // -> 24.3 / 24.9 / 46.7; at 576 / 768 rows (128 x 128) MXFP4 q 16.1 /
+    // 16.5 -> 12.1 / 12.6, down 39.6 / 40.1 -> 28.4 / 30.0, MX-FP8 q 18.8 /
+    // 19.6 -> 16.4 / 17.2, down 48.0 / 48.8 -> 42.1 / 44.2. Where no tile
+    // fits one round (gate at 576 and above), the rules and defaults below.
     const uint32_t nc = cus > 0 ? (uint32_t)cus : 256u;
     auto rounds = [&](uint32_t bm, uint32_t bn) {
         uint32_t cols = 0;
         for (uint32_t s = 0; s < a.count; ++s) cols += (a.n[s] + bn - 1) / bn;
         return (cols * ((a.m + bm - 1) / bm) + nc - 1) / nc;
     };
-    if ((a.m < 384 || a.m > 768) && a.k % 512 == 0) {
+    if ((a.m < 384 || a.m > 512) && a.k % 512 == 0) {
         struct T { uint32_t bm, bn; };
         const T ts[] = {{128, 128}, {64, 128}, {128, 64}, {64, 64}};
         int sel = -1;
@@ -949,11 +952,12 @@ hipError_t dispatch(const PrefillArgs& a, int cus) {
     }
     if (a.k == 4096) {
         if (ntot <= 8192) {
-            // MXFP4 q|k|v beyond 768 rows: the same tile over the whole K, two
-            // workgroups per CU (1024 / 1536 / 2048 / 4096 rows 23.6 / 34.2 /
-            // 37.7 / 70.3 -> 20.4 / 33.9 / 37.3 / 64.5 us)
+            // MXFP4 q|k|v once its ping-pong tiles need more than one round:
+            // the same tile over the whole K, two workgroups per CU (1024 /
+            // 1536 / 2048 / 4096 rows 23.6 / 34.2 / 37.7 / 70.3 -> 20.4 / 33.9
+            // / 37.3 / 64.5 us)
             if constexpr (A_FP8) return go_lds<true, 2, 2, 1, 2, 4, 2>(a);
-            else if (a.m > 768) return go_lds<false, 2, 2, 2, 2, 4, 2>(a);
+            else if (rounds(128, 128) > 1) return go_lds<false, 2, 2, 2, 2, 4, 2>(a);
             else return go_lds<false, 2, 2, 2, 2, 4, 2, 2, true>(a);
         }
         if constexpr (!A_FP8) {

@@ -1956,12 +1956,12 @@ def test_recorded_pass_survives_workspace_growth(mx4, ctx, oracle):
     w2.release()
 
 
-@pytest.mark.parametrize("m", [128, 256, 512, 1024, 2048])
+@pytest.mark.parametrize("m", [128, 256, 512, 640, 1024, 2048])
 @pytest.mark.parametrize("act", ["mxfp4", "mxfp8"])
 @pytest.mark.parametrize("name", ["q", "o", "gate", "up", "down"])
 def test_prefill_8b_shapes_sampled(mx4, ctx, oracle, name, act, m):
     """Every Qwen3-8B prefill shape (q/o 4096->4096, gate/up 4096->12288,
-    down 12288->4096) at 128 / 256 / 512 / 1024 / 2048 token rows, MXFP4 and
+    down 12288->4096) at 128 / 256 / 512 / 640 / 1024 / 2048 token rows, MXFP4 and
     MX-FP8 activations: 24 token rows x sampled weight rows against the oracle
     on dequant(requant(x)), through the default instance of each shape and row
     count (away from 512 rows, the tile nearest one round of the CUs; beyond
